@@ -1,0 +1,177 @@
+/*
+ * nanoinfer_kv.h -- C ABI of the MI355X (gfx950) paged f16 KV-cache hot path.
+ *
+ * A drop-in for the KV part of nanoinfer's batched engine: the page allocator
+ * and block tables of `Batch` (crates/metal/src/batch.rs:129-254), the f16
+ * append (crates/metal/src/shaders/batch.metal:329-344), the block-table
+ * gather (batch.metal:24-26) and paged flash-decoding attention with split-K
+ * partitions and a log-sum-exp merge (batch.metal:349-424, dispatched from
+ * batch.rs:577-616).  Paths are relative to the reference repository.
+ *
+ * Conventions
+ *  - Every call returns an int status (NI_OK or an NI_ERR_* code); the text
+ *    of the last failure is ni_kv_last_error().  Where the reference returns
+ *    Err(String) the text is the reference's.
+ *  - The handle owns the device page pools and its staging buffers.  The
+ *    caller owns every q/k/v/out buffer it passes (device memory).
+ *  - One host thread per handle.  Data-path calls enqueue work on the
+ *    caller's HIP stream (`ni_stream`, a hipStream_t; NULL = null stream) and
+ *    return without waiting; ni_kv_sync() waits.
+ *  - Bookkeeping calls (add/free/truncate/reserve/commit) act on host state
+ *    at once.  A data-path call snapshots the block tables it needs when it
+ *    is made, so later bookkeeping never changes work already enqueued.
+ *  - f32 arguments (q/k/v/out) must be 16-byte aligned with row and layer
+ *    strides that are multiples of 4 floats.  Strides count elements.
+ */
+#ifndef NANOINFER_KV_H
+#define NANOINFER_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ni_kv ni_kv;
+typedef void* ni_stream; /* hipStream_t */
+
+/* Positions per page (crates/metal/src/batch.rs:33, KV_BLOCK). */
+#define NI_KV_BLOCK 16
+/* `layer` argument: run every layer in one launch (inputs at
+ * base + l * layer_stride for l in 0..n_layer). */
+#define NI_ALL_LAYERS (-1)
+
+enum ni_status {
+    NI_OK = 0,
+    NI_ERR_NO_SLOT = 1,         /* add_seq: every sequence slot is live (batch.rs:201-202 -> None) */
+    NI_ERR_CONTEXT_FULL = 2,    /* "sequence {s}: context full ({len} > {n_ctx})" (batch.rs:244-246) */
+    NI_ERR_POOL_EXHAUSTED = 3,  /* "KV cache pool exhausted" (batch.rs:248) */
+    NI_ERR_NOT_LIVE = 4,        /* "sequence {s} is not live" (batch.rs:281-283) */
+    NI_ERR_BAD_LEN = 5,         /* truncate past seq_len: the reference's assert (batch.rs:221) */
+    NI_ERR_HIP = 6,             /* a HIP runtime call failed */
+    NI_ERR_BAD_ARG = 7,         /* bad sequence index, shape, alignment or option */
+    NI_ERR_EMPTY_WORK = 8,      /* "empty work item" (batch.rs:284-286) */
+    NI_ERR_TOO_MANY_ROWS = 9,   /* "{n} rows > max_rows {max}" (batch.rs:300-302) */
+    NI_ERR_NOT_RESERVED = 10,   /* a row's position has no page yet (reserve first) */
+    NI_ERR_NO_DEVICE = 11       /* data-path call on a NI_KV_HOST_ONLY handle */
+};
+
+/* ni_kv_opts.flags: keep only the host bookkeeping (no device memory); the
+ * data-path calls then fail with NI_ERR_NO_DEVICE.  For tests without a GPU. */
+#define NI_KV_HOST_ONLY 1u
+
+/* Sizes and policies (the KV fields of BatchOpts, batch.rs:44-76, plus the
+ * model shape the reference takes from Config, crates/core/src/config.rs:23). */
+typedef struct ni_kv_opts {
+    uint32_t n_layer;   /* layers sharing each page id (batch.rs:166,390) */
+    uint32_t n_head;
+    uint32_t head_dim;  /* 64 or 128 on the device path */
+    uint32_t kv_pages;  /* pages in the pool (BatchOpts::kv_blocks) */
+    uint32_t max_seqs;  /* sequence slots (BatchOpts::max_seqs) */
+    uint32_t max_ctx;   /* most positions per sequence (Config::n_ctx) */
+    uint32_t max_rows;  /* most rows per data-path call (BatchOpts::max_rows) */
+    uint32_t flags;     /* NI_KV_HOST_ONLY */
+    /* Optional (NULL = the reference's order 0, 1, 2, ...): a permutation of
+     * 0..kv_pages-1 giving the order in which free pages are handed out. */
+    const uint32_t* page_order;
+} ni_kv_opts;
+
+/* One row: token `pos` of sequence `seq` (batch.rs:112-117; sent to the
+ * reference's kernels as uint4(seq, pos, 0, 0), batch.rs:306). */
+typedef struct ni_row {
+    uint32_t seq;
+    uint32_t pos;
+} ni_row;
+
+/* One work item of ni_kv_step: append n_new rows to `seq` (positions
+ * seq_len .. seq_len+n_new-1) and run attention for the last n_query of them
+ * (batch.rs:259-315; n_query = n_new is the reference's all_logits). */
+typedef struct ni_work {
+    uint32_t seq;
+    uint32_t n_new;
+    uint32_t n_query;
+} ni_work;
+
+/* ---- lifecycle (BatchEngine::new + BatchEngine::batch, batch.rs:95-104,159-194) ---- */
+int ni_kv_create(const ni_kv_opts* opts, ni_kv** out);
+void ni_kv_destroy(ni_kv* kv);
+/* Text of the last failure on this handle; with kv == NULL, of the last
+ * failed ni_kv_create on this thread. */
+const char* ni_kv_last_error(const ni_kv* kv);
+/* Bytes of one page over all layers, K and V (BatchEngine::kv_block_bytes, batch.rs:107-109). */
+size_t ni_kv_page_bytes(const ni_kv* kv);
+
+/* ---- bookkeeping (batch.rs:200-254, 270) ---- */
+int ni_kv_add_seq(ni_kv* kv, uint32_t* seq);                    /* Batch::add_seq, :201-206 */
+int ni_kv_free_seq(ni_kv* kv, uint32_t seq);                    /* Batch::free_seq, :209-212 */
+int ni_kv_seq_len(const ni_kv* kv, uint32_t seq, uint32_t* len); /* Batch::seq_len, :214-216 */
+int ni_kv_is_live(const ni_kv* kv, uint32_t seq, int* live);     /* Batch::seq_live, :134 */
+int ni_kv_truncate(ni_kv* kv, uint32_t seq, uint32_t len);       /* Batch::truncate, :220-227 */
+int ni_kv_reserve(ni_kv* kv, uint32_t seq, uint32_t len);        /* Batch::ensure_blocks, :243-254 */
+int ni_kv_commit(ni_kv* kv, uint32_t seq, uint32_t n);           /* seq_len += n, :270 */
+/* Batch::block_table, :230-232.  *pages stays valid until the next
+ * bookkeeping call on this handle. */
+int ni_kv_block_table(const ni_kv* kv, uint32_t seq, const uint32_t** pages, uint32_t* n);
+uint32_t ni_kv_blocks_used(const ni_kv* kv);      /* Batch::blocks_used, :235-237 */
+uint32_t ni_kv_free_block_count(const ni_kv* kv); /* Batch::free_block_count, :238-240 */
+
+/* ---- data path (device) ---- */
+
+/* f32 K/V rows -> f16 (round to nearest even, quant.rs:25-54) into each
+ * row's page slot (b_kv_write, batch.metal:329-344).  Row i of k/v is
+ * rows[i]; layer l reads k + l*layer_stride (+ i*row_stride) when
+ * layer == NI_ALL_LAYERS, else `layer` is the only layer written and k/v
+ * point at its rows.  Positions must be reserved. */
+int ni_kv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* k, const float* v,
+                 int64_t row_stride, int64_t layer_stride, ni_stream stream);
+
+/* Block-table gather: f16 bits of K and V at (seq, pos) for each row, in the
+ * reference's row layout [C] = [head][head_dim] (the reads of b_attn_split,
+ * batch.metal:377,392, through kv_slot, :24-26).  Strides in halves. */
+int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint16_t* k_out, uint16_t* v_out,
+                 int64_t row_stride, int64_t layer_stride, ni_stream stream);
+
+/* Paged decode attention (b_attn_split + b_attn_merge, batch.metal:349-424;
+ * math of kv16.rs:144-164): row i attends causally to keys 0..rows[i].pos
+ * of rows[i].seq; out row i = softmax(q.K^T / sqrt(head_dim)) V.  Keys are
+ * split into partitions of `split_tokens` (a multiple of 16; 0 = automatic)
+ * and merged by log-sum-exp.  Consecutive rows of one sequence at
+ * consecutive positions (speculative verify, prefill chunks) share their
+ * K/V reads. */
+int ni_paged_decode_attention(ni_kv* kv, int32_t layer, const float* q, int64_t q_row_stride,
+                              int64_t q_layer_stride, const ni_row* rows, uint32_t n, float* out,
+                              int64_t out_row_stride, int64_t out_layer_stride, uint32_t split_tokens,
+                              ni_stream stream);
+
+/* One step of the hot path over every layer (Batch::step, batch.rs:259-315,
+ * the KV part): for each work item in order check it (not live / empty /
+ * context full / pool exhausted, the reference's errors and texts), reserve
+ * pages, then append all rows and run attention for the queried rows, and
+ * finally commit seq_len += n_new.  Rows are numbered in work order; row r
+ * of layer l is at base + l*layer_stride + r*row_stride in q/k/v and out. */
+int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k, const float* v,
+               int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
+               int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream);
+
+/* Wait for all work this handle enqueued on `stream`. */
+int ni_kv_sync(ni_kv* kv, ni_stream stream);
+
+/* Device pools, for inspection: K and V, each [n_layer][kv_pages][n_head][16][head_dim] f16. */
+int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes_each);
+
+/* quant.rs:25-54 on the device, elementwise (the conversion the append uses). */
+int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream);
+
+/* ---- measurement: HIP events around this handle's kernel launches ---- */
+enum ni_kernel_id { NI_K_APPEND = 0, NI_K_ATTN = 1, NI_K_MERGE = 2, NI_K_COUNT = 3 };
+int ni_kv_profile(ni_kv* kv, int enable);
+/* Total milliseconds and launches of one kernel since the last read (waits). */
+int ni_kv_profile_read(ni_kv* kv, int kernel, double* total_ms, uint64_t* launches);
+
+const char* ni_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NANOINFER_KV_H */

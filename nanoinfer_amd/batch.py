@@ -1,0 +1,290 @@
+"""Host-side mirror of the reference's paged-KV ``Batch`` API over the C ABI.
+
+``PagedKv`` keeps the names, argument meanings and error behaviour of the KV
+part of ``Batch`` (``crates/metal/src/batch.rs:128-363``):
+
+=====================  ==========================================  ==================
+reference              here                                        batch.rs
+=====================  ==========================================  ==================
+``add_seq``            ``add_seq() -> int | None``                 :201-206
+``free_seq``           ``free_seq(s)``                             :209-212
+``seq_len``            ``seq_len(s)``                              :214-216
+``truncate``           ``truncate(s, len)`` (AssertionError)       :220-227
+``block_table``        ``block_table(s) -> list[int]``             :230-232
+``blocks_used``        ``blocks_used()``                           :235-237
+``free_block_count``   ``free_block_count()``                      :238-240
+``ensure_blocks``      ``reserve(s, len)``                         :243-254
+``step``               ``step(work, q, k, v, out)``                :259-315
+``kv_block_bytes``     ``kv_block_bytes()``                        :107-109
+=====================  ==========================================  ==================
+
+``Err(String)`` results raise :class:`KvError` carrying the reference's text;
+the reference's panics (``truncate`` past the length) raise
+``AssertionError``.  Device buffers are torch tensors on the GPU (float32 for
+q/k/v/out, int16 for gathered f16 bits); work is enqueued on the current torch
+stream.  Nothing here computes on the CPU: every data call goes to the gfx950
+library and fails if it cannot.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _abi
+from ._abi import NI_ALL_LAYERS, NI_KV_BLOCK
+
+ALL_LAYERS = NI_ALL_LAYERS
+KV_BLOCK = NI_KV_BLOCK
+
+
+class KvError(RuntimeError):
+    """A failed call; ``code`` is the NI_ERR_* status, ``str()`` the message."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+@dataclass
+class BatchOpts:
+    """Sizes of a :class:`PagedKv` (the KV fields of ``BatchOpts``,
+    batch.rs:44-76, plus the model shape of ``Config``)."""
+
+    n_layer: int = 12
+    n_head: int = 12
+    head_dim: int = 64
+    kv_blocks: int = 1024
+    max_seqs: int = 64
+    n_ctx: int = 1024
+    max_rows: int = 512
+    host_only: bool = False
+    page_order: Optional[Sequence[int]] = None  # order in which pages are handed out
+
+    @property
+    def n_embd(self) -> int:
+        return self.n_head * self.head_dim
+
+
+def _stream_ptr(stream) -> int:
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+def _rows(rows) -> tuple:
+    arr = np.ascontiguousarray(np.asarray(rows, dtype=np.uint32).reshape(-1, 2))
+    n = arr.shape[0]
+    return arr, arr.ctypes.data_as(C.POINTER(_abi.ni_row)), n
+
+
+def _f32_arg(t, name, layered):
+    """(pointer, row_stride, layer_stride) of a float32 device tensor laid out
+    [n_layer][rows][C] (layered) or [rows][C]."""
+    import torch
+
+    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32:
+        raise TypeError(f"{name} must be a float32 CUDA tensor")
+    if layered:
+        if t.dim() != 3 or t.stride(2) != 1:
+            raise ValueError(f"{name} must be [n_layer, rows, C] with unit stride in C")
+        return t.data_ptr(), t.stride(1), t.stride(0)
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be [rows, C] with unit stride in C")
+    return t.data_ptr(), t.stride(0), 0
+
+
+class PagedKv:
+    """The KV cache and block tables of a batch of sequences on one MI355X."""
+
+    def __init__(self, opts: BatchOpts):
+        self.opts = opts
+        self._L = _abi.lib()
+        o = _abi.ni_kv_opts()
+        o.n_layer, o.n_head, o.head_dim = opts.n_layer, opts.n_head, opts.head_dim
+        o.kv_pages, o.max_seqs, o.max_ctx, o.max_rows = opts.kv_blocks, opts.max_seqs, opts.n_ctx, opts.max_rows
+        o.flags = _abi.NI_KV_HOST_ONLY if opts.host_only else 0
+        self._order = None
+        if opts.page_order is not None:
+            self._order = np.ascontiguousarray(np.asarray(opts.page_order, dtype=np.uint32))
+            o.page_order = self._order.ctypes.data_as(C.POINTER(C.c_uint32))
+        h = C.c_void_p()
+        rc = self._L.ni_kv_create(C.byref(o), C.byref(h))
+        if rc != 0:
+            raise KvError(rc, self._L.ni_kv_last_error(None).decode())
+        self._h = h
+
+    # -------------------------------------------------------------- plumbing
+    def close(self):
+        if getattr(self, "_h", None):
+            self._L.ni_kv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def _check(self, rc):
+        if rc != 0:
+            raise KvError(rc, self._L.ni_kv_last_error(self._h).decode())
+
+    @property
+    def max_blocks(self) -> int:
+        """Pages per sequence at most: ceil(n_ctx / 16) (batch.rs:164)."""
+        return -(-self.opts.n_ctx // KV_BLOCK)
+
+    # ------------------------------------------------------------ bookkeeping
+    def add_seq(self) -> Optional[int]:
+        s = C.c_uint32()
+        rc = self._L.ni_kv_add_seq(self._h, C.byref(s))
+        if rc == _abi.NI_ERR_NO_SLOT:
+            return None
+        self._check(rc)
+        return int(s.value)
+
+    def free_seq(self, s: int):
+        self._check(self._L.ni_kv_free_seq(self._h, s))
+
+    def seq_len(self, s: int) -> int:
+        n = C.c_uint32()
+        self._check(self._L.ni_kv_seq_len(self._h, s, C.byref(n)))
+        return int(n.value)
+
+    def is_live(self, s: int) -> bool:
+        v = C.c_int()
+        self._check(self._L.ni_kv_is_live(self._h, s, C.byref(v)))
+        return bool(v.value)
+
+    def truncate(self, s: int, length: int):
+        rc = self._L.ni_kv_truncate(self._h, s, length)
+        if rc == _abi.NI_ERR_BAD_LEN:
+            raise AssertionError(self._L.ni_kv_last_error(self._h).decode())
+        self._check(rc)
+
+    def reserve(self, s: int, length: int):
+        self._check(self._L.ni_kv_reserve(self._h, s, length))
+
+    def commit(self, s: int, n: int):
+        self._check(self._L.ni_kv_commit(self._h, s, n))
+
+    def block_table(self, s: int) -> list:
+        p = C.POINTER(C.c_uint32)()
+        n = C.c_uint32()
+        self._check(self._L.ni_kv_block_table(self._h, s, C.byref(p), C.byref(n)))
+        return [int(p[i]) for i in range(n.value)]
+
+    def blocks_used(self) -> int:
+        return int(self._L.ni_kv_blocks_used(self._h))
+
+    def free_block_count(self) -> int:
+        return int(self._L.ni_kv_free_block_count(self._h))
+
+    def kv_block_bytes(self) -> int:
+        return int(self._L.ni_kv_page_bytes(self._h))
+
+    # -------------------------------------------------------------- data path
+    def append(self, rows, k, v, layer: int = ALL_LAYERS, stream=None):
+        """Write f32 K/V rows as f16 into their pages (b_kv_write)."""
+        arr, rp, n = _rows(rows)
+        layered = layer == ALL_LAYERS
+        kp, rs, ls = _f32_arg(k, "k", layered)
+        vp, rs2, ls2 = _f32_arg(v, "v", layered)
+        if (rs, ls) != (rs2, ls2):
+            raise ValueError("k and v must share strides")
+        self._check(self._L.ni_kv_append(self._h, layer, rp, n, kp, vp, rs, ls, _stream_ptr(stream)))
+
+    def gather(self, rows, layer: int = ALL_LAYERS, stream=None):
+        """f16 bits (int16 tensors) of K and V at each (seq, pos) row."""
+        import torch
+
+        arr, rp, n = _rows(rows)
+        c = self.opts.n_embd
+        shape = (self.opts.n_layer, n, c) if layer == ALL_LAYERS else (n, c)
+        ko = torch.empty(shape, dtype=torch.int16, device="cuda")
+        vo = torch.empty(shape, dtype=torch.int16, device="cuda")
+        ls = n * c if layer == ALL_LAYERS else 0
+        self._check(self._L.ni_kv_gather(self._h, layer, rp, n, ko.data_ptr(), vo.data_ptr(), c, ls,
+                                         _stream_ptr(stream)))
+        return ko, vo
+
+    def attention(self, q, rows, out=None, layer: int = ALL_LAYERS, split_tokens: int = 0, stream=None):
+        """Paged decode attention of each row over keys 0..pos of its sequence."""
+        import torch
+
+        arr, rp, n = _rows(rows)
+        layered = layer == ALL_LAYERS
+        if out is None:
+            out = torch.zeros_like(q)
+        qp, qrs, qls = _f32_arg(q, "q", layered)
+        op, ors, ols = _f32_arg(out, "out", layered)
+        self._check(self._L.ni_paged_decode_attention(self._h, layer, qp, qrs, qls, rp, n, op, ors, ols,
+                                                      split_tokens, _stream_ptr(stream)))
+        return out
+
+    def step(self, work, q, k, v, out=None, split_tokens: int = 0, stream=None):
+        """One step over every layer (Batch::step's KV part).  ``work`` lists
+        ``(seq, n_new, n_query)``; rows are numbered in work order; q/k/v/out
+        are [n_layer, rows, C]."""
+        import torch
+
+        w = np.ascontiguousarray(np.asarray(work, dtype=np.uint32).reshape(-1, 3))
+        wp = w.ctypes.data_as(C.POINTER(_abi.ni_work))
+        kp, rs, ls = _f32_arg(k, "k", True)
+        vp, rs2, ls2 = _f32_arg(v, "v", True)
+        qp, rs3, ls3 = _f32_arg(q, "q", True)
+        if not (rs == rs2 == rs3 and ls == ls2 == ls3):
+            raise ValueError("q, k and v must share strides")
+        if out is None:
+            out = torch.zeros_like(q)
+        op, ors, ols = _f32_arg(out, "out", True)
+        self._check(self._L.ni_kv_step(self._h, wp, w.shape[0], qp, kp, vp, rs, ls, op, ors, ols, split_tokens,
+                                       _stream_ptr(stream)))
+        return out
+
+    def sync(self, stream=None):
+        self._check(self._L.ni_kv_sync(self._h, _stream_ptr(stream)))
+
+    def pools(self):
+        kp, vp, nb = C.c_void_p(), C.c_void_p(), C.c_size_t()
+        self._check(self._L.ni_kv_pools(self._h, C.byref(kp), C.byref(vp), C.byref(nb)))
+        return kp.value, vp.value, nb.value
+
+    # ------------------------------------------------------------ measurement
+    def profile(self, enable: bool = True):
+        self._check(self._L.ni_kv_profile(self._h, 1 if enable else 0))
+
+    def profile_read(self, kernel: int):
+        """(total ms, launches) of one kernel since the last read."""
+        ms, n = C.c_double(), C.c_uint64()
+        self._check(self._L.ni_kv_profile_read(self._h, kernel, C.byref(ms), C.byref(n)))
+        return float(ms.value), int(n.value)
+
+
+def f32_to_f16_device(x, out=None, stream=None):
+    """quant.rs:25-54 on the GPU, elementwise, through the library's device
+    conversion (the one the append uses).  Returns int16 bits."""
+    import torch
+
+    if not x.is_cuda or x.dtype != torch.float32 or not x.is_contiguous():
+        raise TypeError("x must be a contiguous float32 CUDA tensor")
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.int16, device=x.device)
+    rc = _abi.lib().ni_f32_to_f16(x.data_ptr(), out.data_ptr(), x.numel(), _stream_ptr(stream))
+    if rc != 0:
+        raise KvError(rc, "ni_f32_to_f16 failed")
+    return out

@@ -1,0 +1,841 @@
+// kv_host.cpp -- host side of the paged f16 KV-cache path and its C ABI.
+//
+// The page allocator and block tables restate Batch's bookkeeping
+// (crates/metal/src/batch.rs:129-254): a LIFO free stack initialised so that
+// pages are handed out 0, 1, 2, ... (:174), pages grown on demand
+// (ensure_blocks, :243-254), rollback freeing whole trailing pages last-first
+// (truncate, :220-227).  Error texts are the reference's.
+//
+// Each data-path call builds a compact plan (kv_plan.h) from its rows -- the
+// destination slot of every appended row, attention work items sorted
+// longest first, merge items, and the page lists those items read -- copies
+// it into a pinned staging slot, uploads it with one async copy on the
+// caller's stream and launches the kernels over it.  Staging slots are
+// recycled through events, so bookkeeping calls after a data call never
+// race with the work it enqueued.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kv_plan.h"
+#include "nanoinfer_kv.h"
+
+using namespace ni;
+
+namespace {
+
+constexpr uint32_t kRingSlots = 4;
+constexpr size_t kAlign = 256;
+constexpr uint32_t kMinSplit = 64;  // smallest partition the planner uses (tokens)
+
+thread_local std::string g_create_error;
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct StagingSlot {
+    uint8_t* host = nullptr;  // pinned
+    uint8_t* dev = nullptr;
+    size_t cap = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+};
+
+// Work of one data-path call, before serialisation.
+struct Plan {
+    std::vector<AppendEntry> app;
+    std::vector<AttnItem> items;
+    std::vector<MergeItem> merges;
+    std::vector<uint32_t> table;
+    uint32_t n_slots = 0;
+    uint32_t nq_tile = 1;
+    void clear() {
+        app.clear();
+        items.clear();
+        merges.clear();
+        table.clear();
+        n_slots = 0;
+        nq_tile = 1;
+    }
+};
+
+// A query row as the planner sees it.
+struct QRow {
+    uint32_t row, seq, pos;
+};
+
+}  // namespace
+
+struct ni_kv {
+    ni_kv_opts o{};
+    uint32_t max_pages = 0;  // per sequence: ceil(max_ctx / 16) (batch.rs:164)
+    std::vector<uint32_t> seq_len;
+    std::vector<uint8_t> live;
+    std::vector<std::vector<uint32_t>> pages;
+    std::vector<uint32_t> free_pages;  // LIFO stack, back() is handed out next
+    std::string err;
+    bool host_only = false;
+    int device = 0;
+
+    uint16_t* kpool = nullptr;
+    uint16_t* vpool = nullptr;
+    size_t pool_bytes = 0;  // each of K and V
+    uint64_t layer_halves = 0;
+
+    StagingSlot ring[kRingSlots];
+    uint32_t ring_next = 0;
+    float* partials = nullptr;
+    size_t partials_bytes = 0;
+
+    bool profile = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[NI_K_COUNT];
+    std::vector<hipEvent_t> ev_pool;
+
+    // scratch reused across calls
+    Plan plan;
+    std::vector<QRow> qrows;
+    std::vector<int64_t> seq_tab;     // seq -> offset in plan.table, -1 if absent
+    std::vector<uint32_t> seq_need;   // seq -> pages needed this call
+    std::vector<uint8_t> staging_tmp;
+
+    int fail(int code, const char* fmt, ...) __attribute__((format(printf, 3, 4))) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        err = buf;
+        return code;
+    }
+    int hip_fail(hipError_t e, const char* what) {
+        return fail(NI_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    }
+    PoolGeom geom() const {
+        PoolGeom g;
+        g.k = kpool;
+        g.v = vpool;
+        g.layer_halves = layer_halves;
+        g.n_head = o.n_head;
+        g.head_dim = o.head_dim;
+        return g;
+    }
+};
+
+namespace {
+
+int check_seq(ni_kv* kv, uint32_t s) {
+    if (s >= kv->o.max_seqs) return kv->fail(NI_ERR_BAD_ARG, "sequence %u out of range (%u slots)", s, kv->o.max_seqs);
+    return NI_OK;
+}
+
+// Batch::ensure_blocks (batch.rs:243-254).
+int ensure_pages(ni_kv* kv, uint32_t s, uint64_t len) {
+    if (len > kv->o.max_ctx)
+        return kv->fail(NI_ERR_CONTEXT_FULL, "sequence %u: context full (%llu > %u)", s, (unsigned long long)len,
+                        kv->o.max_ctx);
+    auto& pg = kv->pages[s];
+    while ((uint64_t)pg.size() * kPage < len) {
+        if (kv->free_pages.empty()) return kv->fail(NI_ERR_POOL_EXHAUSTED, "KV cache pool exhausted");
+        pg.push_back(kv->free_pages.back());
+        kv->free_pages.pop_back();
+    }
+    return NI_OK;
+}
+
+// Batch::truncate (batch.rs:220-227).
+int truncate_seq(ni_kv* kv, uint32_t s, uint32_t len) {
+    if (len > kv->seq_len[s]) return kv->fail(NI_ERR_BAD_LEN, "assertion failed: len <= self.seq_len[s]");
+    kv->seq_len[s] = len;
+    const size_t keep = (len + kPage - 1) / kPage;
+    auto& pg = kv->pages[s];
+    while (pg.size() > keep) {
+        kv->free_pages.push_back(pg.back());
+        pg.pop_back();
+    }
+    return NI_OK;
+}
+
+// Is position `pos` of live sequence `s` backed by a page?
+int check_row(ni_kv* kv, const ni_row& r) {
+    if (r.seq >= kv->o.max_seqs)
+        return kv->fail(NI_ERR_BAD_ARG, "sequence %u out of range (%u slots)", r.seq, kv->o.max_seqs);
+    if (!kv->live[r.seq]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", r.seq);
+    if ((uint64_t)r.pos >= (uint64_t)kv->pages[r.seq].size() * kPage)
+        return kv->fail(NI_ERR_NOT_RESERVED, "sequence %u: position %u has no page (reserved %zu)", r.seq, r.pos,
+                        kv->pages[r.seq].size() * kPage);
+    return NI_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_f32_operand(ni_kv* kv, const char* name, const void* p, int64_t row_stride, int64_t layer_stride,
+                      bool all_layers) {
+    if (!p) return kv->fail(NI_ERR_BAD_ARG, "%s is NULL", name);
+    if (!aligned16(p) || row_stride % 4 != 0 || (all_layers && layer_stride % 4 != 0) || row_stride < 0 ||
+        (all_layers && layer_stride < 0))
+        return kv->fail(NI_ERR_BAD_ARG, "%s must be 16-byte aligned with non-negative strides that are multiples of 4",
+                        name);
+    return NI_OK;
+}
+
+int layer_range(ni_kv* kv, int32_t layer, uint32_t* layer0, uint32_t* n_lay) {
+    if (layer == NI_ALL_LAYERS) {
+        *layer0 = 0;
+        *n_lay = kv->o.n_layer;
+        return NI_OK;
+    }
+    if (layer < 0 || (uint32_t)layer >= kv->o.n_layer)
+        return kv->fail(NI_ERR_BAD_ARG, "layer %d out of range (%u layers)", layer, kv->o.n_layer);
+    *layer0 = (uint32_t)layer;
+    *n_lay = 1;
+    return NI_OK;
+}
+
+uint32_t pow2_tile(uint32_t nq) {
+    uint32_t t = 1;
+    while (t < nq) t <<= 1;
+    return t;
+}
+
+// Attention part of a plan: group consecutive query rows of one sequence at
+// consecutive positions, split each group's keys into partitions, sort the
+// items longest first.
+int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
+    Plan& P = kv->plan;
+    const auto& qr = kv->qrows;
+    if (qr.empty()) return NI_OK;
+    struct Group {
+        uint32_t seq, row0, pos0, nq;
+    };
+    std::vector<Group> groups;
+    groups.reserve(qr.size());
+    for (const QRow& r : qr) {
+        if (!groups.empty()) {
+            Group& g = groups.back();
+            if (g.seq == r.seq && g.row0 + g.nq == r.row && g.pos0 + g.nq == r.pos && g.nq < kMaxGroupRows) {
+                g.nq++;
+                continue;
+            }
+        }
+        groups.push_back({r.seq, r.row, r.pos, 1});
+    }
+    // Partition size: the caller's, or (0) the largest of 1024/512/256/128
+    // tokens that still yields >= 4096 workgroups, so that every CU has
+    // work and the ragged tail is short.
+    uint32_t part = split_tokens;
+    if (part == 0) {
+        static const uint32_t kChoices[] = {1024, 512, 256, 128};
+        const uint64_t target = 4096;
+        const uint64_t per_unit = (uint64_t)n_lay * kv->o.n_head;
+        part = kChoices[3];
+        for (uint32_t c : kChoices) {
+            uint64_t items = 0;
+            for (const Group& g : groups) items += ((uint64_t)g.pos0 + g.nq + c - 1) / c;
+            if (items * per_unit >= target) {
+                part = c;
+                break;
+            }
+        }
+    } else if (part % kPage != 0 || part < kMinSplit) {
+        return kv->fail(NI_ERR_BAD_ARG, "split_tokens %u must be 0 or a multiple of 16 that is >= %u", split_tokens,
+                        kMinSplit);
+    }
+    // Page lists: one segment per sequence, long enough for its last query.
+    for (const Group& g : groups) {
+        const uint32_t need = (g.pos0 + g.nq + kPage - 1) / kPage;
+        kv->seq_need[g.seq] = std::max(kv->seq_need[g.seq], need);
+    }
+    for (const Group& g : groups) {
+        if (kv->seq_tab[g.seq] >= 0) continue;
+        kv->seq_tab[g.seq] = (int64_t)P.table.size();
+        const auto& pg = kv->pages[g.seq];
+        P.table.insert(P.table.end(), pg.begin(), pg.begin() + kv->seq_need[g.seq]);
+    }
+    uint32_t max_nq = 1;
+    for (const Group& g : groups) {
+        max_nq = std::max(max_nq, g.nq);
+        const uint32_t L = g.pos0 + g.nq;
+        const uint32_t n_parts = (L + part - 1) / part;
+        const uint32_t tab = (uint32_t)kv->seq_tab[g.seq];
+        if (n_parts <= 1) {
+            P.items.push_back({tab, g.row0, g.pos0, g.nq, 0, L, kNoSlot, 0});
+            continue;
+        }
+        const uint32_t slot0 = P.n_slots;
+        for (uint32_t p = 0; p < n_parts; p++)
+            P.items.push_back({tab, g.row0, g.pos0, g.nq, p * part, std::min((p + 1) * part, L), slot0 + p, 0});
+        P.merges.push_back({g.row0, g.nq, slot0, n_parts});
+        P.n_slots += n_parts;
+    }
+    for (const Group& g : groups) {
+        kv->seq_need[g.seq] = 0;
+        kv->seq_tab[g.seq] = -1;
+    }
+    // Longest first, so the long items start early and the short ones fill
+    // the tail.
+    std::stable_sort(P.items.begin(), P.items.end(), [](const AttnItem& x, const AttnItem& y) {
+        return (x.kv_end - x.kv_begin) > (y.kv_end - y.kv_begin);
+    });
+    P.nq_tile = pow2_tile(max_nq);
+    return NI_OK;
+}
+
+hipEvent_t take_event(ni_kv* kv) {
+    if (!kv->ev_pool.empty()) {
+        hipEvent_t e = kv->ev_pool.back();
+        kv->ev_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+struct ProfileScope {
+    ni_kv* kv;
+    int kernel;
+    hipStream_t s;
+    hipEvent_t a = nullptr, b = nullptr;
+    ProfileScope(ni_kv* kv_, int k, hipStream_t s_) : kv(kv_), kernel(k), s(s_) {
+        if (!kv->profile) return;
+        a = take_event(kv);
+        b = take_event(kv);
+        if (a) (void)hipEventRecord(a, s);
+    }
+    ~ProfileScope() {
+        if (!a || !b) return;
+        (void)hipEventRecord(b, s);
+        kv->prof_ev[kernel].push_back({a, b});
+    }
+};
+
+// Reserve a staging slot of at least `bytes`; waits for the slot's previous
+// use to finish.
+int acquire_slot(ni_kv* kv, size_t bytes, StagingSlot** out) {
+    StagingSlot& sl = kv->ring[kv->ring_next];
+    kv->ring_next = (kv->ring_next + 1) % kRingSlots;
+    if (sl.pending) {
+        hipError_t e = hipEventSynchronize(sl.done);
+        if (e != hipSuccess) return kv->hip_fail(e, "hipEventSynchronize(staging)");
+        sl.pending = false;
+    }
+    if (sl.cap < bytes) {
+        size_t cap = std::max<size_t>(align_up(bytes * 2, 1 << 16), 1 << 18);
+        if (sl.host) (void)hipHostFree(sl.host);
+        if (sl.dev) (void)hipFree(sl.dev);
+        sl.host = nullptr;
+        sl.dev = nullptr;
+        sl.cap = 0;
+        hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&sl.host), cap, hipHostMallocDefault);
+        if (e != hipSuccess) return kv->hip_fail(e, "hipHostMalloc(staging)");
+        e = hipMalloc(reinterpret_cast<void**>(&sl.dev), cap);
+        if (e != hipSuccess) return kv->hip_fail(e, "hipMalloc(staging)");
+        sl.cap = cap;
+    }
+    *out = &sl;
+    return NI_OK;
+}
+
+int ensure_partials(ni_kv* kv, size_t bytes) {
+    if (bytes <= kv->partials_bytes) return NI_OK;
+    // In-flight kernels may still read the old buffer.
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return kv->hip_fail(e, "hipDeviceSynchronize");
+    if (kv->partials) (void)hipFree(kv->partials);
+    kv->partials = nullptr;
+    kv->partials_bytes = 0;
+    size_t cap = align_up(bytes + bytes / 2, 1 << 20);
+    e = hipMalloc(reinterpret_cast<void**>(&kv->partials), cap);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipMalloc(partials)");
+    kv->partials_bytes = cap;
+    return NI_OK;
+}
+
+struct Offsets {
+    size_t app, items, merges, table, total;
+};
+
+Offsets layout(const Plan& P) {
+    Offsets o;
+    o.app = 0;
+    o.items = align_up(o.app + P.app.size() * sizeof(AppendEntry), kAlign);
+    o.merges = align_up(o.items + P.items.size() * sizeof(AttnItem), kAlign);
+    o.table = align_up(o.merges + P.merges.size() * sizeof(MergeItem), kAlign);
+    o.total = align_up(o.table + P.table.size() * sizeof(uint32_t), kAlign);
+    return o;
+}
+
+// Copy the plan into a staging slot and enqueue its upload.
+int upload_plan(ni_kv* kv, hipStream_t s, StagingSlot** slot_out, Offsets* off) {
+    const Plan& P = kv->plan;
+    *off = layout(P);
+    StagingSlot* sl = nullptr;
+    int rc = acquire_slot(kv, off->total, &sl);
+    if (rc) return rc;
+    if (!P.app.empty()) memcpy(sl->host + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
+    if (!P.items.empty()) memcpy(sl->host + off->items, P.items.data(), P.items.size() * sizeof(AttnItem));
+    if (!P.merges.empty()) memcpy(sl->host + off->merges, P.merges.data(), P.merges.size() * sizeof(MergeItem));
+    if (!P.table.empty()) memcpy(sl->host + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
+    hipError_t e = hipMemcpyAsync(sl->dev, sl->host, off->total, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipMemcpyAsync(plan)");
+    *slot_out = sl;
+    return NI_OK;
+}
+
+int finish_slot(ni_kv* kv, StagingSlot* sl, hipStream_t s) {
+    hipError_t e = hipEventRecord(sl->done, s);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipEventRecord(staging)");
+    sl->pending = true;
+    return NI_OK;
+}
+
+// Append + attention + merge over an already built plan.
+int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const float* v, int64_t kv_row_stride,
+             int64_t kv_layer_stride, const float* q, int64_t q_row_stride, int64_t q_layer_stride, float* out,
+             int64_t out_row_stride, int64_t out_layer_stride, hipStream_t s) {
+    Plan& P = kv->plan;
+    const uint32_t D = kv->o.head_dim, H = kv->o.n_head;
+    if (!P.items.empty() && P.n_slots > 0) {
+        const size_t need = (size_t)P.n_slots * n_lay * H * P.nq_tile * (D + 2) * sizeof(float);
+        int rc = ensure_partials(kv, need);
+        if (rc) return rc;
+    }
+    StagingSlot* sl = nullptr;
+    Offsets off;
+    int rc = upload_plan(kv, s, &sl, &off);
+    if (rc) return rc;
+    if (!P.app.empty()) {
+        AppendLaunch a;
+        a.pool = kv->geom();
+        a.k = k;
+        a.v = v;
+        a.row_stride = kv_row_stride;
+        a.layer_stride = kv_layer_stride;
+        a.entries = reinterpret_cast<const AppendEntry*>(sl->dev + off.app);
+        a.n_rows = (uint32_t)P.app.size();
+        a.layer0 = layer0;
+        a.n_lay = n_lay;
+        ProfileScope ps(kv, NI_K_APPEND, s);
+        hipError_t e = launch_append(a, s);
+        if (e != hipSuccess) return kv->hip_fail(e, "append kernel");
+    }
+    if (!P.items.empty()) {
+        AttnLaunch a;
+        a.pool = kv->geom();
+        a.q = q;
+        a.q_row_stride = q_row_stride;
+        a.q_layer_stride = q_layer_stride;
+        a.out = out;
+        a.out_row_stride = out_row_stride;
+        a.out_layer_stride = out_layer_stride;
+        a.items = reinterpret_cast<const AttnItem*>(sl->dev + off.items);
+        a.table = reinterpret_cast<const uint32_t*>(sl->dev + off.table);
+        a.partials = kv->partials;
+        a.merges = reinterpret_cast<const MergeItem*>(sl->dev + off.merges);
+        a.n_items = (uint32_t)P.items.size();
+        a.n_merges = (uint32_t)P.merges.size();
+        a.layer0 = layer0;
+        a.n_lay = n_lay;
+        a.nq_tile = P.nq_tile;
+        a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
+        {
+            ProfileScope ps(kv, NI_K_ATTN, s);
+            hipError_t e = launch_attention(a, s);
+            if (e != hipSuccess) return kv->hip_fail(e, "attention kernel");
+        }
+        if (!P.merges.empty()) {
+            ProfileScope ps(kv, NI_K_MERGE, s);
+            hipError_t e = launch_merge(a, s);
+            if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
+        }
+    }
+    return finish_slot(kv, sl, s);
+}
+
+void reset_plan(ni_kv* kv) {
+    kv->plan.clear();
+    kv->qrows.clear();
+}
+
+}  // namespace
+
+// ============================================================= C ABI
+
+extern "C" {
+
+const char* ni_version(void) { return "nanoinfer-amd 0.1 (gfx950 paged f16 KV)"; }
+
+const char* ni_kv_last_error(const ni_kv* kv) { return kv ? kv->err.c_str() : g_create_error.c_str(); }
+
+int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
+    if (!out) return NI_ERR_BAD_ARG;
+    *out = nullptr;
+    if (!opts) {
+        g_create_error = "opts is NULL";
+        return NI_ERR_BAD_ARG;
+    }
+    const ni_kv_opts& o = *opts;
+    const uint64_t C = (uint64_t)o.n_head * o.head_dim;
+    if (o.n_layer == 0 || o.n_head == 0 || o.head_dim == 0 || o.kv_pages == 0 || o.max_seqs == 0 || o.max_ctx == 0 ||
+        o.max_rows == 0 || o.head_dim % 8 != 0) {
+        g_create_error = "n_layer, n_head, kv_pages, max_seqs, max_ctx and max_rows must be > 0; head_dim a multiple of 8";
+        return NI_ERR_BAD_ARG;
+    }
+    const bool host_only = (o.flags & NI_KV_HOST_ONLY) != 0;
+    if (!host_only && !attention_supported(o.head_dim)) {
+        g_create_error = "head_dim " + std::to_string(o.head_dim) + " unsupported on the device (64 or 128)";
+        return NI_ERR_BAD_ARG;
+    }
+    // 32-bit index limits of the append/gather grids.
+    if ((uint64_t)o.n_layer * o.max_rows * 2 * (C / 8) >= (1ull << 31)) {
+        g_create_error = "n_layer * max_rows * C too large";
+        return NI_ERR_BAD_ARG;
+    }
+    ni_kv* kv = new ni_kv();
+    kv->o = o;
+    kv->o.page_order = nullptr;
+    kv->host_only = host_only;
+    kv->max_pages = (o.max_ctx + kPage - 1) / kPage;
+    kv->seq_len.assign(o.max_seqs, 0);
+    kv->live.assign(o.max_seqs, 0);
+    kv->pages.assign(o.max_seqs, {});
+    kv->seq_tab.assign(o.max_seqs, -1);
+    kv->seq_need.assign(o.max_seqs, 0);
+    // batch.rs:174: (0..kv_blocks).rev() so that pop() yields 0, 1, 2, ...
+    kv->free_pages.resize(o.kv_pages);
+    if (o.page_order) {
+        std::vector<uint8_t> seen(o.kv_pages, 0);
+        for (uint32_t i = 0; i < o.kv_pages; i++) {
+            const uint32_t p = o.page_order[i];
+            if (p >= o.kv_pages || seen[p]) {
+                g_create_error = "page_order must be a permutation of 0..kv_pages-1";
+                delete kv;
+                return NI_ERR_BAD_ARG;
+            }
+            seen[p] = 1;
+            kv->free_pages[o.kv_pages - 1 - i] = p;
+        }
+    } else {
+        for (uint32_t i = 0; i < o.kv_pages; i++) kv->free_pages[i] = o.kv_pages - 1 - i;
+    }
+    if (!host_only) {
+        hipError_t e = hipGetDevice(&kv->device);
+        if (e == hipSuccess) {
+            kv->layer_halves = (uint64_t)o.kv_pages * kPage * C;
+            kv->pool_bytes = (size_t)(kv->layer_halves * o.n_layer * sizeof(uint16_t));
+            e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
+        }
+        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&kv->vpool), kv->pool_bytes);
+        // Zero pages: a page that was never written reads as finite zeros.
+        if (e == hipSuccess) e = hipMemset(kv->kpool, 0, kv->pool_bytes);
+        if (e == hipSuccess) e = hipMemset(kv->vpool, 0, kv->pool_bytes);
+        for (uint32_t i = 0; e == hipSuccess && i < kRingSlots; i++)
+            e = hipEventCreateWithFlags(&kv->ring[i].done, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            g_create_error = std::string("device setup failed: ") + hipGetErrorString(e);
+            ni_kv_destroy(kv);
+            return NI_ERR_HIP;
+        }
+    }
+    *out = kv;
+    return NI_OK;
+}
+
+void ni_kv_destroy(ni_kv* kv) {
+    if (!kv) return;
+    if (!kv->host_only) {
+        for (auto& sl : kv->ring)
+            if (sl.pending) (void)hipEventSynchronize(sl.done);
+        (void)hipDeviceSynchronize();
+        for (auto& sl : kv->ring) {
+            if (sl.host) (void)hipHostFree(sl.host);
+            if (sl.dev) (void)hipFree(sl.dev);
+            if (sl.done) (void)hipEventDestroy(sl.done);
+        }
+        for (auto& v : kv->prof_ev)
+            for (auto& pr : v) {
+                (void)hipEventDestroy(pr.first);
+                (void)hipEventDestroy(pr.second);
+            }
+        for (hipEvent_t e : kv->ev_pool) (void)hipEventDestroy(e);
+        if (kv->partials) (void)hipFree(kv->partials);
+        if (kv->kpool) (void)hipFree(kv->kpool);
+        if (kv->vpool) (void)hipFree(kv->vpool);
+    }
+    delete kv;
+}
+
+size_t ni_kv_page_bytes(const ni_kv* kv) {
+    return kv ? (size_t)2 * kv->o.n_layer * kPage * kv->o.n_head * kv->o.head_dim * 2 : 0;
+}
+
+int ni_kv_add_seq(ni_kv* kv, uint32_t* seq) {
+    if (!kv || !seq) return NI_ERR_BAD_ARG;
+    for (uint32_t s = 0; s < kv->o.max_seqs; s++) {
+        if (!kv->live[s]) {
+            kv->live[s] = 1;
+            kv->seq_len[s] = 0;
+            *seq = s;
+            return NI_OK;
+        }
+    }
+    return kv->fail(NI_ERR_NO_SLOT, "no sequence slot");
+}
+
+int ni_kv_free_seq(ni_kv* kv, uint32_t s) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (int rc = check_seq(kv, s)) return rc;
+    truncate_seq(kv, s, 0);
+    kv->live[s] = 0;
+    return NI_OK;
+}
+
+int ni_kv_seq_len(const ni_kv* kv, uint32_t s, uint32_t* len) {
+    if (!kv || !len) return NI_ERR_BAD_ARG;
+    if (s >= kv->o.max_seqs) return NI_ERR_BAD_ARG;
+    *len = kv->seq_len[s];
+    return NI_OK;
+}
+
+int ni_kv_is_live(const ni_kv* kv, uint32_t s, int* live) {
+    if (!kv || !live) return NI_ERR_BAD_ARG;
+    if (s >= kv->o.max_seqs) return NI_ERR_BAD_ARG;
+    *live = kv->live[s] ? 1 : 0;
+    return NI_OK;
+}
+
+int ni_kv_truncate(ni_kv* kv, uint32_t s, uint32_t len) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (int rc = check_seq(kv, s)) return rc;
+    return truncate_seq(kv, s, len);
+}
+
+int ni_kv_reserve(ni_kv* kv, uint32_t s, uint32_t len) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (int rc = check_seq(kv, s)) return rc;
+    if (!kv->live[s]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", s);
+    return ensure_pages(kv, s, len);
+}
+
+int ni_kv_commit(ni_kv* kv, uint32_t s, uint32_t n) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (int rc = check_seq(kv, s)) return rc;
+    if (!kv->live[s]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", s);
+    const uint64_t len = (uint64_t)kv->seq_len[s] + n;
+    if (len > (uint64_t)kv->pages[s].size() * kPage)
+        return kv->fail(NI_ERR_NOT_RESERVED, "sequence %u: commit to %llu past reserved %zu", s,
+                        (unsigned long long)len, kv->pages[s].size() * kPage);
+    kv->seq_len[s] = (uint32_t)len;
+    return NI_OK;
+}
+
+int ni_kv_block_table(const ni_kv* kv, uint32_t s, const uint32_t** pages, uint32_t* n) {
+    if (!kv || !pages || !n) return NI_ERR_BAD_ARG;
+    if (s >= kv->o.max_seqs) return NI_ERR_BAD_ARG;
+    *pages = kv->pages[s].data();
+    *n = (uint32_t)kv->pages[s].size();
+    return NI_OK;
+}
+
+uint32_t ni_kv_blocks_used(const ni_kv* kv) { return kv ? kv->o.kv_pages - (uint32_t)kv->free_pages.size() : 0; }
+
+uint32_t ni_kv_free_block_count(const ni_kv* kv) { return kv ? (uint32_t)kv->free_pages.size() : 0; }
+
+int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes_each) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (k_pool) *k_pool = kv->kpool;
+    if (v_pool) *v_pool = kv->vpool;
+    if (bytes_each) *bytes_each = kv->pool_bytes;
+    return NI_OK;
+}
+
+int ni_kv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* k, const float* v,
+                 int64_t row_stride, int64_t layer_stride, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    uint32_t layer0, n_lay;
+    if (int rc = layer_range(kv, layer, &layer0, &n_lay)) return rc;
+    if (n == 0) return NI_OK;
+    if (!rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
+    if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "%u rows > max_rows %u", n, kv->o.max_rows);
+    const bool all = layer == NI_ALL_LAYERS;
+    if (int rc = check_f32_operand(kv, "k", k, row_stride, layer_stride, all)) return rc;
+    if (int rc = check_f32_operand(kv, "v", v, row_stride, layer_stride, all)) return rc;
+    reset_plan(kv);
+    for (uint32_t i = 0; i < n; i++) {
+        if (int rc = check_row(kv, rows[i])) return rc;
+        const ni_row& r = rows[i];
+        kv->plan.app.push_back({i, kv->pages[r.seq][r.pos / kPage], r.pos % kPage, 0});
+    }
+    return run_plan(kv, layer0, n_lay, k, v, row_stride, all ? layer_stride : 0, nullptr, 0, 0, nullptr, 0, 0,
+                    (hipStream_t)stream);
+}
+
+int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint16_t* k_out, uint16_t* v_out,
+                 int64_t row_stride, int64_t layer_stride, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    uint32_t layer0, n_lay;
+    if (int rc = layer_range(kv, layer, &layer0, &n_lay)) return rc;
+    if (n == 0) return NI_OK;
+    if (!rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
+    if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "%u rows > max_rows %u", n, kv->o.max_rows);
+    const bool all = layer == NI_ALL_LAYERS;
+    if (!k_out || !v_out || !aligned16(k_out) || !aligned16(v_out) || row_stride % 8 != 0 || row_stride < 0 ||
+        (all && (layer_stride % 8 != 0 || layer_stride < 0)))
+        return kv->fail(NI_ERR_BAD_ARG, "k_out/v_out must be 16-byte aligned with strides that are multiples of 8");
+    reset_plan(kv);
+    for (uint32_t i = 0; i < n; i++) {
+        if (int rc = check_row(kv, rows[i])) return rc;
+        const ni_row& r = rows[i];
+        kv->plan.app.push_back({i, kv->pages[r.seq][r.pos / kPage], r.pos % kPage, 0});
+    }
+    StagingSlot* sl = nullptr;
+    Offsets off;
+    hipStream_t s = (hipStream_t)stream;
+    if (int rc = upload_plan(kv, s, &sl, &off)) return rc;
+    GatherLaunch g;
+    g.pool = kv->geom();
+    g.k_out = k_out;
+    g.v_out = v_out;
+    g.row_stride = row_stride;
+    g.layer_stride = all ? layer_stride : 0;
+    g.entries = reinterpret_cast<const AppendEntry*>(sl->dev + off.app);
+    g.n_rows = n;
+    g.layer0 = layer0;
+    g.n_lay = n_lay;
+    hipError_t e = launch_gather(g, s);
+    if (e != hipSuccess) return kv->hip_fail(e, "gather kernel");
+    return finish_slot(kv, sl, s);
+}
+
+int ni_paged_decode_attention(ni_kv* kv, int32_t layer, const float* q, int64_t q_row_stride,
+                              int64_t q_layer_stride, const ni_row* rows, uint32_t n, float* out,
+                              int64_t out_row_stride, int64_t out_layer_stride, uint32_t split_tokens,
+                              ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    uint32_t layer0, n_lay;
+    if (int rc = layer_range(kv, layer, &layer0, &n_lay)) return rc;
+    if (n == 0) return NI_OK;
+    if (!rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
+    if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "%u rows > max_rows %u", n, kv->o.max_rows);
+    const bool all = layer == NI_ALL_LAYERS;
+    if (int rc = check_f32_operand(kv, "q", q, q_row_stride, q_layer_stride, all)) return rc;
+    if (int rc = check_f32_operand(kv, "out", out, out_row_stride, out_layer_stride, all)) return rc;
+    reset_plan(kv);
+    for (uint32_t i = 0; i < n; i++) {
+        if (int rc = check_row(kv, rows[i])) return rc;
+        kv->qrows.push_back({i, rows[i].seq, rows[i].pos});
+    }
+    if (int rc = plan_attention(kv, split_tokens, n_lay)) return rc;
+    return run_plan(kv, layer0, n_lay, nullptr, nullptr, 0, 0, q, q_row_stride, all ? q_layer_stride : 0, out,
+                    out_row_stride, all ? out_layer_stride : 0, (hipStream_t)stream);
+}
+
+int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k, const float* v,
+               int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
+               int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    if (n_work == 0) return NI_OK;
+    if (!work) return kv->fail(NI_ERR_BAD_ARG, "work is NULL");
+    if (int rc = check_f32_operand(kv, "k", k, row_stride, layer_stride, true)) return rc;
+    if (int rc = check_f32_operand(kv, "v", v, row_stride, layer_stride, true)) return rc;
+    bool any_query = false;
+    for (uint32_t w = 0; w < n_work; w++) any_query |= work[w].n_query > 0;
+    if (any_query) {
+        if (int rc = check_f32_operand(kv, "q", q, row_stride, layer_stride, true)) return rc;
+        if (int rc = check_f32_operand(kv, "out", out, out_row_stride, out_layer_stride, true)) return rc;
+    }
+    reset_plan(kv);
+    // Batch::encode_step (batch.rs:280-305): check each item, grow its pages,
+    // lay out its rows.
+    uint64_t n_rows = 0;
+    for (uint32_t w = 0; w < n_work; w++) {
+        const ni_work& it = work[w];
+        if (int rc = check_seq(kv, it.seq)) return rc;
+        if (!kv->live[it.seq]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", it.seq);
+        if (it.n_new == 0) return kv->fail(NI_ERR_EMPTY_WORK, "empty work item");
+        if (it.n_query > it.n_new)
+            return kv->fail(NI_ERR_BAD_ARG, "work item %u: n_query %u > n_new %u", w, it.n_query, it.n_new);
+        if (kv->seq_tab[it.seq] == -2) {
+            for (uint32_t v2 = 0; v2 < w; v2++) kv->seq_tab[work[v2].seq] = -1;
+            return kv->fail(NI_ERR_BAD_ARG, "sequence %u appears twice in one step", it.seq);
+        }
+        kv->seq_tab[it.seq] = -2;  // seen in this step
+        const uint32_t len = kv->seq_len[it.seq];
+        if (int rc = ensure_pages(kv, it.seq, (uint64_t)len + it.n_new)) return rc;
+        n_rows += it.n_new;
+    }
+    for (uint32_t w = 0; w < n_work; w++) kv->seq_tab[work[w].seq] = -1;
+    if (n_rows > kv->o.max_rows)
+        return kv->fail(NI_ERR_TOO_MANY_ROWS, "%llu rows > max_rows %u", (unsigned long long)n_rows, kv->o.max_rows);
+    uint32_t row = 0;
+    for (uint32_t w = 0; w < n_work; w++) {
+        const ni_work& it = work[w];
+        const uint32_t len = kv->seq_len[it.seq];
+        const auto& pg = kv->pages[it.seq];
+        for (uint32_t i = 0; i < it.n_new; i++, row++) {
+            const uint32_t pos = len + i;
+            kv->plan.app.push_back({row, pg[pos / kPage], pos % kPage, 0});
+            if (i >= it.n_new - it.n_query) kv->qrows.push_back({row, it.seq, pos});
+        }
+    }
+    if (int rc = plan_attention(kv, split_tokens, kv->o.n_layer)) return rc;
+    int rc = run_plan(kv, 0, kv->o.n_layer, k, v, row_stride, layer_stride, q, row_stride, layer_stride, out,
+                      out_row_stride, out_layer_stride, (hipStream_t)stream);
+    if (rc) return rc;
+    // batch.rs:270: the step's rows now belong to their sequences.
+    for (uint32_t w = 0; w < n_work; w++) kv->seq_len[work[w].seq] += work[w].n_new;
+    return NI_OK;
+}
+
+int ni_kv_sync(ni_kv* kv, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return NI_OK;
+    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipStreamSynchronize");
+    return NI_OK;
+}
+
+int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream) {
+    if (n == 0) return NI_OK;
+    if (!in || !out) return NI_ERR_BAD_ARG;
+    hipError_t e = launch_f32_to_f16(in, out, n, (hipStream_t)stream);
+    return e == hipSuccess ? NI_OK : NI_ERR_HIP;
+}
+
+int ni_kv_profile(ni_kv* kv, int enable) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device");
+    kv->profile = enable != 0;
+    return NI_OK;
+}
+
+int ni_kv_profile_read(ni_kv* kv, int kernel, double* total_ms, uint64_t* launches) {
+    if (!kv || kernel < 0 || kernel >= NI_K_COUNT) return NI_ERR_BAD_ARG;
+    double ms = 0;
+    uint64_t cnt = 0;
+    for (auto& pr : kv->prof_ev[kernel]) {
+        hipError_t e = hipEventSynchronize(pr.second);
+        float t = 0;
+        if (e == hipSuccess) e = hipEventElapsedTime(&t, pr.first, pr.second);
+        if (e != hipSuccess) return kv->hip_fail(e, "profile events");
+        ms += t;
+        cnt++;
+        kv->ev_pool.push_back(pr.first);
+        kv->ev_pool.push_back(pr.second);
+    }
+    kv->prof_ev[kernel].clear();
+    if (total_ms) *total_ms = ms;
+    if (launches) *launches = cnt;
+    return NI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,428 @@
+// kv_kernels.hip -- gfx950 (MI355X) kernels of the paged f16 KV-cache path.
+//
+// Pool layout (device): K and V each [n_layer][kv_pages][n_head][16][D] f16.
+// One (page, head) block of K is 16*D halves contiguous (2 KB at D = 64), so a
+// wave64 reading it with 16-byte lanes moves 1 KB per load instruction with
+// every lane on consecutive bytes.  The reference keeps [page][16][C]
+// (crates/metal/src/batch.rs:166); values are identical per (seq, pos, head, d),
+// only the placement differs.
+//
+// Kernels:
+//   kv_append_kernel   f32 K/V rows -> f16 page slots (b_kv_write, batch.metal:329-344)
+//   kv_gather_kernel   page slots -> f16 rows in the reference layout (kv_slot reads, :24-26)
+//   attn_split_kernel  paged flash-decoding, one workgroup per (item, layer, head)
+//                      (b_attn_split, batch.metal:349-400)
+//   attn_merge_kernel  log-sum-exp merge of partitions (b_attn_merge, :403-424)
+//
+// Everything is HBM-bound streaming of f16 K/V: no MFMA.  Arithmetic is f32;
+// softmax runs in the base-2 domain (scores pre-scaled by log2(e)/sqrt(D)).
+#include <hip/hip_runtime.h>
+
+#include "kv_plan.h"
+
+namespace ni {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+// f32 -> f16 bits with round to nearest even (the hardware conversion under
+// the default rounding mode keeps f16 subnormals and overflows to inf), NaN
+// made canonical sign|0x7e00 -- the rules of crates/core/src/quant.rs:25-54.
+__device__ __forceinline__ uint32_t f16_bits(float x) {
+    uint32_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+    const uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) > 0x7f800000u) h = ((b >> 16) & 0x8000u) | 0x7e00u;
+    return h;
+}
+
+__device__ __forceinline__ uint4 pack8(const float4 a, const float4 b) {
+    uint4 r;
+    r.x = f16_bits(a.x) | (f16_bits(a.y) << 16);
+    r.y = f16_bits(a.z) | (f16_bits(a.w) << 16);
+    r.z = f16_bits(b.x) | (f16_bits(b.y) << 16);
+    r.w = f16_bits(b.z) | (f16_bits(b.w) << 16);
+    return r;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane move inside a row of 16 lanes (DPP; no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the LPK consecutive lanes that hold one key row (LPK = 8 or 16).
+template <int LPK>
+__device__ __forceinline__ float key_sum(float x) {
+    x += dpp_move<0xb1>(x);                            // quad_perm(1,0,3,2): lane ^ 1
+    x += dpp_move<0x4e>(x);                            // quad_perm(2,3,0,1): lane ^ 2
+    if constexpr (LPK >= 8) x += dpp_move<0x141>(x);   // row_half_mirror: the other quad of 8
+    if constexpr (LPK >= 16) x += dpp_move<0x140>(x);  // row_mirror: the other 8 of 16
+    return x;
+}
+
+// (m, l, o) <- (m, l, o) (+) (m2, l2, o2): the log-sum-exp merge of two
+// partial softmax states (batch.metal:415-423), base 2.
+__device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[8], float m2, float l2,
+                                            const float (&o2)[8]) {
+    const float mn = fmaxf(m, m2);
+    const float a1 = fast_exp2(m - mn), a2 = fast_exp2(m2 - mn);
+    l = l * a1 + l2 * a2;
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = o[e] * a1 + o2[e] * a2;
+    m = mn;
+}
+
+// Running max starts at a finite sentinel so that exp2(m - m_new) of two
+// empty states is 1 (not NaN); masked scores are -inf and weigh 0.
+constexpr float kMinScore = -1e30f;
+
+// ------------------------------------------------------------------ append
+
+__global__ __launch_bounds__(256) void kv_append_kernel(const AppendLaunch a) {
+    const uint32_t D = a.pool.head_dim;
+    const uint32_t chunks = (a.pool.n_head * D) >> 3;  // 8 elements per thread
+    const uint32_t per_row = 2 * chunks;                 // K then V
+    const uint32_t per_layer = per_row * a.n_rows;
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    if (gid >= per_layer * a.n_lay) return;
+    const uint32_t lay = gid / per_layer;
+    uint32_t r = gid - lay * per_layer;
+    const uint32_t row = r / per_row;
+    r -= row * per_row;
+    const uint32_t is_v = r >= chunks;
+    const uint32_t c8 = (r - is_v * chunks) * 8;
+    const AppendEntry e = a.entries[row];
+    const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.layer_stride + (int64_t)e.src_row * a.row_stride + c8;
+    const float4 x0 = reinterpret_cast<const float4*>(src)[0];
+    const float4 x1 = reinterpret_cast<const float4*>(src)[1];
+    const uint32_t head = c8 / D, d0 = c8 - head * D;
+    uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)(a.layer0 + lay) * a.pool.layer_halves +
+                    ((uint64_t)e.page * a.pool.n_head + head) * (kPage * D) + e.slot * D + d0;
+    *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
+}
+
+__global__ __launch_bounds__(256) void kv_gather_kernel(const GatherLaunch a) {
+    const uint32_t D = a.pool.head_dim;
+    const uint32_t chunks = (a.pool.n_head * D) >> 3;
+    const uint32_t per_row = 2 * chunks;
+    const uint32_t per_layer = per_row * a.n_rows;
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    if (gid >= per_layer * a.n_lay) return;
+    const uint32_t lay = gid / per_layer;
+    uint32_t r = gid - lay * per_layer;
+    const uint32_t row = r / per_row;
+    r -= row * per_row;
+    const uint32_t is_v = r >= chunks;
+    const uint32_t c8 = (r - is_v * chunks) * 8;
+    const AppendEntry e = a.entries[row];
+    const uint32_t head = c8 / D, d0 = c8 - head * D;
+    const uint16_t* src = (is_v ? a.pool.v : a.pool.k) + (uint64_t)(a.layer0 + lay) * a.pool.layer_halves +
+                          ((uint64_t)e.page * a.pool.n_head + head) * (kPage * D) + e.slot * D + d0;
+    uint16_t* dst = (is_v ? a.v_out : a.k_out) + (int64_t)lay * a.layer_stride + (int64_t)e.src_row * a.row_stride + c8;
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+}
+
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ in, uint16_t* __restrict__ out,
+                                                         size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+    if (i < n) out[i] = static_cast<uint16_t>(f16_bits(in[i]));
+}
+
+// --------------------------------------------------------------- attention
+
+// One workgroup = W waves = one (item, layer, head).  Waves take the item's
+// pages round-robin, PB pages per iteration.  Inside a wave, lane l reads 16
+// bytes (8 halves) of key row kl = l / LPK, dims ds*8 .. ds*8+7 (ds = l % LPK):
+// one load instruction covers KPL = 64 / LPK key rows, a page LPP = 16 / KPL
+// loads.  Each lane keeps its own flash state (m, l, o[8]) per query over the
+// keys its key-row group sees; the groups are merged once at the end (wave
+// shuffles, then LDS across waves).
+template <int D, int NQ, int W, int PB>
+__global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a) {
+    constexpr int LPK = D / 8;
+    constexpr int KPL = 64 / LPK;
+    constexpr int LPP = kPage / KPL;
+    constexpr uint32_t PAGE_HALVES = kPage * D;
+    __shared__ float red[W][NQ][D + 2];
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t H = a.pool.n_head;
+    const uint32_t lh = a.n_lay * H;
+    const uint32_t item_i = blockIdx.x / lh;
+    const uint32_t rem = blockIdx.x - item_i * lh;
+    const uint32_t lay = rem / H;
+    const uint32_t head = rem - lay * H;
+    const AttnItem it = a.items[item_i];
+    const int kl = lane / LPK;
+    const int ds = lane % LPK;
+
+    float q[NQ][8];
+    {
+        const float* qb = a.q + (int64_t)lay * a.q_layer_stride + (int64_t)it.row0 * a.q_row_stride + head * D + ds * 8;
+#pragma unroll
+        for (int r = 0; r < NQ; r++) {
+            if (r < (int)it.nq) {
+                const float4 x0 = reinterpret_cast<const float4*>(qb + (int64_t)r * a.q_row_stride)[0];
+                const float4 x1 = reinterpret_cast<const float4*>(qb + (int64_t)r * a.q_row_stride)[1];
+                q[r][0] = x0.x * a.qscale; q[r][1] = x0.y * a.qscale;
+                q[r][2] = x0.z * a.qscale; q[r][3] = x0.w * a.qscale;
+                q[r][4] = x1.x * a.qscale; q[r][5] = x1.y * a.qscale;
+                q[r][6] = x1.z * a.qscale; q[r][7] = x1.w * a.qscale;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) q[r][e] = 0.f;
+            }
+        }
+    }
+    float m[NQ], l[NQ], o[NQ][8];
+#pragma unroll
+    for (int r = 0; r < NQ; r++) {
+        m[r] = kMinScore;
+        l[r] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[r][e] = 0.f;
+    }
+
+    const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * PAGE_HALVES;
+    const uint16_t* __restrict__ kbase = a.pool.k + layer_off;
+    const uint16_t* __restrict__ vbase = a.pool.v + layer_off;
+    const uint64_t page_stride = (uint64_t)H * PAGE_HALVES;
+    const uint32_t* __restrict__ tab = a.table + it.tab;
+    const uint32_t pg_begin = it.kv_begin / kPage;
+    const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
+    // Keys below full_end are visible to every query of the item.
+    const uint32_t full_end = min(it.pos0 + 1, it.kv_end);
+
+    for (uint32_t pg = pg_begin + wave * PB; pg < pg_end; pg += W * PB) {
+        uint4 kr[PB][LPP], vr[PB][LPP];
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+            if (pg + b < pg_end) {
+                const uint64_t phys = tab[pg + b];
+                const uint4* kp = reinterpret_cast<const uint4*>(kbase + phys * page_stride) + lane;
+                const uint4* vp = reinterpret_cast<const uint4*>(vbase + phys * page_stride) + lane;
+#pragma unroll
+                for (int i = 0; i < LPP; i++) {
+                    kr[b][i] = kp[i * 64];
+                    vr[b][i] = vp[i * 64];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < LPP; i++) {
+                    kr[b][i] = make_uint4(0, 0, 0, 0);
+                    vr[b][i] = make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
+        float s[NQ][PB][LPP];
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+#pragma unroll
+            for (int i = 0; i < LPP; i++) {
+                const half8_t kh = __builtin_bit_cast(half8_t, kr[b][i]);
+#pragma unroll
+                for (int r = 0; r < NQ; r++) {
+                    float acc = 0.f;
+                    if (r < (int)it.nq) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc = fmaf(q[r][e], static_cast<float>(kh[e]), acc);
+                    }
+                    s[r][b][i] = key_sum<LPK>(acc);
+                }
+            }
+        }
+        if ((pg + PB) * kPage > full_end) {  // a page past the first query's position: mask
+#pragma unroll
+            for (int b = 0; b < PB; b++) {
+#pragma unroll
+                for (int i = 0; i < LPP; i++) {
+                    const uint32_t j = (pg + b) * kPage + i * KPL + kl;
+                    if (j >= it.kv_end) vr[b][i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < NQ; r++)
+                        if (j > it.pos0 + r || j >= it.kv_end) s[r][b][i] = -INFINITY;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NQ; r++) {
+            if (r >= (int)it.nq) continue;
+            float mb = s[r][0][0];
+#pragma unroll
+            for (int b = 0; b < PB; b++)
+#pragma unroll
+                for (int i = 0; i < LPP; i++) mb = fmaxf(mb, s[r][b][i]);
+            const float mn = fmaxf(m[r], mb);
+            const float alpha = fast_exp2(m[r] - mn);
+            m[r] = mn;
+            l[r] *= alpha;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[r][e] *= alpha;
+#pragma unroll
+            for (int b = 0; b < PB; b++) {
+#pragma unroll
+                for (int i = 0; i < LPP; i++) {
+                    const float p = fast_exp2(s[r][b][i] - mn);
+                    l[r] += p;
+                    const half8_t vh = __builtin_bit_cast(half8_t, vr[b][i]);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o[r][e] = fmaf(p, static_cast<float>(vh[e]), o[r][e]);
+                }
+            }
+        }
+    }
+
+    // Merge the KPL key-row groups of the wave (lanes ds, ds+LPK, ...).
+#pragma unroll
+    for (int r = 0; r < NQ; r++) {
+        if (r >= (int)it.nq) continue;
+#pragma unroll
+        for (int off = LPK; off < 64; off <<= 1) {
+            const float m2 = __shfl_xor(m[r], off);
+            const float l2 = __shfl_xor(l[r], off);
+            float o2[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) o2[e] = __shfl_xor(o[r][e], off);
+            merge_state(m[r], l[r], o[r], m2, l2, o2);
+        }
+    }
+    if (kl == 0) {
+#pragma unroll
+        for (int r = 0; r < NQ; r++) {
+            if (r >= (int)it.nq) continue;
+#pragma unroll
+            for (int e = 0; e < 8; e++) red[wave][r][2 + ds * 8 + e] = o[r][e];
+            if (ds == 0) {
+                red[wave][r][0] = m[r];
+                red[wave][r][1] = l[r];
+            }
+        }
+    }
+    __syncthreads();
+    // Merge the W waves and write: the output itself when the item is its
+    // group's only partition, else the partial (m, l, o) for the merge kernel.
+    for (uint32_t t = threadIdx.x; t < it.nq * D; t += 64 * W) {
+        const uint32_t r = t / D, d = t - r * D;
+        float M = red[0][r][0];
+#pragma unroll
+        for (int w = 1; w < W; w++) M = fmaxf(M, red[w][r][0]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            const float wt = fast_exp2(red[w][r][0] - M);
+            L += red[w][r][1] * wt;
+            O += red[w][r][2 + d] * wt;
+        }
+        if (it.part_slot == kNoSlot) {
+            a.out[(int64_t)lay * a.out_layer_stride + (int64_t)(it.row0 + r) * a.out_row_stride + head * D + d] = O / L;
+        } else {
+            float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * H + head) * NQ + r) * (D + 2);
+            if (d == 0) {
+                p[0] = M;
+                p[1] = L;
+            }
+            p[2 + d] = O;
+        }
+    }
+}
+
+// One workgroup of D threads per (merge item, layer, head); thread d owns
+// output dimension d of every query row of the group.
+template <int D, int NQ>
+__global__ __launch_bounds__(D) void attn_merge_kernel(const AttnLaunch a) {
+    const uint32_t H = a.pool.n_head;
+    const uint32_t lh = a.n_lay * H;
+    const uint32_t mi = blockIdx.x / lh;
+    const uint32_t rem = blockIdx.x - mi * lh;
+    const uint32_t lay = rem / H;
+    const uint32_t head = rem - lay * H;
+    const MergeItem g = a.merges[mi];
+    const uint32_t d = threadIdx.x;
+    const uint64_t slot_stride = (uint64_t)a.n_lay * H * NQ * (D + 2);
+    for (uint32_t r = 0; r < g.nq; r++) {
+        const float* p0 = a.partials + ((((uint64_t)g.slot0 * a.n_lay + lay) * H + head) * NQ + r) * (D + 2);
+        float M = p0[0];
+        for (uint32_t s = 1; s < g.n_parts; s++) M = fmaxf(M, p0[s * slot_stride]);
+        float L = 0.f, O = 0.f;
+        for (uint32_t s = 0; s < g.n_parts; s++) {
+            const float* p = p0 + s * slot_stride;
+            const float wt = fast_exp2(p[0] - M);
+            L += p[1] * wt;
+            O += p[2 + d] * wt;
+        }
+        a.out[(int64_t)lay * a.out_layer_stride + (int64_t)(g.row0 + r) * a.out_row_stride + head * D + d] = O / L;
+    }
+}
+
+// Waves per workgroup and pages per wave iteration of the split kernel.
+constexpr int kWaves = 4;
+constexpr int kPagesPerIter = 2;
+
+template <int D, int NQ>
+hipError_t attn_launch_t(const AttnLaunch& a, hipStream_t s) {
+    const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, kPagesPerIter>), dim3((uint32_t)blocks), dim3(64 * kWaves),
+                       0, s, a);
+    return hipGetLastError();
+}
+
+template <int D, int NQ>
+hipError_t merge_launch_t(const AttnLaunch& a, hipStream_t s) {
+    const uint64_t blocks = (uint64_t)a.n_merges * a.n_lay * a.pool.n_head;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL((attn_merge_kernel<D, NQ>), dim3((uint32_t)blocks), dim3(D), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D>
+hipError_t attn_dispatch_nq(const AttnLaunch& a, hipStream_t s, bool merge) {
+    switch (a.nq_tile) {
+        case 1: return merge ? merge_launch_t<D, 1>(a, s) : attn_launch_t<D, 1>(a, s);
+        case 2: return merge ? merge_launch_t<D, 2>(a, s) : attn_launch_t<D, 2>(a, s);
+        case 4: return merge ? merge_launch_t<D, 4>(a, s) : attn_launch_t<D, 4>(a, s);
+        case 8: return merge ? merge_launch_t<D, 8>(a, s) : attn_launch_t<D, 8>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t attn_dispatch(const AttnLaunch& a, hipStream_t s, bool merge) {
+    switch (a.pool.head_dim) {
+        case 64: return attn_dispatch_nq<64>(a, s, merge);
+        case 128: return attn_dispatch_nq<128>(a, s, merge);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool attention_supported(uint32_t head_dim) { return head_dim == 64 || head_dim == 128; }
+
+hipError_t launch_append(const AppendLaunch& a, hipStream_t s) {
+    const uint64_t threads = (uint64_t)a.n_lay * a.n_rows * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_append_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const GatherLaunch& a, hipStream_t s) {
+    const uint64_t threads = (uint64_t)a.n_lay * a.n_rows * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(kv_gather_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) { return attn_dispatch(a, s, false); }
+
+hipError_t launch_merge(const AttnLaunch& a, hipStream_t s) { return attn_dispatch(a, s, true); }
+
+hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, in, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace ni

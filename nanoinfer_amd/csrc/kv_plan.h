@@ -1,0 +1,112 @@
+// kv_plan.h -- the per-call plan the host builds and the kernels read.
+//
+// Shared by the host side (kv_host.cpp) and the gfx950 kernels
+// (kv_kernels.hip).  A data-path call turns its rows into a compact plan
+// (append destinations, attention work items, merge items and the block-table
+// segments those items read), uploads it with one async copy and launches the
+// kernels over it.  The device never sees the host's full block tables.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ni {
+
+constexpr uint32_t kPage = 16;           // positions per page (batch.rs:33)
+constexpr uint32_t kNoSlot = 0xffffffffu; // AttnItem::part_slot: the item is its group's only partition
+constexpr uint32_t kMaxGroupRows = 8;    // most query rows sharing one K/V stream
+
+// Where one appended row goes: pool page `page`, position `slot` (0..15) in it.
+struct AppendEntry {
+    uint32_t src_row;  // row index in the k/v input
+    uint32_t page;
+    uint32_t slot;
+    uint32_t pad;
+};
+
+// One attention work item: the queries of one group (consecutive rows of one
+// sequence at consecutive positions pos0 .. pos0+nq-1) over the keys of one
+// partition [kv_begin, kv_end).  One workgroup runs it per (layer, head).
+struct AttnItem {
+    uint32_t tab;       // offset of this sequence's page list in the plan table
+    uint32_t row0;      // q/out row of the first query
+    uint32_t pos0;      // position of the first query; query r sees keys <= pos0 + r
+    uint32_t nq;        // queries (1..kMaxGroupRows)
+    uint32_t kv_begin;  // first key (multiple of 16)
+    uint32_t kv_end;    // one past the last key: min(partition end, pos0 + nq)
+    uint32_t part_slot; // partial-result slot, or kNoSlot (write out directly)
+    uint32_t pad;
+};
+
+// A group split into n_parts partitions, merged by log-sum-exp.
+struct MergeItem {
+    uint32_t row0;
+    uint32_t nq;
+    uint32_t slot0;   // partial slots slot0 .. slot0+n_parts-1
+    uint32_t n_parts;
+};
+
+// Device pool geometry: K and V each [n_layer][kv_pages][n_head][16][head_dim].
+struct PoolGeom {
+    uint16_t* k;
+    uint16_t* v;
+    uint64_t layer_halves;  // kv_pages * n_head * 16 * head_dim
+    uint32_t n_head;
+    uint32_t head_dim;
+};
+
+struct AppendLaunch {
+    PoolGeom pool;
+    const float* k;
+    const float* v;
+    int64_t row_stride;
+    int64_t layer_stride;
+    const AppendEntry* entries;  // device
+    uint32_t n_rows;
+    uint32_t layer0;
+    uint32_t n_lay;
+};
+
+struct GatherLaunch {
+    PoolGeom pool;
+    uint16_t* k_out;
+    uint16_t* v_out;
+    int64_t row_stride;  // halves
+    int64_t layer_stride;
+    const AppendEntry* entries;  // src_row = output row
+    uint32_t n_rows;
+    uint32_t layer0;
+    uint32_t n_lay;
+};
+
+struct AttnLaunch {
+    PoolGeom pool;
+    const float* q;
+    int64_t q_row_stride;
+    int64_t q_layer_stride;
+    float* out;
+    int64_t out_row_stride;
+    int64_t out_layer_stride;
+    const AttnItem* items;    // device, sorted longest first
+    const uint32_t* table;    // device, plan table (physical page ids)
+    float* partials;          // [slot][n_lay][n_head][nq_tile][head_dim + 2]
+    const MergeItem* merges;  // device
+    uint32_t n_items;
+    uint32_t n_merges;
+    uint32_t layer0;
+    uint32_t n_lay;
+    uint32_t nq_tile;         // compile-time query tile the kernels use (1, 2, 4 or 8)
+    float qscale;             // log2(e) / sqrt(head_dim)
+};
+
+// Kernel launchers (kv_kernels.hip).  They validate nothing; the host checks
+// every index the plan holds before calling them.
+hipError_t launch_append(const AppendLaunch& a, hipStream_t s);
+hipError_t launch_gather(const GatherLaunch& a, hipStream_t s);
+hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);
+hipError_t launch_merge(const AttnLaunch& a, hipStream_t s);
+hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s);
+bool attention_supported(uint32_t head_dim);
+
+}  // namespace ni

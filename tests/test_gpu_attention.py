@@ -1,0 +1,176 @@
+"""Paged split-K decode attention on the device against the oracle
+(kv16.rs:144-164 over kv_slot, batch.metal:349-424), within the north
+star's 1e-3 max-abs / 1e-3 relative; closed forms and invariances exactly."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import nanoinfer_amd as na
+from nanoinfer_amd import workloads
+from paged_mirror import Mirror, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+def opts(shape, **kw):
+    base = dict(**shape, kv_blocks=256, max_seqs=8, n_ctx=2048, max_rows=512)
+    base.update(kw)
+    return na.BatchOpts(**base)
+
+
+@pytest.mark.parametrize("shape", [workloads.GPT2, dict(n_layer=2, n_head=4, head_dim=128)], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("split", [0, 64, 128, 512])
+def test_decode_contexts(gpu, oracle_lib, shape, split):
+    rng = np.random.default_rng(20)
+    m = Mirror(opts(shape, page_order=rng.permutation(256).tolist()))
+    lens = [1, 15, 16, 17, 65, 300, 1023, 1024]
+    seqs = [m.kv.add_seq() for _ in lens]
+    for s, L in zip(seqs, lens):
+        m.fill(s, L, rng)
+    rows = [(s, L - 1) for s, L in zip(seqs, lens)]
+    q = rng.standard_normal((shape["n_layer"], len(rows), m.c)).astype(np.float32)
+    got, want = m.attention(rows, q, split_tokens=split)
+    err = assert_close(got, want, f"split {split}")
+    say(f"{shape} split {split}: max abs err {err:.2e}")
+
+
+def test_causal_groups_spec_verify_shape(gpu, oracle_lib):
+    """Five consecutive rows of one sequence (g + 4 drafts) attend causally
+    and share their K/V reads; rows straddle page and partition edges."""
+    rng = np.random.default_rng(21)
+    m = Mirror(opts(workloads.GPT2))
+    for split in (0, 64, 128):
+        for L in (5, 14, 16, 62, 127, 130, 512):
+            m2 = m
+            s = m2.kv.add_seq()
+            m2.fill(s, L, rng)
+            rows = [(s, p) for p in range(L - 5, L)]
+            q = rng.standard_normal((12, 5, m.c)).astype(np.float32)
+            got, want = m2.attention(rows, q, split_tokens=split)
+            assert_close(got, want, f"L {L} split {split}")
+            m2.kv.free_seq(s)
+
+
+def test_mixed_rows_and_long_groups(gpu, oracle_lib):
+    """Decode rows, a 5-row group and a 20-row group (split into groups of
+    at most 8) in one call, rows interleaved."""
+    rng = np.random.default_rng(22)
+    m = Mirror(opts(workloads.GPT2))
+    a, b, c = m.kv.add_seq(), m.kv.add_seq(), m.kv.add_seq()
+    m.fill(a, 200, rng)
+    m.fill(b, 77, rng)
+    m.fill(c, 900, rng)
+    rows = [(a, 199)] + [(b, p) for p in range(72, 77)] + [(c, p) for p in range(880, 900)] + [(a, 150)]
+    q = rng.standard_normal((12, len(rows), m.c)).astype(np.float32)
+    for split in (0, 128):
+        got, want = m.attention(rows, q, split_tokens=split)
+        assert_close(got, want, f"split {split}")
+
+
+def test_single_key_copies_value(gpu, oracle_lib):
+    """reference.rs:188-199 on the device: one key -> out == v exactly."""
+    rng = np.random.default_rng(23)
+    m = Mirror(opts(workloads.GPT2))
+    s = m.kv.add_seq()
+    m.fill(s, 1, rng)
+    q = rng.standard_normal((12, 1, m.c)).astype(np.float32)
+    got, want = m.attention([(s, 0)], q)
+    (kg, vg), _ = m.gather([(s, 0)])
+    assert np.array_equal(got, vg.view(np.float16).astype(np.float32))
+    assert np.array_equal(got, want)
+
+
+def test_identical_keys_give_mean(gpu, oracle_lib):
+    rng = np.random.default_rng(24)
+    m = Mirror(opts(workloads.GPT2, n_layer=1))
+    s = m.kv.add_seq()
+    L = 333
+    m.kv.reserve(s, L)
+    k = np.tile(rng.standard_normal((1, 1, m.c)).astype(np.float32), (1, L, 1))
+    v = rng.standard_normal((1, L, m.c)).astype(np.float32)
+    m.append([(s, p) for p in range(L)], k, v)
+    m.kv.commit(s, L)
+    q = rng.standard_normal((1, 1, m.c)).astype(np.float32)
+    got, _ = m.attention([(s, L - 1)], q, split_tokens=64)
+    mean = oracle.f16_to_f32(oracle.f32_to_f16(v[0])).astype(np.float64).mean(0)
+    assert np.abs(got[0, 0] - mean).max() < 1e-5
+
+
+def test_split_size_invariance(gpu, oracle_lib):
+    """The log-sum-exp merge: every partition size gives the same output
+    (to f32 rounding)."""
+    rng = np.random.default_rng(25)
+    m = Mirror(opts(dict(n_layer=1, n_head=4, head_dim=128), n_ctx=4096, kv_blocks=300))
+    s = m.kv.add_seq()
+    m.fill(s, 4000, rng, chunk=512)
+    q = rng.standard_normal((1, 1, m.c)).astype(np.float32)
+    outs = []
+    for split in (64, 128, 512, 1024, 4096):
+        outs.append(m.kv.attention(torch.from_numpy(q).cuda(), [(s, 3999)], split_tokens=split).cpu().numpy())
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() < 1e-5
+
+
+def test_batch_invariance(gpu, oracle_lib):
+    """A sequence's output is bit-identical alone or batched with others
+    (fixed partition size), as the reference's batch tests require of its
+    kernels (crates/metal/tests/batch.rs:82-111)."""
+    rng = np.random.default_rng(26)
+    m = Mirror(opts(workloads.GPT2))
+    seqs = [m.kv.add_seq() for _ in range(5)]
+    lens = [100, 513, 64, 999, 7]
+    for s, L in zip(seqs, lens):
+        m.fill(s, L, rng)
+    rows = [(s, L - 1) for s, L in zip(seqs, lens)]
+    q = rng.standard_normal((12, len(rows), m.c)).astype(np.float32)
+    qd = torch.from_numpy(q).cuda()
+    together = m.kv.attention(qd, rows, split_tokens=128).cpu().numpy()
+    for i, r in enumerate(rows):
+        alone = m.kv.attention(qd[:, i:i + 1].contiguous(), [r], split_tokens=128).cpu().numpy()
+        assert np.array_equal(alone[:, 0], together[:, i])
+
+
+def test_config2_full_size(gpu, oracle_lib):
+    """Config 2: 16 sequences, contexts U[64,1024], pages from a seeded
+    permutation of a 1024-page pool; append 1 token each, then attention."""
+    ctx, order = workloads.config2_contexts()
+    m = Mirror(na.BatchOpts(**workloads.GPT2, kv_blocks=1024, max_seqs=16, n_ctx=1024, page_order=order))
+    rng = np.random.default_rng(27)
+    seqs = [m.kv.add_seq() for _ in ctx]
+    for s, L in zip(seqs, ctx):
+        m.fill(s, L - 1, rng, chunk=512)
+    from paged_mirror import mirror_step
+
+    work = [(s, 1, 1) for s in seqs]
+    n = len(work)
+    q, k, v = (rng.standard_normal((12, n, m.c)).astype(np.float32) for _ in range(3))
+    got, want, qrows = mirror_step(m, work, q, k, v)
+    err = assert_close(got[:, qrows], want[:, qrows], "config 2")
+    say(f"config 2: max abs err {err:.2e}")
+    assert [m.kv.seq_len(s) for s in seqs] == ctx
+
+
+def test_config4_full_size(gpu, oracle_lib):
+    """Config 4: batch 4, 32 heads x 128, context 32768, random page tables,
+    512-token partitions + LSE merge; k/v ~ N(0, 0.5), q ~ N(0, 1)."""
+    B, L = 4, 32768
+    order = workloads.XorShift.seeded(4).permutation(B * L // 16)
+    m = Mirror(na.BatchOpts(**workloads.LONG, kv_blocks=B * L // 16, max_seqs=B, n_ctx=L, max_rows=4096,
+                            page_order=order))
+    rng = np.random.default_rng(28)
+    seqs = [m.kv.add_seq() for _ in range(B)]
+    for s in seqs:
+        m.fill(s, L, rng, std=0.5, chunk=4096)
+        say(f"config 4: filled seq {s}")
+    rows = [(s, L - 1) for s in seqs]
+    q = rng.standard_normal((1, B, m.c)).astype(np.float32)
+    got, want = m.attention(rows, q, split_tokens=512)
+    err = assert_close(got, want, "config 4")
+    say(f"config 4: max abs err {err:.2e}")
