@@ -101,7 +101,8 @@ struct ni_kv {
     std::vector<QRow> qrows;
     std::vector<int64_t> seq_tab;     // seq -> offset in plan.table, -1 if absent
     std::vector<uint32_t> seq_need;   // seq -> pages needed this call
-    std::vector<uint8_t> staging_tmp;
+    std::vector<uint32_t> step_mark;  // seq -> stamp of the last step that listed it
+    uint32_t step_stamp = 0;
 
     int fail(int code, const char* fmt, ...) __attribute__((format(printf, 3, 4))) {
         char buf[512];
@@ -506,6 +507,7 @@ int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
     kv->pages.assign(o.max_seqs, {});
     kv->seq_tab.assign(o.max_seqs, -1);
     kv->seq_need.assign(o.max_seqs, 0);
+    kv->step_mark.assign(o.max_seqs, 0);
     // batch.rs:174: (0..kv_blocks).rev() so that pop() yields 0, 1, 2, ...
     kv->free_pages.resize(o.kv_pages);
     if (o.page_order) {
@@ -754,6 +756,10 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
         if (int rc = check_f32_operand(kv, "out", out, out_row_stride, out_layer_stride, true)) return rc;
     }
     reset_plan(kv);
+    if (++kv->step_stamp == 0) {  // stamps wrapped: forget every old mark
+        std::fill(kv->step_mark.begin(), kv->step_mark.end(), 0u);
+        kv->step_stamp = 1;
+    }
     // Batch::encode_step (batch.rs:280-305): check each item, grow its pages,
     // lay out its rows.
     uint64_t n_rows = 0;
@@ -764,16 +770,13 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
         if (it.n_new == 0) return kv->fail(NI_ERR_EMPTY_WORK, "empty work item");
         if (it.n_query > it.n_new)
             return kv->fail(NI_ERR_BAD_ARG, "work item %u: n_query %u > n_new %u", w, it.n_query, it.n_new);
-        if (kv->seq_tab[it.seq] == -2) {
-            for (uint32_t v2 = 0; v2 < w; v2++) kv->seq_tab[work[v2].seq] = -1;
+        if (kv->step_mark[it.seq] == kv->step_stamp)
             return kv->fail(NI_ERR_BAD_ARG, "sequence %u appears twice in one step", it.seq);
-        }
-        kv->seq_tab[it.seq] = -2;  // seen in this step
+        kv->step_mark[it.seq] = kv->step_stamp;
         const uint32_t len = kv->seq_len[it.seq];
         if (int rc = ensure_pages(kv, it.seq, (uint64_t)len + it.n_new)) return rc;
         n_rows += it.n_new;
     }
-    for (uint32_t w = 0; w < n_work; w++) kv->seq_tab[work[w].seq] = -1;
     if (n_rows > kv->o.max_rows)
         return kv->fail(NI_ERR_TOO_MANY_ROWS, "%llu rows > max_rows %u", (unsigned long long)n_rows, kv->o.max_rows);
     uint32_t row = 0;

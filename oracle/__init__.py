@@ -245,7 +245,7 @@ def paged_append(pools: PagedPools, layer, table, max_blocks, seqs, poss, k, v):
     k, v = _f32(k), _f32(v)
     n = len(seqs)
     lib().or_paged_append(pools.k[layer], pools.v[layer], np.ascontiguousarray(table, np.uint32).reshape(-1),
-                          max_blocks, np.asarray(seqs, np.uint32), np.asarray(poss, np.uint32), n,
+                          max_blocks, np.ascontiguousarray(seqs, np.uint32), np.ascontiguousarray(poss, np.uint32), n,
                           k.reshape(-1), v.reshape(-1), k.shape[-1] if k.ndim > 1 else pools.c, pools.c)
 
 
@@ -255,7 +255,7 @@ def paged_gather(pools: PagedPools, layer, table, max_blocks, seqs, poss):
     ko = np.zeros((n, pools.c), np.uint16)
     vo = np.zeros((n, pools.c), np.uint16)
     lib().or_paged_gather(ko, vo, pools.k[layer], pools.v[layer], np.ascontiguousarray(table, np.uint32).reshape(-1),
-                          max_blocks, np.asarray(seqs, np.uint32), np.asarray(poss, np.uint32), n, pools.c)
+                          max_blocks, np.ascontiguousarray(seqs, np.uint32), np.ascontiguousarray(poss, np.uint32), n, pools.c)
     return ko, vo
 
 
@@ -270,7 +270,7 @@ def paged_attention(pools: PagedPools, layer, table, max_blocks, seqs, poss, q, 
     scores = np.zeros(max_kv, np.float32)
     lib().or_paged_attention(out, c, q.reshape(-1), q.shape[-1] if q.ndim > 1 else c, pools.k[layer],
                              pools.v[layer], np.ascontiguousarray(table, np.uint32).reshape(-1), max_blocks,
-                             np.asarray(seqs, np.uint32), np.asarray(poss, np.uint32), n, n_head, hd, scores)
+                             np.ascontiguousarray(seqs, np.uint32), np.ascontiguousarray(poss, np.uint32), n, n_head, hd, scores)
     return out
 
 
@@ -360,6 +360,6 @@ class CpuStep:
         assert k.shape[1] * c == ls and v.shape[1] * c == ls
         lib().or_cpu_step(self._p, pools.k.reshape(-1), pools.v.reshape(-1), pools.kv_blocks,
                           np.ascontiguousarray(table, np.uint32).reshape(-1), max_blocks,
-                          np.asarray(seqs, np.uint32), np.asarray(poss, np.uint32), n,
-                          np.asarray(qrows, np.uint32), len(qrows), q.reshape(-1), k.reshape(-1), v.reshape(-1),
+                          np.ascontiguousarray(seqs, np.uint32), np.ascontiguousarray(poss, np.uint32), n,
+                          np.ascontiguousarray(qrows, np.uint32), len(qrows), q.reshape(-1), k.reshape(-1), v.reshape(-1),
                           c, ls, out.reshape(-1), c, out.shape[1] * c, n_layer, n_head, hd)

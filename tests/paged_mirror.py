@@ -93,10 +93,15 @@ class Mirror:
     def gather(self, rows, layer=na.ALL_LAYERS):
         """Device gather (f16 bits as uint16) and the oracle's."""
         rows = np.asarray(rows, np.uint32).reshape(-1, 2)
-        kd, vd = self.kv.gather(rows, layer=layer)
-        torch.cuda.synchronize()
-        kg = kd.cpu().numpy().view(np.uint16)
-        vg = vd.cpu().numpy().view(np.uint16)
+        ks, vs = [], []
+        step = self.opts.max_rows
+        for i in range(0, len(rows), step):  # one call holds at most max_rows rows
+            kd, vd = self.kv.gather(rows[i:i + step], layer=layer)
+            ks.append(kd.cpu().numpy().view(np.uint16))
+            vs.append(vd.cpu().numpy().view(np.uint16))
+        axis = 1 if layer == na.ALL_LAYERS else 0
+        kg = np.concatenate(ks, axis)
+        vg = np.concatenate(vs, axis)
         t = self.table()
         layers = range(self.opts.n_layer) if layer == na.ALL_LAYERS else [layer]
         kw = np.zeros_like(kg)
