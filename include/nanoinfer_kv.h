@@ -157,15 +157,21 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
 /* Wait for all work this handle enqueued on `stream`. */
 int ni_kv_sync(ni_kv* kv, ni_stream stream);
 
-/* Device pools, for inspection: K and V, each [n_layer][kv_pages][n_head][16][head_dim] f16. */
-int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes_each);
+/* The device pool, for inspection: one allocation of `bytes`, laid out
+ * [n_layer][kv_pages][n_head][K|V][16][head_dim] f16; *k_pool is its start
+ * and *v_pool = *k_pool + 16*head_dim halves (V follows K in every
+ * (page, head) block). */
+int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes);
 
 /* quant.rs:25-54 on the device, elementwise (the conversion the append uses). */
 int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream);
 
 /* ---- measurement: HIP events around this handle's kernel launches ---- */
 enum ni_kernel_id { NI_K_APPEND = 0, NI_K_ATTN = 1, NI_K_MERGE = 2, NI_K_COUNT = 3 };
-int ni_kv_profile(ni_kv* kv, int enable);
+/* Bit k of kernel_mask brackets every launch of kernel k (ni_kernel_id) with
+ * a pair of HIP events on the launch's stream; 0 stops.  NI_K_ATTN is the
+ * attention launch (with the append fused into it when ni_kv_step fuses). */
+int ni_kv_profile(ni_kv* kv, uint32_t kernel_mask);
 /* Total milliseconds and launches of one kernel since the last read (waits). */
 int ni_kv_profile_read(ni_kv* kv, int kernel, double* total_ms, uint64_t* launches);
 

@@ -109,7 +109,7 @@ def _declare(L):
     L.ni_f32_to_f16.restype = C.c_int
     L.ni_f32_to_f16.argtypes = [_vp, _vp, C.c_size_t, _vp]
     L.ni_kv_profile.restype = C.c_int
-    L.ni_kv_profile.argtypes = [_vp, C.c_int]
+    L.ni_kv_profile.argtypes = [_vp, _u32]
     L.ni_kv_profile_read.restype = C.c_int
     L.ni_kv_profile_read.argtypes = [_vp, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]
 

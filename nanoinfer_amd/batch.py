@@ -265,8 +265,13 @@ class PagedKv:
         return kp.value, vp.value, nb.value
 
     # ------------------------------------------------------------ measurement
-    def profile(self, enable: bool = True):
-        self._check(self._L.ni_kv_profile(self._h, 1 if enable else 0))
+    def profile(self, kernels=(0, 1, 2)):
+        """Bracket launches of the listed kernels (0 append, 1 attention,
+        2 merge) with HIP events; an empty list stops."""
+        mask = 0
+        for k in kernels:
+            mask |= 1 << int(k)
+        self._check(self._L.ni_kv_profile(self._h, mask))
 
     def profile_read(self, kernel: int):
         """(total ms, launches) of one kernel since the last read."""

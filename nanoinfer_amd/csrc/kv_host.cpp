@@ -31,8 +31,16 @@ using namespace ni;
 namespace {
 
 constexpr uint32_t kRingSlots = 4;
+
+// Plans are uploaded on the handle's own copy stream and the caller's stream
+// waits for the upload with an event, so the copy overlaps the previous
+// step's kernels instead of sitting between them.
+#ifndef NI_PLAN_COPY_STREAM
+#define NI_PLAN_COPY_STREAM 1
+#endif
 constexpr size_t kAlign = 256;
 constexpr uint32_t kMinSplit = 64;  // smallest partition the planner uses (tokens)
+constexpr size_t kProfileEvents = 8192;  // events created when profiling starts
 
 thread_local std::string g_create_error;
 
@@ -42,31 +50,41 @@ struct StagingSlot {
     uint8_t* host = nullptr;  // pinned
     uint8_t* dev = nullptr;
     size_t cap = 0;
-    hipEvent_t done = nullptr;
+    hipEvent_t done = nullptr;      // the kernels that read this slot finished
+    hipEvent_t uploaded = nullptr;  // the slot's upload finished (copy stream)
     bool pending = false;
 };
 
 // Work of one data-path call, before serialisation.
 struct Plan {
     std::vector<AppendEntry> app;
+    std::vector<AppendEntry> orphans;  // fused: rows of sequences without queries
     std::vector<AttnItem> items;
     std::vector<MergeItem> merges;
     std::vector<uint32_t> table;
     uint32_t n_slots = 0;
     uint32_t nq_tile = 1;
+    uint32_t napp_total = 0;  // fused: rows the attention items append
+    bool fused = false;
     void clear() {
         app.clear();
+        orphans.clear();
         items.clear();
         merges.clear();
         table.clear();
         n_slots = 0;
         nq_tile = 1;
+        napp_total = 0;
+        fused = false;
     }
 };
 
-// A query row as the planner sees it.
+// A query row as the planner sees it.  [new_begin, new_end) are the positions
+// its sequence appends in this call, starting at append entry app_first
+// (new_begin == new_end when the call appends nothing).
 struct QRow {
     uint32_t row, seq, pos;
+    uint32_t new_begin, new_end, app_first;
 };
 
 }  // namespace
@@ -84,20 +102,24 @@ struct ni_kv {
 
     uint16_t* kpool = nullptr;
     uint16_t* vpool = nullptr;
-    size_t pool_bytes = 0;  // each of K and V
+    size_t pool_bytes = 0;  // K and V together
     uint64_t layer_halves = 0;
+    uint64_t page_halves = 0;
+    uint32_t head_halves = 0;
 
     StagingSlot ring[kRingSlots];
     uint32_t ring_next = 0;
+    hipStream_t copy_stream = nullptr;
     float* partials = nullptr;
     size_t partials_bytes = 0;
 
-    bool profile = false;
+    uint32_t profile = 0;  // bit k: bracket kernel k's launches with events
     std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[NI_K_COUNT];
     std::vector<hipEvent_t> ev_pool;
 
     // scratch reused across calls
     Plan plan;
+    std::vector<uint8_t> blob;  // the serialised plan
     std::vector<QRow> qrows;
     std::vector<int64_t> seq_tab;     // seq -> offset in plan.table, -1 if absent
     std::vector<uint32_t> seq_need;   // seq -> pages needed this call
@@ -121,6 +143,8 @@ struct ni_kv {
         g.k = kpool;
         g.v = vpool;
         g.layer_halves = layer_halves;
+        g.page_halves = page_halves;
+        g.head_halves = head_halves;
         g.n_head = o.n_head;
         g.head_dim = o.head_dim;
         return g;
@@ -212,6 +236,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     if (qr.empty()) return NI_OK;
     struct Group {
         uint32_t seq, row0, pos0, nq;
+        uint32_t new_begin, new_end, app_first;
     };
     std::vector<Group> groups;
     groups.reserve(qr.size());
@@ -223,7 +248,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
                 continue;
             }
         }
-        groups.push_back({r.seq, r.row, r.pos, 1});
+        groups.push_back({r.seq, r.row, r.pos, 1, r.new_begin, r.new_end, r.app_first});
     }
     // Partition size: the caller's, or (0) the largest of 1024/512/256/128
     // tokens that still yields >= 4096 workgroups, so that every CU has
@@ -258,18 +283,37 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         P.table.insert(P.table.end(), pg.begin(), pg.begin() + kv->seq_need[g.seq]);
     }
     uint32_t max_nq = 1;
+    // An item [b, e) of a fused step appends this call's new rows in [b, e).
+    auto item = [&](const Group& g, uint32_t tab, uint32_t b, uint32_t e, uint32_t slot) {
+        AttnItem it{};
+        it.tab = tab;
+        it.row0 = g.row0;
+        it.pos0 = g.pos0;
+        it.nq = g.nq;
+        it.kv_begin = b;
+        it.kv_end = e;
+        it.part_slot = slot;
+        if (P.fused) {
+            const uint32_t lo = std::max(b, g.new_begin), hi = std::min(e, g.new_end);
+            if (hi > lo) {
+                it.app0 = g.app_first + (lo - g.new_begin);
+                it.napp = hi - lo;
+                P.napp_total += it.napp;
+            }
+        }
+        P.items.push_back(it);
+    };
     for (const Group& g : groups) {
         max_nq = std::max(max_nq, g.nq);
         const uint32_t L = g.pos0 + g.nq;
         const uint32_t n_parts = (L + part - 1) / part;
         const uint32_t tab = (uint32_t)kv->seq_tab[g.seq];
         if (n_parts <= 1) {
-            P.items.push_back({tab, g.row0, g.pos0, g.nq, 0, L, kNoSlot, 0});
+            item(g, tab, 0, L, kNoSlot);
             continue;
         }
         const uint32_t slot0 = P.n_slots;
-        for (uint32_t p = 0; p < n_parts; p++)
-            P.items.push_back({tab, g.row0, g.pos0, g.nq, p * part, std::min((p + 1) * part, L), slot0 + p, 0});
+        for (uint32_t p = 0; p < n_parts; p++) item(g, tab, p * part, std::min((p + 1) * part, L), slot0 + p);
         P.merges.push_back({g.row0, g.nq, slot0, n_parts});
         P.n_slots += n_parts;
     }
@@ -303,7 +347,7 @@ struct ProfileScope {
     hipStream_t s;
     hipEvent_t a = nullptr, b = nullptr;
     ProfileScope(ni_kv* kv_, int k, hipStream_t s_) : kv(kv_), kernel(k), s(s_) {
-        if (!kv->profile) return;
+        if (!(kv->profile & (1u << k))) return;
         a = take_event(kv);
         b = take_event(kv);
         if (a) (void)hipEventRecord(a, s);
@@ -358,40 +402,73 @@ int ensure_partials(ni_kv* kv, size_t bytes) {
 }
 
 struct Offsets {
-    size_t app, items, merges, table, total;
+    size_t app, orphans, items, merges, table, total;
 };
 
 Offsets layout(const Plan& P) {
     Offsets o;
     o.app = 0;
-    o.items = align_up(o.app + P.app.size() * sizeof(AppendEntry), kAlign);
+    o.orphans = align_up(o.app + P.app.size() * sizeof(AppendEntry), kAlign);
+    o.items = align_up(o.orphans + P.orphans.size() * sizeof(AppendEntry), kAlign);
     o.merges = align_up(o.items + P.items.size() * sizeof(AttnItem), kAlign);
     o.table = align_up(o.merges + P.merges.size() * sizeof(MergeItem), kAlign);
     o.total = align_up(o.table + P.table.size() * sizeof(uint32_t), kAlign);
     return o;
 }
 
-// Copy the plan into a staging slot and enqueue its upload.
-int upload_plan(ni_kv* kv, hipStream_t s, StagingSlot** slot_out, Offsets* off) {
+// Where the kernels find this call's plan: in the launch arguments (small
+// plans) or in a staging slot uploaded on the copy stream.
+struct PlanRef {
+    const void* inl = nullptr;
+    uint32_t inl_bytes = 0;
+    const uint8_t* dev = nullptr;
+    StagingSlot* slot = nullptr;
+};
+
+// Serialise the plan and make it reachable from `s`.
+int place_plan(ni_kv* kv, hipStream_t s, Offsets* off, PlanRef* ref) {
     const Plan& P = kv->plan;
     *off = layout(P);
+    auto& blob = kv->blob;
+    blob.resize(off->total);
+    if (!P.app.empty()) memcpy(blob.data() + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
+    if (!P.orphans.empty())
+        memcpy(blob.data() + off->orphans, P.orphans.data(), P.orphans.size() * sizeof(AppendEntry));
+    if (!P.items.empty()) memcpy(blob.data() + off->items, P.items.data(), P.items.size() * sizeof(AttnItem));
+    if (!P.merges.empty()) memcpy(blob.data() + off->merges, P.merges.data(), P.merges.size() * sizeof(MergeItem));
+    if (!P.table.empty()) memcpy(blob.data() + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
+    *ref = PlanRef{};
+    if (off->total <= kInlinePlanBytes) {
+        ref->inl = blob.data();
+        ref->inl_bytes = (uint32_t)off->total;
+        return NI_OK;
+    }
     StagingSlot* sl = nullptr;
     int rc = acquire_slot(kv, off->total, &sl);
     if (rc) return rc;
-    if (!P.app.empty()) memcpy(sl->host + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
-    if (!P.items.empty()) memcpy(sl->host + off->items, P.items.data(), P.items.size() * sizeof(AttnItem));
-    if (!P.merges.empty()) memcpy(sl->host + off->merges, P.merges.data(), P.merges.size() * sizeof(MergeItem));
-    if (!P.table.empty()) memcpy(sl->host + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
+    memcpy(sl->host, blob.data(), off->total);
+#if NI_PLAN_COPY_STREAM
+    hipError_t e = hipMemcpyAsync(sl->dev, sl->host, off->total, hipMemcpyHostToDevice, kv->copy_stream);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipMemcpyAsync(plan)");
+    e = hipEventRecord(sl->uploaded, kv->copy_stream);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipEventRecord(upload)");
+    e = hipStreamWaitEvent(s, sl->uploaded, 0);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
+#else
     hipError_t e = hipMemcpyAsync(sl->dev, sl->host, off->total, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return kv->hip_fail(e, "hipMemcpyAsync(plan)");
-    *slot_out = sl;
+#endif
+    ref->dev = sl->dev;
+    ref->slot = sl;
     return NI_OK;
 }
 
-int finish_slot(ni_kv* kv, StagingSlot* sl, hipStream_t s) {
-    hipError_t e = hipEventRecord(sl->done, s);
+// After the launches that read a staged plan: mark its slot busy until they end.
+int release_plan(ni_kv* kv, const PlanRef& ref, hipStream_t s) {
+    if (!ref.slot) return NI_OK;
+    hipError_t e = hipEventRecord(ref.slot->done, s);
     if (e != hipSuccess) return kv->hip_fail(e, "hipEventRecord(staging)");
-    sl->pending = true;
+    ref.slot->pending = true;
     return NI_OK;
 }
 
@@ -406,56 +483,67 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
         int rc = ensure_partials(kv, need);
         if (rc) return rc;
     }
-    StagingSlot* sl = nullptr;
     Offsets off;
-    int rc = upload_plan(kv, s, &sl, &off);
+    PlanRef ref;
+    int rc = place_plan(kv, s, &off, &ref);
     if (rc) return rc;
-    if (!P.app.empty()) {
+    if (!P.app.empty() && !P.fused) {
         AppendLaunch a;
         a.pool = kv->geom();
         a.k = k;
         a.v = v;
         a.row_stride = kv_row_stride;
         a.layer_stride = kv_layer_stride;
-        a.entries = reinterpret_cast<const AppendEntry*>(sl->dev + off.app);
+        a.plan = ref.dev;
+        a.off_entries = (uint32_t)off.app;
         a.n_rows = (uint32_t)P.app.size();
         a.layer0 = layer0;
         a.n_lay = n_lay;
         ProfileScope ps(kv, NI_K_APPEND, s);
-        hipError_t e = launch_append(a, s);
+        hipError_t e = launch_append(a, ref.inl, ref.inl_bytes, s);
         if (e != hipSuccess) return kv->hip_fail(e, "append kernel");
     }
-    if (!P.items.empty()) {
+    if (!P.items.empty() || !P.orphans.empty()) {
         AttnLaunch a;
         a.pool = kv->geom();
+        a.k = k;
+        a.v = v;
+        a.kv_row_stride = kv_row_stride;
+        a.kv_layer_stride = kv_layer_stride;
+        a.off_app = (uint32_t)off.app;
+        a.off_orphans = (uint32_t)off.orphans;
+        a.n_orphans = (uint32_t)P.orphans.size();
+        a.napp_total = P.napp_total;
         a.q = q;
         a.q_row_stride = q_row_stride;
         a.q_layer_stride = q_layer_stride;
         a.out = out;
         a.out_row_stride = out_row_stride;
         a.out_layer_stride = out_layer_stride;
-        a.items = reinterpret_cast<const AttnItem*>(sl->dev + off.items);
-        a.table = reinterpret_cast<const uint32_t*>(sl->dev + off.table);
+        a.plan = ref.dev;
+        a.off_items = (uint32_t)off.items;
+        a.off_table = (uint32_t)off.table;
+        a.off_merges = (uint32_t)off.merges;
         a.partials = kv->partials;
-        a.merges = reinterpret_cast<const MergeItem*>(sl->dev + off.merges);
         a.n_items = (uint32_t)P.items.size();
         a.n_merges = (uint32_t)P.merges.size();
         a.layer0 = layer0;
         a.n_lay = n_lay;
         a.nq_tile = P.nq_tile;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
+        a.n_orphan_blocks = P.fused ? orphan_blocks(a) : 0;
         {
             ProfileScope ps(kv, NI_K_ATTN, s);
-            hipError_t e = launch_attention(a, s);
+            hipError_t e = launch_attention(a, ref.inl, ref.inl_bytes, s);
             if (e != hipSuccess) return kv->hip_fail(e, "attention kernel");
         }
         if (!P.merges.empty()) {
             ProfileScope ps(kv, NI_K_MERGE, s);
-            hipError_t e = launch_merge(a, s);
+            hipError_t e = launch_merge(a, ref.inl, ref.inl_bytes, s);
             if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
         }
     }
-    return finish_slot(kv, sl, s);
+    return release_plan(kv, ref, s);
 }
 
 void reset_plan(ni_kv* kv) {
@@ -528,16 +616,34 @@ int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
     if (!host_only) {
         hipError_t e = hipGetDevice(&kv->device);
         if (e == hipSuccess) {
-            kv->layer_halves = (uint64_t)o.kv_pages * kPage * C;
+            // One allocation, [n_layer][kv_pages][n_head][K|V][16][head_dim]:
+            // a (page, head) holds its K block and then its V block, one
+            // contiguous run of 2 * 16 * head_dim halves.
+            const uint64_t block = (uint64_t)kPage * o.head_dim;
+#ifdef NI_KV_SEPARATE_POOLS
+            kv->head_halves = (uint32_t)block;
+            kv->page_halves = block * o.n_head;
+            kv->layer_halves = kv->page_halves * o.kv_pages;
+            kv->pool_bytes = (size_t)(2 * kv->layer_halves * o.n_layer * sizeof(uint16_t));
+            e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
+            if (e == hipSuccess) kv->vpool = kv->kpool + kv->layer_halves * o.n_layer;
+#else
+            kv->head_halves = (uint32_t)(2 * block);
+            kv->page_halves = 2 * block * o.n_head;
+            kv->layer_halves = kv->page_halves * o.kv_pages;
             kv->pool_bytes = (size_t)(kv->layer_halves * o.n_layer * sizeof(uint16_t));
             e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
+            if (e == hipSuccess) kv->vpool = kv->kpool + block;
+#endif
         }
-        if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&kv->vpool), kv->pool_bytes);
         // Zero pages: a page that was never written reads as finite zeros.
         if (e == hipSuccess) e = hipMemset(kv->kpool, 0, kv->pool_bytes);
-        if (e == hipSuccess) e = hipMemset(kv->vpool, 0, kv->pool_bytes);
-        for (uint32_t i = 0; e == hipSuccess && i < kRingSlots; i++)
+        for (uint32_t i = 0; e == hipSuccess && i < kRingSlots; i++) {
             e = hipEventCreateWithFlags(&kv->ring[i].done, hipEventDisableTiming);
+            if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->ring[i].uploaded, hipEventDisableTiming);
+        }
+        // Default priority: the copy stream only moves plans.
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->copy_stream, hipStreamNonBlocking);
         if (e != hipSuccess) {
             g_create_error = std::string("device setup failed: ") + hipGetErrorString(e);
             ni_kv_destroy(kv);
@@ -558,6 +664,7 @@ void ni_kv_destroy(ni_kv* kv) {
             if (sl.host) (void)hipHostFree(sl.host);
             if (sl.dev) (void)hipFree(sl.dev);
             if (sl.done) (void)hipEventDestroy(sl.done);
+            if (sl.uploaded) (void)hipEventDestroy(sl.uploaded);
         }
         for (auto& v : kv->prof_ev)
             for (auto& pr : v) {
@@ -567,7 +674,7 @@ void ni_kv_destroy(ni_kv* kv) {
         for (hipEvent_t e : kv->ev_pool) (void)hipEventDestroy(e);
         if (kv->partials) (void)hipFree(kv->partials);
         if (kv->kpool) (void)hipFree(kv->kpool);
-        if (kv->vpool) (void)hipFree(kv->vpool);
+        if (kv->copy_stream) (void)hipStreamDestroy(kv->copy_stream);
     }
     delete kv;
 }
@@ -648,11 +755,11 @@ uint32_t ni_kv_blocks_used(const ni_kv* kv) { return kv ? kv->o.kv_pages - (uint
 
 uint32_t ni_kv_free_block_count(const ni_kv* kv) { return kv ? (uint32_t)kv->free_pages.size() : 0; }
 
-int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes_each) {
+int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes) {
     if (!kv) return NI_ERR_BAD_ARG;
     if (k_pool) *k_pool = kv->kpool;
     if (v_pool) *v_pool = kv->vpool;
-    if (bytes_each) *bytes_each = kv->pool_bytes;
+    if (bytes) *bytes = kv->pool_bytes;
     return NI_OK;
 }
 
@@ -697,23 +804,24 @@ int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint1
         const ni_row& r = rows[i];
         kv->plan.app.push_back({i, kv->pages[r.seq][r.pos / kPage], r.pos % kPage, 0});
     }
-    StagingSlot* sl = nullptr;
     Offsets off;
+    PlanRef ref;
     hipStream_t s = (hipStream_t)stream;
-    if (int rc = upload_plan(kv, s, &sl, &off)) return rc;
+    if (int rc = place_plan(kv, s, &off, &ref)) return rc;
     GatherLaunch g;
     g.pool = kv->geom();
     g.k_out = k_out;
     g.v_out = v_out;
     g.row_stride = row_stride;
     g.layer_stride = all ? layer_stride : 0;
-    g.entries = reinterpret_cast<const AppendEntry*>(sl->dev + off.app);
+    g.plan = ref.dev;
+    g.off_entries = (uint32_t)off.app;
     g.n_rows = n;
     g.layer0 = layer0;
     g.n_lay = n_lay;
-    hipError_t e = launch_gather(g, s);
+    hipError_t e = launch_gather(g, ref.inl, ref.inl_bytes, s);
     if (e != hipSuccess) return kv->hip_fail(e, "gather kernel");
-    return finish_slot(kv, sl, s);
+    return release_plan(kv, ref, s);
 }
 
 int ni_paged_decode_attention(ni_kv* kv, int32_t layer, const float* q, int64_t q_row_stride,
@@ -733,7 +841,7 @@ int ni_paged_decode_attention(ni_kv* kv, int32_t layer, const float* q, int64_t 
     reset_plan(kv);
     for (uint32_t i = 0; i < n; i++) {
         if (int rc = check_row(kv, rows[i])) return rc;
-        kv->qrows.push_back({i, rows[i].seq, rows[i].pos});
+        kv->qrows.push_back({i, rows[i].seq, rows[i].pos, 0, 0, 0});
     }
     if (int rc = plan_attention(kv, split_tokens, n_lay)) return rc;
     return run_plan(kv, layer0, n_lay, nullptr, nullptr, 0, 0, q, q_row_stride, all ? q_layer_stride : 0, out,
@@ -779,15 +887,24 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
     }
     if (n_rows > kv->o.max_rows)
         return kv->fail(NI_ERR_TOO_MANY_ROWS, "%llu rows > max_rows %u", (unsigned long long)n_rows, kv->o.max_rows);
+    // Fuse the append into the attention launch when every sequence has a
+    // single query group: then exactly one workgroup per (layer, head, page)
+    // touches this step's new rows.
+    bool fused = true;
+    for (uint32_t w = 0; w < n_work; w++) fused &= work[w].n_query <= kMaxGroupRows;
+    kv->plan.fused = fused;
     uint32_t row = 0;
     for (uint32_t w = 0; w < n_work; w++) {
         const ni_work& it = work[w];
         const uint32_t len = kv->seq_len[it.seq];
         const auto& pg = kv->pages[it.seq];
+        const uint32_t first = (uint32_t)kv->plan.app.size();
         for (uint32_t i = 0; i < it.n_new; i++, row++) {
             const uint32_t pos = len + i;
-            kv->plan.app.push_back({row, pg[pos / kPage], pos % kPage, 0});
-            if (i >= it.n_new - it.n_query) kv->qrows.push_back({row, it.seq, pos});
+            const AppendEntry e{row, pg[pos / kPage], pos % kPage, 0};
+            kv->plan.app.push_back(e);
+            if (fused && it.n_query == 0) kv->plan.orphans.push_back(e);
+            if (i >= it.n_new - it.n_query) kv->qrows.push_back({row, it.seq, pos, len, len + it.n_new, first});
         }
     }
     if (int rc = plan_attention(kv, split_tokens, kv->o.n_layer)) return rc;
@@ -814,10 +931,19 @@ int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream) {
     return e == hipSuccess ? NI_OK : NI_ERR_HIP;
 }
 
-int ni_kv_profile(ni_kv* kv, int enable) {
+int ni_kv_profile(ni_kv* kv, uint32_t kernel_mask) {
     if (!kv) return NI_ERR_BAD_ARG;
     if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device");
-    kv->profile = enable != 0;
+    if (kernel_mask >> NI_K_COUNT) return kv->fail(NI_ERR_BAD_ARG, "kernel mask %#x has unknown bits", kernel_mask);
+    // Create the events up front: hipEventCreate inside a timed loop costs
+    // far more than recording.
+    while (kernel_mask && kv->ev_pool.size() < kProfileEvents) {
+        hipEvent_t e = nullptr;
+        hipError_t rc = hipEventCreate(&e);
+        if (rc != hipSuccess) return kv->hip_fail(rc, "hipEventCreate(profile)");
+        kv->ev_pool.push_back(e);
+    }
+    kv->profile = kernel_mask;
     return NI_OK;
 }
 

@@ -18,6 +18,8 @@
 // softmax runs in the base-2 domain (scores pre-scaled by log2(e)/sqrt(D)).
 #include <hip/hip_runtime.h>
 
+#include <cstring>
+
 #include "kv_plan.h"
 
 namespace ni {
@@ -78,32 +80,60 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[8], f
 // empty states is 1 (not NaN); masked scores are -inf and weigh 0.
 constexpr float kMinScore = -1e30f;
 
+// A plan passed with the kernel arguments (N > 0) or left in device memory
+// (N == 0: the launch struct's `plan` pointer).  Arguments live in the
+// read-only kernarg segment; the kernels index it in place.
+template <int N>
+struct PlanArg {
+    uint8_t b[N > 0 ? N : 4];
+};
+
+template <int N>
+__device__ __forceinline__ const uint8_t* plan_base(const PlanArg<N>& pa, const uint8_t* dev) {
+    if constexpr (N > 0)
+        return pa.b;
+    else
+        return dev;
+}
+
 // ------------------------------------------------------------------ append
 
-__global__ __launch_bounds__(256) void kv_append_kernel(const AppendLaunch a) {
-    const uint32_t D = a.pool.head_dim;
-    const uint32_t chunks = (a.pool.n_head * D) >> 3;  // 8 elements per thread
-    const uint32_t per_row = 2 * chunks;                 // K then V
-    const uint32_t per_layer = per_row * a.n_rows;
-    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-    if (gid >= per_layer * a.n_lay) return;
+// One thread's share of an append: 8 elements (two float4 loads, one 16-byte
+// store) of K or V of one row of one layer.  `gid` enumerates
+// [layer][row][K then V][C/8] over the n_rows entries.
+__device__ __forceinline__ void append_chunk(const PoolGeom& pool, const float* k, const float* v, int64_t row_stride,
+                                             int64_t layer_stride, const AppendEntry* entries, uint32_t n_rows,
+                                             uint32_t layer0, uint32_t n_lay, uint32_t gid) {
+    const uint32_t D = pool.head_dim;
+    const uint32_t chunks = (pool.n_head * D) >> 3;  // 8 elements per thread
+    const uint32_t per_row = 2 * chunks;               // K then V
+    const uint32_t per_layer = per_row * n_rows;
+    if (gid >= per_layer * n_lay) return;
     const uint32_t lay = gid / per_layer;
     uint32_t r = gid - lay * per_layer;
     const uint32_t row = r / per_row;
     r -= row * per_row;
     const uint32_t is_v = r >= chunks;
     const uint32_t c8 = (r - is_v * chunks) * 8;
-    const AppendEntry e = a.entries[row];
-    const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.layer_stride + (int64_t)e.src_row * a.row_stride + c8;
+    const AppendEntry e = entries[row];
+    const float* src = (is_v ? v : k) + (int64_t)lay * layer_stride + (int64_t)e.src_row * row_stride + c8;
     const float4 x0 = reinterpret_cast<const float4*>(src)[0];
     const float4 x1 = reinterpret_cast<const float4*>(src)[1];
     const uint32_t head = c8 / D, d0 = c8 - head * D;
-    uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)(a.layer0 + lay) * a.pool.layer_halves +
-                    ((uint64_t)e.page * a.pool.n_head + head) * (kPage * D) + e.slot * D + d0;
+    uint16_t* dst = (is_v ? pool.v : pool.k) + (uint64_t)(layer0 + lay) * pool.layer_halves +
+                    (uint64_t)e.page * pool.page_halves + head * pool.head_halves + e.slot * D + d0;
     *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
 }
 
-__global__ __launch_bounds__(256) void kv_gather_kernel(const GatherLaunch a) {
+template <int INL>
+__global__ __launch_bounds__(256) void kv_append_kernel(const AppendLaunch a, const PlanArg<INL> pa) {
+    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
+    append_chunk(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
+                 blockIdx.x * 256u + threadIdx.x);
+}
+
+template <int INL>
+__global__ __launch_bounds__(256) void kv_gather_kernel(const GatherLaunch a, const PlanArg<INL> pa) {
     const uint32_t D = a.pool.head_dim;
     const uint32_t chunks = (a.pool.n_head * D) >> 3;
     const uint32_t per_row = 2 * chunks;
@@ -116,10 +146,10 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherLaunch a) {
     r -= row * per_row;
     const uint32_t is_v = r >= chunks;
     const uint32_t c8 = (r - is_v * chunks) * 8;
-    const AppendEntry e = a.entries[row];
+    const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries)[row];
     const uint32_t head = c8 / D, d0 = c8 - head * D;
     const uint16_t* src = (is_v ? a.pool.v : a.pool.k) + (uint64_t)(a.layer0 + lay) * a.pool.layer_halves +
-                          ((uint64_t)e.page * a.pool.n_head + head) * (kPage * D) + e.slot * D + d0;
+                          (uint64_t)e.page * a.pool.page_halves + head * a.pool.head_halves + e.slot * D + d0;
     uint16_t* dst = (is_v ? a.v_out : a.k_out) + (int64_t)lay * a.layer_stride + (int64_t)e.src_row * a.row_stride + c8;
     *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
 }
@@ -132,6 +162,64 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict
 
 // --------------------------------------------------------------- attention
 
+// Tuning knobs of the split kernel (compile-time; the defaults are the
+// measured best on MI355X for the GPT-2 and long-context shapes).
+#ifndef NI_ATTN_WAVES
+#define NI_ATTN_WAVES 4      // waves per workgroup sharing one item's pages
+#endif
+#ifndef NI_ATTN_PAGES
+#define NI_ATTN_PAGES 2      // pages per wave per loop iteration
+#endif
+#ifndef NI_ATTN_PREFETCH
+#define NI_ATTN_PREFETCH 1   // issue the next iteration's loads before computing
+#endif
+#ifndef NI_ATTN_NT
+#define NI_ATTN_NT 1         // non-temporal K/V loads (streamed once per step)
+#endif
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 load16(const u32x4* p) {
+#if NI_ATTN_NT
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
+// K and V chunks of PB pages for one lane: page pg+b, load i covers key rows
+// i*KPL .. i*KPL+KPL-1 of the page.  Pages past pg_end read as zeros.
+template <int PB, int LPP>
+struct PageRegs {
+    u32x4 k[PB][LPP];
+    u32x4 v[PB][LPP];
+};
+
+template <int PB, int LPP>
+__device__ __forceinline__ void load_pages(PageRegs<PB, LPP>& r, const uint32_t* __restrict__ tab, uint32_t pg,
+                                           uint32_t pg_end, const uint16_t* __restrict__ kbase,
+                                           const uint16_t* __restrict__ vbase, uint64_t page_stride, int lane) {
+#pragma unroll
+    for (int b = 0; b < PB; b++) {
+        if (pg + b < pg_end) {
+            const uint64_t phys = tab[pg + b];
+            const u32x4* kp = reinterpret_cast<const u32x4*>(kbase + phys * page_stride) + lane;
+            const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
+#pragma unroll
+            for (int i = 0; i < LPP; i++) {
+                r.k[b][i] = load16(kp + i * 64);
+                r.v[b][i] = load16(vp + i * 64);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < LPP; i++) {
+                r.k[b][i] = u32x4{0, 0, 0, 0};
+                r.v[b][i] = u32x4{0, 0, 0, 0};
+            }
+        }
+    }
+}
+
 // One workgroup = W waves = one (item, layer, head).  Waves take the item's
 // pages round-robin, PB pages per iteration.  Inside a wave, lane l reads 16
 // bytes (8 halves) of key row kl = l / LPK, dims ds*8 .. ds*8+7 (ds = l % LPK):
@@ -139,25 +227,77 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict
 // loads.  Each lane keeps its own flash state (m, l, o[8]) per query over the
 // keys its key-row group sees; the groups are merged once at the end (wave
 // shuffles, then LDS across waves).
-template <int D, int NQ, int W, int PB>
-__global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a) {
+template <int D, int NQ, int W, int PB, bool FUSED, int INL>
+__global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
     constexpr int LPK = D / 8;
     constexpr int KPL = 64 / LPK;
     constexpr int LPP = kPage / KPL;
-    constexpr uint32_t PAGE_HALVES = kPage * D;
     __shared__ float red[W][NQ][D + 2];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t H = a.pool.n_head;
     const uint32_t lh = a.n_lay * H;
+    const uint8_t* plan = plan_base(pa, a.plan);
+    if constexpr (FUSED) {
+        // Blocks past the items' append the rows of sequences without queries.
+        const uint32_t n_attn = a.n_items * lh;
+        if (blockIdx.x >= n_attn) {
+            const uint32_t base = (blockIdx.x - n_attn) * (64u * W);
+            append_chunk(a.pool, a.k, a.v, a.kv_row_stride, a.kv_layer_stride,
+                         reinterpret_cast<const AppendEntry*>(plan + a.off_orphans), a.n_orphans, a.layer0,
+                         a.n_lay, base + threadIdx.x);
+            return;
+        }
+    }
     const uint32_t item_i = blockIdx.x / lh;
     const uint32_t rem = blockIdx.x - item_i * lh;
     const uint32_t lay = rem / H;
     const uint32_t head = rem - lay * H;
-    const AttnItem it = a.items[item_i];
+    const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
     const int kl = lane / LPK;
     const int ds = lane % LPK;
+
+    const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
+    const uint16_t* kbase = a.pool.k + layer_off;
+    const uint16_t* vbase = a.pool.v + layer_off;
+    const uint64_t page_stride = a.pool.page_halves;
+    const uint32_t* __restrict__ tab = reinterpret_cast<const uint32_t*>(plan + a.off_table) + it.tab;
+    const uint32_t pg_begin = it.kv_begin / kPage;
+    const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
+    // Keys below full_end are visible to every query of the item.
+    const uint32_t full_end = min(it.pos0 + 1, it.kv_end);
+    constexpr uint32_t STRIDE = W * PB;
+
+    if constexpr (FUSED) {
+        // This step's new rows in [kv_begin, kv_end), this (layer, head)'s
+        // slice: no other workgroup of the launch reads or writes these
+        // blocks and the vector L1 starts the kernel clean, so after the
+        // barrier this workgroup's loads see its own stores.
+        if (it.napp) {
+            constexpr uint32_t CH = D / 8;  // 16-byte chunks per row of one head
+            for (uint32_t t = threadIdx.x; t < it.napp * 2 * CH; t += 64 * W) {
+                const uint32_t row = t / (2 * CH);
+                const uint32_t rem2 = t - row * (2 * CH);
+                const uint32_t is_v = rem2 >= CH;
+                const uint32_t c = (rem2 - is_v * CH) * 8;
+                const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan + a.off_app)[it.app0 + row];
+                const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride +
+                                   (int64_t)e.src_row * a.kv_row_stride + head * D + c;
+                const float4 x0 = reinterpret_cast<const float4*>(src)[0];
+                const float4 x1 = reinterpret_cast<const float4*>(src)[1];
+                uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + layer_off + (uint64_t)e.page * page_stride +
+                                e.slot * D + c;
+                *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
+            }
+            __syncthreads();
+        }
+    }
+
+    // First pages in flight before the query loads.
+    PageRegs<PB, LPP> cur;
+    uint32_t pg = pg_begin + wave * PB;
+    if (pg < pg_end) load_pages(cur, tab, pg, pg_end, kbase, vbase, page_stride, lane);
 
     float q[NQ][8];
     {
@@ -186,43 +326,17 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a) 
         for (int e = 0; e < 8; e++) o[r][e] = 0.f;
     }
 
-    const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * PAGE_HALVES;
-    const uint16_t* __restrict__ kbase = a.pool.k + layer_off;
-    const uint16_t* __restrict__ vbase = a.pool.v + layer_off;
-    const uint64_t page_stride = (uint64_t)H * PAGE_HALVES;
-    const uint32_t* __restrict__ tab = a.table + it.tab;
-    const uint32_t pg_begin = it.kv_begin / kPage;
-    const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
-    // Keys below full_end are visible to every query of the item.
-    const uint32_t full_end = min(it.pos0 + 1, it.kv_end);
-
-    for (uint32_t pg = pg_begin + wave * PB; pg < pg_end; pg += W * PB) {
-        uint4 kr[PB][LPP], vr[PB][LPP];
-#pragma unroll
-        for (int b = 0; b < PB; b++) {
-            if (pg + b < pg_end) {
-                const uint64_t phys = tab[pg + b];
-                const uint4* kp = reinterpret_cast<const uint4*>(kbase + phys * page_stride) + lane;
-                const uint4* vp = reinterpret_cast<const uint4*>(vbase + phys * page_stride) + lane;
-#pragma unroll
-                for (int i = 0; i < LPP; i++) {
-                    kr[b][i] = kp[i * 64];
-                    vr[b][i] = vp[i * 64];
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < LPP; i++) {
-                    kr[b][i] = make_uint4(0, 0, 0, 0);
-                    vr[b][i] = make_uint4(0, 0, 0, 0);
-                }
-            }
-        }
+    for (; pg < pg_end; pg += STRIDE) {
+#if NI_ATTN_PREFETCH
+        PageRegs<PB, LPP> nxt;
+        if (pg + STRIDE < pg_end) load_pages(nxt, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane);
+#endif
         float s[NQ][PB][LPP];
 #pragma unroll
         for (int b = 0; b < PB; b++) {
 #pragma unroll
             for (int i = 0; i < LPP; i++) {
-                const half8_t kh = __builtin_bit_cast(half8_t, kr[b][i]);
+                const half8_t kh = __builtin_bit_cast(half8_t, cur.k[b][i]);
 #pragma unroll
                 for (int r = 0; r < NQ; r++) {
                     float acc = 0.f;
@@ -240,7 +354,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a) 
 #pragma unroll
                 for (int i = 0; i < LPP; i++) {
                     const uint32_t j = (pg + b) * kPage + i * KPL + kl;
-                    if (j >= it.kv_end) vr[b][i] = make_uint4(0, 0, 0, 0);
+                    if (j >= it.kv_end) cur.v[b][i] = u32x4{0, 0, 0, 0};
 #pragma unroll
                     for (int r = 0; r < NQ; r++)
                         if (j > it.pos0 + r || j >= it.kv_end) s[r][b][i] = -INFINITY;
@@ -267,12 +381,17 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a) 
                 for (int i = 0; i < LPP; i++) {
                     const float p = fast_exp2(s[r][b][i] - mn);
                     l[r] += p;
-                    const half8_t vh = __builtin_bit_cast(half8_t, vr[b][i]);
+                    const half8_t vh = __builtin_bit_cast(half8_t, cur.v[b][i]);
 #pragma unroll
                     for (int e = 0; e < 8; e++) o[r][e] = fmaf(p, static_cast<float>(vh[e]), o[r][e]);
                 }
             }
         }
+#if NI_ATTN_PREFETCH
+        cur = nxt;
+#else
+        if (pg + STRIDE < pg_end) load_pages(cur, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane);
+#endif
     }
 
     // Merge the KPL key-row groups of the wave (lanes ds, ds+LPK, ...).
@@ -331,15 +450,15 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a) 
 
 // One workgroup of D threads per (merge item, layer, head); thread d owns
 // output dimension d of every query row of the group.
-template <int D, int NQ>
-__global__ __launch_bounds__(D) void attn_merge_kernel(const AttnLaunch a) {
+template <int D, int NQ, int INL>
+__global__ __launch_bounds__(D) void attn_merge_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
     const uint32_t H = a.pool.n_head;
     const uint32_t lh = a.n_lay * H;
     const uint32_t mi = blockIdx.x / lh;
     const uint32_t rem = blockIdx.x - mi * lh;
     const uint32_t lay = rem / H;
     const uint32_t head = rem - lay * H;
-    const MergeItem g = a.merges[mi];
+    const MergeItem g = reinterpret_cast<const MergeItem*>(plan_base(pa, a.plan) + a.off_merges)[mi];
     const uint32_t d = threadIdx.x;
     const uint64_t slot_stride = (uint64_t)a.n_lay * H * NQ * (D + 2);
     for (uint32_t r = 0; r < g.nq; r++) {
@@ -357,42 +476,64 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(const AttnLaunch a) {
     }
 }
 
-// Waves per workgroup and pages per wave iteration of the split kernel.
-constexpr int kWaves = 4;
-constexpr int kPagesPerIter = 2;
+constexpr int kWaves = NI_ATTN_WAVES;
+constexpr int kPagesPerIter = NI_ATTN_PAGES;
 
-template <int D, int NQ>
-hipError_t attn_launch_t(const AttnLaunch& a, hipStream_t s) {
-    const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head;
-    if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, kPagesPerIter>), dim3((uint32_t)blocks), dim3(64 * kWaves),
-                       0, s, a);
-    return hipGetLastError();
+// Launch `kern<INL>` with the plan inline (kInlinePlanBytes of arguments) or
+// through the device pointer in the launch struct.
+template <typename L, typename Fn>
+hipError_t with_plan(const L& a, const void* inline_plan, uint32_t inline_bytes, Fn&& launch) {
+    if (inline_plan) {
+        if (inline_bytes > kInlinePlanBytes) return hipErrorInvalidValue;
+        PlanArg<kInlinePlanBytes> pa;
+        memcpy(pa.b, inline_plan, inline_bytes);
+        return launch(pa);
+    }
+    return launch(PlanArg<0>{});
 }
 
 template <int D, int NQ>
-hipError_t merge_launch_t(const AttnLaunch& a, hipStream_t s) {
+hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+    const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
+    if (blocks == 0) return hipSuccess;
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        if (a.napp_total || a.n_orphan_blocks)
+            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, kPagesPerIter, true, INL>), dim3((uint32_t)blocks),
+                               dim3(64 * kWaves), 0, s, a, pa);
+        else
+            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, kPagesPerIter, false, INL>), dim3((uint32_t)blocks),
+                               dim3(64 * kWaves), 0, s, a, pa);
+        return hipGetLastError();
+    });
+}
+
+template <int D, int NQ>
+hipError_t merge_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
     const uint64_t blocks = (uint64_t)a.n_merges * a.n_lay * a.pool.n_head;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((attn_merge_kernel<D, NQ>), dim3((uint32_t)blocks), dim3(D), 0, s, a);
-    return hipGetLastError();
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        hipLaunchKernelGGL((attn_merge_kernel<D, NQ, INL>), dim3((uint32_t)blocks), dim3(D), 0, s, a, pa);
+        return hipGetLastError();
+    });
 }
 
 template <int D>
-hipError_t attn_dispatch_nq(const AttnLaunch& a, hipStream_t s, bool merge) {
+hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
     switch (a.nq_tile) {
-        case 1: return merge ? merge_launch_t<D, 1>(a, s) : attn_launch_t<D, 1>(a, s);
-        case 2: return merge ? merge_launch_t<D, 2>(a, s) : attn_launch_t<D, 2>(a, s);
-        case 4: return merge ? merge_launch_t<D, 4>(a, s) : attn_launch_t<D, 4>(a, s);
-        case 8: return merge ? merge_launch_t<D, 8>(a, s) : attn_launch_t<D, 8>(a, s);
+        case 1: return merge ? merge_launch_t<D, 1>(a, ip, ib, s) : attn_launch_t<D, 1>(a, ip, ib, s);
+        case 2: return merge ? merge_launch_t<D, 2>(a, ip, ib, s) : attn_launch_t<D, 2>(a, ip, ib, s);
+        case 4: return merge ? merge_launch_t<D, 4>(a, ip, ib, s) : attn_launch_t<D, 4>(a, ip, ib, s);
+        case 8: return merge ? merge_launch_t<D, 8>(a, ip, ib, s) : attn_launch_t<D, 8>(a, ip, ib, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t attn_dispatch(const AttnLaunch& a, hipStream_t s, bool merge) {
+hipError_t attn_dispatch(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
     switch (a.pool.head_dim) {
-        case 64: return attn_dispatch_nq<64>(a, s, merge);
-        case 128: return attn_dispatch_nq<128>(a, s, merge);
+        case 64: return attn_dispatch_nq<64>(a, ip, ib, s, merge);
+        case 128: return attn_dispatch_nq<128>(a, ip, ib, s, merge);
         default: return hipErrorInvalidValue;
     }
 }
@@ -401,23 +542,38 @@ hipError_t attn_dispatch(const AttnLaunch& a, hipStream_t s, bool merge) {
 
 bool attention_supported(uint32_t head_dim) { return head_dim == 64 || head_dim == 128; }
 
-hipError_t launch_append(const AppendLaunch& a, hipStream_t s) {
+hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
     const uint64_t threads = (uint64_t)a.n_lay * a.n_rows * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
     if (threads == 0) return hipSuccess;
-    hipLaunchKernelGGL(kv_append_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a);
-    return hipGetLastError();
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        hipLaunchKernelGGL(kv_append_kernel<INL>, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a, pa);
+        return hipGetLastError();
+    });
 }
 
-hipError_t launch_gather(const GatherLaunch& a, hipStream_t s) {
+hipError_t launch_gather(const GatherLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
     const uint64_t threads = (uint64_t)a.n_lay * a.n_rows * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
     if (threads == 0) return hipSuccess;
-    hipLaunchKernelGGL(kv_gather_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a);
-    return hipGetLastError();
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        hipLaunchKernelGGL(kv_gather_kernel<INL>, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a, pa);
+        return hipGetLastError();
+    });
 }
 
-hipError_t launch_attention(const AttnLaunch& a, hipStream_t s) { return attn_dispatch(a, s, false); }
+hipError_t launch_attention(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+    return attn_dispatch(a, ip, ib, s, false);
+}
 
-hipError_t launch_merge(const AttnLaunch& a, hipStream_t s) { return attn_dispatch(a, s, true); }
+uint32_t orphan_blocks(const AttnLaunch& a) {
+    const uint64_t threads = (uint64_t)a.n_lay * a.n_orphans * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
+    return (uint32_t)((threads + 64 * kWaves - 1) / (64 * kWaves));
+}
+
+hipError_t launch_merge(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+    return attn_dispatch(a, ip, ib, s, true);
+}
 
 hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;

@@ -36,7 +36,9 @@ struct AttnItem {
     uint32_t kv_begin;  // first key (multiple of 16)
     uint32_t kv_end;    // one past the last key: min(partition end, pos0 + nq)
     uint32_t part_slot; // partial-result slot, or kNoSlot (write out directly)
-    uint32_t pad;
+    uint32_t app0;      // fused launches: first append entry of this step's new
+    uint32_t napp;      //   rows inside [kv_begin, kv_end), and their count
+    uint32_t pad[3];
 };
 
 // A group split into n_parts partitions, merged by log-sum-exp.
@@ -47,11 +49,15 @@ struct MergeItem {
     uint32_t n_parts;
 };
 
-// Device pool geometry: K and V each [n_layer][kv_pages][n_head][16][head_dim].
+// Device pool geometry.  The (layer, page, head) block of K starts at
+// k + layer*layer_halves + page*page_halves + head*head_halves and holds the
+// page's 16 positions x head_dim halves contiguously; V likewise from v.
 struct PoolGeom {
     uint16_t* k;
     uint16_t* v;
-    uint64_t layer_halves;  // kv_pages * n_head * 16 * head_dim
+    uint64_t layer_halves;
+    uint64_t page_halves;
+    uint32_t head_halves;
     uint32_t n_head;
     uint32_t head_dim;
 };
@@ -62,7 +68,8 @@ struct AppendLaunch {
     const float* v;
     int64_t row_stride;
     int64_t layer_stride;
-    const AppendEntry* entries;  // device
+    const uint8_t* plan;         // device staging buffer (unused when inline)
+    uint32_t off_entries;
     uint32_t n_rows;
     uint32_t layer0;
     uint32_t n_lay;
@@ -74,7 +81,8 @@ struct GatherLaunch {
     uint16_t* v_out;
     int64_t row_stride;  // halves
     int64_t layer_stride;
-    const AppendEntry* entries;  // src_row = output row
+    const uint8_t* plan;
+    uint32_t off_entries;        // src_row = output row
     uint32_t n_rows;
     uint32_t layer0;
     uint32_t n_lay;
@@ -82,16 +90,29 @@ struct GatherLaunch {
 
 struct AttnLaunch {
     PoolGeom pool;
+    // Fused append (0 rows when the step's rows were appended beforehand):
+    // item rows come from `app`, rows of sequences without queries from
+    // `orphans`, handled by the n_orphan_blocks blocks after the items'.
+    const float* k;
+    const float* v;
+    int64_t kv_row_stride;
+    int64_t kv_layer_stride;
+    uint32_t off_app;
+    uint32_t off_orphans;
+    uint32_t n_orphans;
+    uint32_t n_orphan_blocks;
+    uint32_t napp_total;  // rows the items append (0: not fused)
     const float* q;
     int64_t q_row_stride;
     int64_t q_layer_stride;
     float* out;
     int64_t out_row_stride;
     int64_t out_layer_stride;
-    const AttnItem* items;    // device, sorted longest first
-    const uint32_t* table;    // device, plan table (physical page ids)
+    const uint8_t* plan;      // device staging buffer (unused when inline)
+    uint32_t off_items;       // AttnItem[n_items], sorted longest first
+    uint32_t off_table;       // uint32_t page ids the items index
+    uint32_t off_merges;      // MergeItem[n_merges]
     float* partials;          // [slot][n_lay][n_head][nq_tile][head_dim + 2]
-    const MergeItem* merges;  // device
     uint32_t n_items;
     uint32_t n_merges;
     uint32_t layer0;
@@ -100,13 +121,23 @@ struct AttnLaunch {
     float qscale;             // log2(e) / sqrt(head_dim)
 };
 
+// A plan travels to the device either inside the kernel arguments (up to
+// kInlinePlanBytes: the runtime copies arguments with the launch, so no
+// separate transfer sits on the stream) or in a device staging buffer.
+// Launch structs locate each part of the plan by its byte offset.
+constexpr uint32_t kInlinePlanBytes = 32768;
+
 // Kernel launchers (kv_kernels.hip).  They validate nothing; the host checks
 // every index the plan holds before calling them.
-hipError_t launch_append(const AppendLaunch& a, hipStream_t s);
-hipError_t launch_gather(const GatherLaunch& a, hipStream_t s);
-hipError_t launch_attention(const AttnLaunch& a, hipStream_t s);
-hipError_t launch_merge(const AttnLaunch& a, hipStream_t s);
+// `inline_plan` (nullptr: the plan is at a.plan on the device) holds
+// `inline_bytes` <= kInlinePlanBytes of plan passed with the arguments.
+hipError_t launch_append(const AppendLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
+hipError_t launch_gather(const GatherLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
+hipError_t launch_attention(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
+hipError_t launch_merge(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
 hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s);
+// Blocks a fused launch needs for its orphan rows (n_orphans set).
+uint32_t orphan_blocks(const AttnLaunch& a);
 bool attention_supported(uint32_t head_dim);
 
 }  // namespace ni

@@ -95,15 +95,19 @@ def test_truncate_rollback_matches_sequential(gpu):
     assert np.array_equal(out, want)
 
 
-def test_continuous_batching_trace(gpu, oracle_lib):
+@pytest.mark.parametrize("prefill_queries", ["all", "last"])
+def test_continuous_batching_trace(gpu, oracle_lib, prefill_queries):
     """Scaled config 3: Poisson arrivals, admission by free pages, decode rows
-    plus budgeted prefill chunks (attention at every prefill row), retire and
-    reuse pages; every step checked against the oracle."""
+    plus budgeted prefill chunks, retire and reuse pages; every step checked
+    against the oracle.  "all": attention at every prefill row (many query
+    groups per sequence, separate append launch); "last": only the row that
+    ends a prompt (the append fused into the attention launch, mid-prompt
+    chunks appended by the launch's extra blocks)."""
     rng = np.random.default_rng(32)
     opts = gpt2(kv_blocks=160, max_seqs=8, max_rows=128)
     m = Mirror(opts)
     trace = workloads.ContinuousBatching(m.kv, seed=3, max_batch=8, prompt=(20, 100), out=(3, 12), rate=0.7,
-                                         budget=64, max_rows=128, prefill_queries="all")
+                                         budget=64, max_rows=128, prefill_queries=prefill_queries)
     worst = 0.0
     for step in range(40):
         st = trace.plan()
