@@ -40,6 +40,27 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "attn_split_fused_config3.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the attention kernel from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy calibration
+    it records), with the algorithmic bytes of the same profiled steps."""
+    vals = {}
+    try:
+        for line in open(PROFILE_SUMMARY):
+            if "=" in line and line.split("=")[0].strip() in ("traffic_bytes_per_launch",
+                                                              "algorithmic_bytes_per_launch_same_steps"):
+                k, v = line.split("=")
+                vals[k.strip()] = int(float(v))
+    except OSError:
+        return None
+    if len(vals) != 2:
+        return None
+    return vals
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -281,6 +302,12 @@ def run_config3(args):
             "kernel": "attn_split_kernel<64,1,4,2,fused>", "avg_launch_us": round(ms / n * 1e3, 3), "launches": n,
             "algorithmic_bytes_per_launch": int(kbytes / n),
         }
+        tr = measured_traffic()
+        if tr:
+            res["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
+            res["roofline"]["traffic_vs_algorithmic"] = round(
+                tr["traffic_bytes_per_launch"] / tr["algorithmic_bytes_per_launch_same_steps"], 3)
+            res["roofline"]["traffic_source"] = "profiles/attn_split_fused_config3.md (rocprofv3 --pmc, scaled)"
     if args.cpu_seconds > 0:
         threads = args.threads or min(os.cpu_count() or 1, 16)
         log(f"bench: CPU baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
