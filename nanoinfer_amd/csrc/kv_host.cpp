@@ -221,12 +221,6 @@ int layer_range(ni_kv* kv, int32_t layer, uint32_t* layer0, uint32_t* n_lay) {
     return NI_OK;
 }
 
-uint32_t pow2_tile(uint32_t nq) {
-    uint32_t t = 1;
-    while (t < nq) t <<= 1;
-    return t;
-}
-
 // Attention part of a plan: group consecutive query rows of one sequence at
 // consecutive positions, split each group's keys into partitions, sort the
 // items longest first.
@@ -326,7 +320,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     std::stable_sort(P.items.begin(), P.items.end(), [](const AttnItem& x, const AttnItem& y) {
         return (x.kv_end - x.kv_begin) > (y.kv_end - y.kv_begin);
     });
-    P.nq_tile = pow2_tile(max_nq);
+    P.nq_tile = max_nq;  // kernels exist for every tile 1..kMaxGroupRows
     return NI_OK;
 }
 
@@ -627,6 +621,27 @@ int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
             kv->pool_bytes = (size_t)(2 * kv->layer_halves * o.n_layer * sizeof(uint16_t));
             e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
             if (e == hipSuccess) kv->vpool = kv->kpool + kv->layer_halves * o.n_layer;
+#elif defined(NI_KV_PAGE_OUTER)
+            // [kv_pages][n_layer][n_head][K|V][16][head_dim]: all of a page together.
+            kv->head_halves = (uint32_t)(2 * block);
+            kv->layer_halves = 2 * block * o.n_head;
+            kv->page_halves = kv->layer_halves * o.n_layer;
+            kv->pool_bytes = (size_t)(kv->page_halves * o.kv_pages * sizeof(uint16_t));
+            e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
+            if (e == hipSuccess) kv->vpool = kv->kpool + block;
+#elif defined(NI_KV_HEAD_MAJOR)
+            // [n_layer][n_head][kv_pages][K|V][16][head_dim]: a head's pages adjacent.
+            kv->page_halves = 2 * block;
+            kv->head_halves = (uint32_t)0;  // set below (may exceed 32 bits? checked)
+            {
+                const uint64_t hh = 2 * block * o.kv_pages;
+                if (hh > 0xffffffffull) e = hipErrorInvalidValue;
+                kv->head_halves = (uint32_t)hh;
+            }
+            kv->layer_halves = (uint64_t)kv->head_halves * o.n_head;
+            kv->pool_bytes = (size_t)(kv->layer_halves * o.n_layer * sizeof(uint16_t));
+            if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
+            if (e == hipSuccess) kv->vpool = kv->kpool + block;
 #else
             kv->head_halves = (uint32_t)(2 * block);
             kv->page_halves = 2 * block * o.n_head;

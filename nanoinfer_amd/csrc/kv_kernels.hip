@@ -121,7 +121,7 @@ __device__ __forceinline__ void append_chunk(const PoolGeom& pool, const float* 
     const float4 x1 = reinterpret_cast<const float4*>(src)[1];
     const uint32_t head = c8 / D, d0 = c8 - head * D;
     uint16_t* dst = (is_v ? pool.v : pool.k) + (uint64_t)(layer0 + lay) * pool.layer_halves +
-                    (uint64_t)e.page * pool.page_halves + head * pool.head_halves + e.slot * D + d0;
+                    (uint64_t)e.page * pool.page_halves + (uint64_t)head * pool.head_halves + e.slot * D + d0;
     *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
 }
 
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(const GatherLaunch a, co
     const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries)[row];
     const uint32_t head = c8 / D, d0 = c8 - head * D;
     const uint16_t* src = (is_v ? a.pool.v : a.pool.k) + (uint64_t)(a.layer0 + lay) * a.pool.layer_halves +
-                          (uint64_t)e.page * a.pool.page_halves + head * a.pool.head_halves + e.slot * D + d0;
+                          (uint64_t)e.page * a.pool.page_halves + (uint64_t)head * a.pool.head_halves + e.slot * D + d0;
     uint16_t* dst = (is_v ? a.v_out : a.k_out) + (int64_t)lay * a.layer_stride + (int64_t)e.src_row * a.row_stride + c8;
     *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
 }
@@ -175,6 +175,9 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict
 #endif
 #ifndef NI_ATTN_NT
 #define NI_ATTN_NT 1         // non-temporal K/V loads (streamed once per step)
+#endif
+#ifndef NI_ATTN_LDS_PAD
+#define NI_ATTN_LDS_PAD 0    // extra LDS floats per workgroup (caps workgroups per CU)
 #endif
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
     constexpr int LPK = D / 8;
     constexpr int KPL = 64 / LPK;
     constexpr int LPP = kPage / KPL;
-    __shared__ float red[W][NQ][D + 2];
+    __shared__ float red[W][NQ][D + 2 + NI_ATTN_LDS_PAD / (W * NQ)];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -494,15 +497,21 @@ hipError_t with_plan(const L& a, const void* inline_plan, uint32_t inline_bytes,
 
 template <int D, int NQ>
 hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+    // Several queries per item hold NQ times the softmax state: one page per
+    // iteration keeps their registers (and occupancy) in check.
+#ifndef NI_ATTN_PAGES_D128
+#define NI_ATTN_PAGES_D128 2
+#endif
+    constexpr int PB = NQ > 1 ? 1 : (D == 128 ? NI_ATTN_PAGES_D128 : kPagesPerIter);
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         if (a.napp_total || a.n_orphan_blocks)
-            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, kPagesPerIter, true, INL>), dim3((uint32_t)blocks),
+            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, PB, true, INL>), dim3((uint32_t)blocks),
                                dim3(64 * kWaves), 0, s, a, pa);
         else
-            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, kPagesPerIter, false, INL>), dim3((uint32_t)blocks),
+            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, PB, false, INL>), dim3((uint32_t)blocks),
                                dim3(64 * kWaves), 0, s, a, pa);
         return hipGetLastError();
     });
@@ -522,10 +531,11 @@ hipError_t merge_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipS
 template <int D>
 hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
     switch (a.nq_tile) {
-        case 1: return merge ? merge_launch_t<D, 1>(a, ip, ib, s) : attn_launch_t<D, 1>(a, ip, ib, s);
-        case 2: return merge ? merge_launch_t<D, 2>(a, ip, ib, s) : attn_launch_t<D, 2>(a, ip, ib, s);
-        case 4: return merge ? merge_launch_t<D, 4>(a, ip, ib, s) : attn_launch_t<D, 4>(a, ip, ib, s);
-        case 8: return merge ? merge_launch_t<D, 8>(a, ip, ib, s) : attn_launch_t<D, 8>(a, ip, ib, s);
+#define NI_NQ_CASE(N) \
+    case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s) : attn_launch_t<D, N>(a, ip, ib, s);
+        NI_NQ_CASE(1) NI_NQ_CASE(2) NI_NQ_CASE(3) NI_NQ_CASE(4)
+        NI_NQ_CASE(5) NI_NQ_CASE(6) NI_NQ_CASE(7) NI_NQ_CASE(8)
+#undef NI_NQ_CASE
         default: return hipErrorInvalidValue;
     }
 }

@@ -117,7 +117,7 @@ struct AttnLaunch {
     uint32_t n_merges;
     uint32_t layer0;
     uint32_t n_lay;
-    uint32_t nq_tile;         // compile-time query tile the kernels use (1, 2, 4 or 8)
+    uint32_t nq_tile;         // compile-time query tile the kernels use (1..kMaxGroupRows)
     float qscale;             // log2(e) / sqrt(head_dim)
 };
 
