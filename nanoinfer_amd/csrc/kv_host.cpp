@@ -320,7 +320,8 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     std::stable_sort(P.items.begin(), P.items.end(), [](const AttnItem& x, const AttnItem& y) {
         return (x.kv_end - x.kv_begin) > (y.kv_end - y.kv_begin);
     });
-    P.nq_tile = max_nq;  // kernels exist for every tile 1..kMaxGroupRows
+    // Single queries stream on the vector kernel; groups go to matrix cores.
+    P.nq_tile = (NI_ATTN_MFMA && max_nq > 1) ? kMfmaTile : max_nq;
     return NI_OK;
 }
 

@@ -190,6 +190,29 @@ __device__ __forceinline__ u32x4 load16(const u32x4* p) {
 #endif
 }
 
+// Fused append of one item: this step's new rows in [kv_begin, kv_end),
+// this (layer, head)'s slice.  No other workgroup of the launch reads or
+// writes these blocks and the vector L1 starts the kernel clean, so after a
+// barrier the workgroup's loads see its own stores.
+template <int D>
+__device__ __forceinline__ void item_append(const AttnLaunch& a, const uint8_t* plan, const AttnItem& it, uint32_t lay,
+                                            uint32_t head, uint64_t layer_off, uint64_t page_stride, uint32_t nthreads) {
+    constexpr uint32_t CH = D / 8;  // 16-byte chunks per row of one head
+    for (uint32_t t = threadIdx.x; t < it.napp * 2 * CH; t += nthreads) {
+        const uint32_t row = t / (2 * CH);
+        const uint32_t rem2 = t - row * (2 * CH);
+        const uint32_t is_v = rem2 >= CH;
+        const uint32_t c = (rem2 - is_v * CH) * 8;
+        const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan + a.off_app)[it.app0 + row];
+        const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride + (int64_t)e.src_row * a.kv_row_stride +
+                           head * D + c;
+        const float4 x0 = reinterpret_cast<const float4*>(src)[0];
+        const float4 x1 = reinterpret_cast<const float4*>(src)[1];
+        uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + layer_off + (uint64_t)e.page * page_stride + e.slot * D + c;
+        *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
+    }
+}
+
 // K and V chunks of PB pages for one lane: page pg+b, load i covers key rows
 // i*KPL .. i*KPL+KPL-1 of the page.  Pages past pg_end read as zeros.
 template <int PB, int LPP>
@@ -273,26 +296,8 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
     constexpr uint32_t STRIDE = W * PB;
 
     if constexpr (FUSED) {
-        // This step's new rows in [kv_begin, kv_end), this (layer, head)'s
-        // slice: no other workgroup of the launch reads or writes these
-        // blocks and the vector L1 starts the kernel clean, so after the
-        // barrier this workgroup's loads see its own stores.
         if (it.napp) {
-            constexpr uint32_t CH = D / 8;  // 16-byte chunks per row of one head
-            for (uint32_t t = threadIdx.x; t < it.napp * 2 * CH; t += 64 * W) {
-                const uint32_t row = t / (2 * CH);
-                const uint32_t rem2 = t - row * (2 * CH);
-                const uint32_t is_v = rem2 >= CH;
-                const uint32_t c = (rem2 - is_v * CH) * 8;
-                const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan + a.off_app)[it.app0 + row];
-                const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride +
-                                   (int64_t)e.src_row * a.kv_row_stride + head * D + c;
-                const float4 x0 = reinterpret_cast<const float4*>(src)[0];
-                const float4 x1 = reinterpret_cast<const float4*>(src)[1];
-                uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + layer_off + (uint64_t)e.page * page_stride +
-                                e.slot * D + c;
-                *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
-            }
+            item_append<D>(a, plan, it, lay, head, layer_off, page_stride, 64 * W);
             __syncthreads();
         }
     }
@@ -451,6 +456,230 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
     }
 }
 
+// ------------------------------------------------ attention, several queries
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+// f32 -> two f16 whose sum carries ~22 bits: MFMA on f16 operands with f32
+// accumulation then reproduces f32 products to ~2^-22 relative.
+__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
+    hi = static_cast<_Float16>(x);
+    lo = static_cast<_Float16>(x - static_cast<float>(hi));
+}
+
+// Groups of 2..16 queries of one sequence (speculative verify, prefill
+// chunks) on matrix cores: one wave per page walks S^T = K Q^T (16 keys x 16
+// query slots, v_mfma_f32_16x16x32_f16, q split into f16 hi + lo), the
+// online softmax on S^T's columns, and O^T += V^T P^T (v_mfma_f32_16x16x16_f16,
+// p split hi + lo), V transposed through a padded LDS tile.  Lane l owns
+// query column l % 16 of S^T and O^T, rows 4*(l/16) .. +3 (MFMA output
+// layout), so the softmax state of a query lives in lanes q, q+16, q+32, q+48.
+// Waves take the item's pages round-robin and merge through LDS at the end,
+// as in attn_split_kernel.
+template <int D, int W, bool FUSED, int INL>
+__global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+    constexpr int QC = D / 32;      // 32-dim chunks of the QK product
+    constexpr int VC = D / 16;      // 16-dim chunks of the PV product
+    constexpr int LPK = D / 8;      // lanes per key row in a coalesced V load
+    constexpr int KPL = 64 / LPK;   // key rows per V load
+    constexpr int LPP = kPage / KPL;
+    constexpr int VROW = D + 8;     // LDS halves per V row (pad: conflict-free column reads)
+    constexpr int NQ = 16;
+    __shared__ float red[W][NQ][D + 2];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[W][kPage * VROW];
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t H = a.pool.n_head;
+    const uint32_t lh = a.n_lay * H;
+    const uint8_t* plan = plan_base(pa, a.plan);
+    if constexpr (FUSED) {
+        const uint32_t n_attn = a.n_items * lh;
+        if (blockIdx.x >= n_attn) {
+            const uint32_t base = (blockIdx.x - n_attn) * (64u * W);
+            append_chunk(a.pool, a.k, a.v, a.kv_row_stride, a.kv_layer_stride,
+                         reinterpret_cast<const AppendEntry*>(plan + a.off_orphans), a.n_orphans, a.layer0,
+                         a.n_lay, base + threadIdx.x);
+            return;
+        }
+    }
+    const uint32_t item_i = blockIdx.x / lh;
+    const uint32_t rem = blockIdx.x - item_i * lh;
+    const uint32_t lay = rem / H;
+    const uint32_t head = rem - lay * H;
+    const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
+    const int col = lane & 15;  // query slot of S^T / O^T columns
+    const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
+
+    const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
+    const uint16_t* kbase = a.pool.k + layer_off;
+    const uint16_t* vbase = a.pool.v + layer_off;
+    const uint64_t page_stride = a.pool.page_halves;
+    const uint32_t* __restrict__ tab = reinterpret_cast<const uint32_t*>(plan + a.off_table) + it.tab;
+    const uint32_t pg_begin = it.kv_begin / kPage;
+    const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
+
+    if constexpr (FUSED) {
+        if (it.napp) {
+            item_append<D>(a, plan, it, lay, head, layer_off, page_stride, 64 * W);
+            __syncthreads();
+        }
+    }
+
+    // Page registers: K as the A operand (key col, dims c*32 + 8*rg ..), V
+    // as coalesced rows (key i*KPL + lane/LPK, dims (lane%LPK)*8 ..).
+    u32x4 kr[QC], vr[LPP];
+    auto load = [&](uint32_t pg, u32x4 (&kk)[QC], u32x4 (&vv)[LPP]) {
+        const uint64_t phys = tab[pg];
+        const uint16_t* kp = kbase + phys * page_stride + col * D + 8 * rg;
+#pragma unroll
+        for (int c = 0; c < QC; c++) kk[c] = load16(reinterpret_cast<const u32x4*>(kp + c * 32));
+        const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
+#pragma unroll
+        for (int i = 0; i < LPP; i++) vv[i] = load16(vp + i * 64);
+    };
+    uint32_t pg = pg_begin + wave;
+    if (pg < pg_end) load(pg, kr, vr);
+
+    // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo.
+    half8_t qh[QC], ql[QC];
+    {
+        const bool has = col < (int)it.nq;
+        const float* qb = a.q + (int64_t)lay * a.q_layer_stride + (int64_t)(it.row0 + (has ? col : 0)) * a.q_row_stride +
+                          head * D + 8 * rg;
+#pragma unroll
+        for (int c = 0; c < QC; c++) {
+            float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (has) {
+                const float4 x0 = reinterpret_cast<const float4*>(qb + c * 32)[0];
+                const float4 x1 = reinterpret_cast<const float4*>(qb + c * 32)[1];
+                x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
+                x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                _Float16 h, l;
+                split_f16(x[e] * a.qscale, h, l);
+                qh[c][e] = h;
+                ql[c][e] = l;
+            }
+        }
+    }
+    float m = kMinScore, lsum = 0.f;
+    float4_t o[VC];
+#pragma unroll
+    for (int c = 0; c < VC; c++) o[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    _Float16* my_vt = vt[wave];
+    const uint32_t qpos = it.pos0 + col;  // this lane's query position
+
+    for (; pg < pg_end; pg += W) {
+        u32x4 kn[QC], vn[LPP];
+        if (pg + W < pg_end) load(pg + W, kn, vn);
+        // V rows to LDS (rows past kv_end as zeros: stale halves must not
+        // reach the product even with p = 0).
+#pragma unroll
+        for (int i = 0; i < LPP; i++) {
+            const uint32_t key = i * KPL + lane / LPK;
+            const u32x4 val = pg * kPage + key < it.kv_end ? vr[i] : u32x4{0, 0, 0, 0};
+            *reinterpret_cast<u32x4*>(my_vt + key * VROW + (lane % LPK) * 8) = val;
+        }
+        // S^T = K Q^T.
+        float4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < QC; c++) {
+            const half8_t kh = __builtin_bit_cast(half8_t, kr[c]);
+            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], st, 0, 0, 0);
+        }
+        float s[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t kp = pg * kPage + 4 * rg + j;
+            const bool ok = col < (int)it.nq && kp < it.kv_end && kp <= qpos;
+            s[j] = ok ? st[j] : -INFINITY;
+            mx = fmaxf(mx, s[j]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float alpha = fast_exp2(m - mn);
+        m = mn;
+        half4_t ph, pl;
+        float ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float p = fast_exp2(s[j] - mn);
+            ps += p;
+            _Float16 h, l;
+            split_f16(p, h, l);
+            ph[j] = h;
+            pl[j] = l;
+        }
+        lsum = lsum * alpha + ps;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // O^T += V^T P^T, 16 dims per product.
+#pragma unroll
+        for (int c = 0; c < VC; c++) {
+            half4_t vt4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) vt4[j] = my_vt[(4 * rg + j) * VROW + c * 16 + col];
+            o[c] *= alpha;
+            o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, ph, o[c], 0, 0, 0);
+            o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl, o[c], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (pg + W < pg_end) {
+#pragma unroll
+            for (int c = 0; c < QC; c++) kr[c] = kn[c];
+#pragma unroll
+            for (int i = 0; i < LPP; i++) vr[i] = vn[i];
+        }
+    }
+    // Lanes q, q+16, q+32, q+48 hold partial sums of query q's softmax.
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (col < (int)it.nq) {
+        if (rg == 0) {
+            red[wave][col][0] = m;
+            red[wave][col][1] = lsum;
+        }
+#pragma unroll
+        for (int c = 0; c < VC; c++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) red[wave][col][2 + c * 16 + 4 * rg + j] = o[c][j];
+    }
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < it.nq * D; t += 64 * W) {
+        const uint32_t r = t / D, d = t - r * D;
+        float M = red[0][r][0];
+#pragma unroll
+        for (int w = 1; w < W; w++) M = fmaxf(M, red[w][r][0]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            const float wt = fast_exp2(red[w][r][0] - M);
+            L += red[w][r][1] * wt;
+            O += red[w][r][2 + d] * wt;
+        }
+        if (it.part_slot == kNoSlot) {
+            a.out[(int64_t)lay * a.out_layer_stride + (int64_t)(it.row0 + r) * a.out_row_stride + head * D + d] = O / L;
+        } else {
+            float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * H + head) * NQ + r) * (D + 2);
+            if (d == 0) {
+                p[0] = M;
+                p[1] = L;
+            }
+            p[2 + d] = O;
+        }
+    }
+}
+
 // One workgroup of D threads per (merge item, layer, head); thread d owns
 // output dimension d of every query row of the group.
 template <int D, int NQ, int INL>
@@ -529,7 +758,25 @@ hipError_t merge_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipS
 }
 
 template <int D>
+hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+    const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
+    if (blocks == 0) return hipSuccess;
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        if (a.napp_total || a.n_orphan_blocks)
+            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, true, INL>), dim3((uint32_t)blocks), dim3(64 * kWaves), 0,
+                               s, a, pa);
+        else
+            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, false, INL>), dim3((uint32_t)blocks), dim3(64 * kWaves), 0,
+                               s, a, pa);
+        return hipGetLastError();
+    });
+}
+
+template <int D>
 hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
+    if (a.nq_tile == kMfmaTile)
+        return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s) : mfma_launch_t<D>(a, ip, ib, s);
     switch (a.nq_tile) {
 #define NI_NQ_CASE(N) \
     case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s) : attn_launch_t<D, N>(a, ip, ib, s);

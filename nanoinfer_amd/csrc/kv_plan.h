@@ -15,7 +15,13 @@ namespace ni {
 
 constexpr uint32_t kPage = 16;           // positions per page (batch.rs:33)
 constexpr uint32_t kNoSlot = 0xffffffffu; // AttnItem::part_slot: the item is its group's only partition
-constexpr uint32_t kMaxGroupRows = 8;    // most query rows sharing one K/V stream
+// Groups of several queries run on matrix cores (tile of 16 query slots);
+// with NI_ATTN_MFMA=0 they run on the vector kernel in tiles of up to 8.
+#ifndef NI_ATTN_MFMA
+#define NI_ATTN_MFMA 1
+#endif
+constexpr uint32_t kMfmaTile = 16;
+constexpr uint32_t kMaxGroupRows = NI_ATTN_MFMA ? kMfmaTile : 8;  // most query rows sharing one K/V stream
 
 // Where one appended row goes: pool page `page`, position `slot` (0..15) in it.
 struct AppendEntry {
@@ -117,7 +123,7 @@ struct AttnLaunch {
     uint32_t n_merges;
     uint32_t layer0;
     uint32_t n_lay;
-    uint32_t nq_tile;         // compile-time query tile the kernels use (1..kMaxGroupRows)
+    uint32_t nq_tile;         // query tile: 1..8 (vector kernel) or kMfmaTile (matrix cores)
     float qscale;             // log2(e) / sqrt(head_dim)
 };
 

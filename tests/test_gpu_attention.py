@@ -41,21 +41,25 @@ def test_decode_contexts(gpu, oracle_lib, shape, split):
     say(f"{shape} split {split}: max abs err {err:.2e}")
 
 
-def test_causal_groups_spec_verify_shape(gpu, oracle_lib):
-    """Five consecutive rows of one sequence (g + 4 drafts) attend causally
-    and share their K/V reads; rows straddle page and partition edges."""
-    rng = np.random.default_rng(21)
-    m = Mirror(opts(workloads.GPT2))
+@pytest.mark.parametrize("shape", [workloads.GPT2, dict(n_layer=2, n_head=4, head_dim=128)], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("nq", [2, 5, 8, 13, 16, 20])
+def test_causal_groups(gpu, oracle_lib, shape, nq):
+    """nq consecutive rows of one sequence (g + drafts, prefill chunks) attend
+    causally and share their K/V reads; rows straddle page and partition
+    edges; groups over 16 rows split in two."""
+    rng = np.random.default_rng(21 + nq)
+    m = Mirror(opts(shape))
     for split in (0, 64, 128):
-        for L in (5, 14, 16, 62, 127, 130, 512):
-            m2 = m
-            s = m2.kv.add_seq()
-            m2.fill(s, L, rng)
-            rows = [(s, p) for p in range(L - 5, L)]
-            q = rng.standard_normal((12, 5, m.c)).astype(np.float32)
-            got, want = m2.attention(rows, q, split_tokens=split)
-            assert_close(got, want, f"L {L} split {split}")
-            m2.kv.free_seq(s)
+        for L in sorted({nq, nq + 1, 14 + nq, 16, 62, 127, 130, 512}):
+            if L < nq:
+                continue
+            s = m.kv.add_seq()
+            m.fill(s, L, rng)
+            rows = [(s, p) for p in range(L - nq, L)]
+            q = rng.standard_normal((shape["n_layer"], nq, m.c)).astype(np.float32)
+            got, want = m.attention(rows, q, split_tokens=split)
+            assert_close(got, want, f"nq {nq} L {L} split {split}")
+            m.kv.free_seq(s)
 
 
 def test_mixed_rows_and_long_groups(gpu, oracle_lib):
