@@ -461,12 +461,19 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-// f32 -> two f16 whose sum carries ~22 bits: MFMA on f16 operands with f32
-// accumulation then reproduces f32 products to ~2^-22 relative.
+// f32 -> f16 hi plus the residual scaled by 2^11 (kept in the normal range
+// of f16, where the residual itself would often be subnormal): x ~= hi +
+// lo * 2^-11 to ~2^-22 relative.  Products of hi and of lo are accumulated
+// separately on the matrix cores and combined in f32.
+constexpr float kLoScale = 2048.f, kLoUnscale = 1.f / 2048.f;
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
-    hi = static_cast<_Float16>(x);
-    lo = static_cast<_Float16>(x - static_cast<float>(hi));
+    // A hi below the normal range would be flushed by the matrix cores; the
+    // whole value then goes to lo.
+    hi = static_cast<_Float16>(fabsf(x) < 6.103515625e-05f ? 0.f : x);
+    lo = static_cast<_Float16>((x - static_cast<float>(hi)) * kLoScale);
 }
+// p in [0, 1] enters PV scaled by 2^14 so that p down to ~4e-9 is a normal f16.
+constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
 
 // Groups of 2..16 queries of one sequence (speculative verify, prefill
 // chunks) on matrix cores: one wave per page walks S^T = K Q^T (16 keys x 16
@@ -477,7 +484,7 @@ __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
 // layout), so the softmax state of a query lives in lanes q, q+16, q+32, q+48.
 // Waves take the item's pages round-robin and merge through LDS at the end,
 // as in attn_split_kernel.
-template <int D, int W, bool FUSED, int INL>
+template <int D, int W, int PB, bool FUSED, int INL>
 __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
     constexpr int QC = D / 32;      // 32-dim chunks of the QK product
     constexpr int VC = D / 16;      // 16-dim chunks of the PV product
@@ -487,7 +494,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, c
     constexpr int VROW = D + 8;     // LDS halves per V row (pad: conflict-free column reads)
     constexpr int NQ = 16;
     __shared__ float red[W][NQ][D + 2];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[W][kPage * VROW];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[W][PB * kPage * VROW];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -519,6 +526,7 @@ __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, c
     const uint32_t* __restrict__ tab = reinterpret_cast<const uint32_t*>(plan + a.off_table) + it.tab;
     const uint32_t pg_begin = it.kv_begin / kPage;
     const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
+    constexpr uint32_t STRIDE = W * PB;
 
     if constexpr (FUSED) {
         if (it.napp) {
@@ -528,19 +536,28 @@ __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, c
     }
 
     // Page registers: K as the A operand (key col, dims c*32 + 8*rg ..), V
-    // as coalesced rows (key i*KPL + lane/LPK, dims (lane%LPK)*8 ..).
-    u32x4 kr[QC], vr[LPP];
-    auto load = [&](uint32_t pg, u32x4 (&kk)[QC], u32x4 (&vv)[LPP]) {
-        const uint64_t phys = tab[pg];
-        const uint16_t* kp = kbase + phys * page_stride + col * D + 8 * rg;
-#pragma unroll
-        for (int c = 0; c < QC; c++) kk[c] = load16(reinterpret_cast<const u32x4*>(kp + c * 32));
-        const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
-#pragma unroll
-        for (int i = 0; i < LPP; i++) vv[i] = load16(vp + i * 64);
+    // as coalesced rows (key i*KPL + lane/LPK, dims (lane%LPK)*8 ..).  Pages
+    // past pg_end are not loaded (their keys are masked).
+    struct Regs {
+        u32x4 k[PB][QC];
+        u32x4 v[PB][LPP];
     };
-    uint32_t pg = pg_begin + wave;
-    if (pg < pg_end) load(pg, kr, vr);
+    auto load = [&](uint32_t pg, Regs& r) {
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+            if (pg + b >= pg_end) continue;
+            const uint64_t phys = tab[pg + b];
+            const uint16_t* kp = kbase + phys * page_stride + col * D + 8 * rg;
+#pragma unroll
+            for (int c = 0; c < QC; c++) r.k[b][c] = load16(reinterpret_cast<const u32x4*>(kp + c * 32));
+            const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
+#pragma unroll
+            for (int i = 0; i < LPP; i++) r.v[b][i] = load16(vp + i * 64);
+        }
+    };
+    Regs cur;
+    uint32_t pg = pg_begin + wave * PB;
+    if (pg < pg_end) load(pg, cur);
 
     // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo.
     half8_t qh[QC], ql[QC];
@@ -567,55 +584,65 @@ __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, c
         }
     }
     float m = kMinScore, lsum = 0.f;
-    float4_t o[VC];
+    float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
 #pragma unroll
-    for (int c = 0; c < VC; c++) o[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
     _Float16* my_vt = vt[wave];
     const uint32_t qpos = it.pos0 + col;  // this lane's query position
+    const bool qok = col < (int)it.nq;
 
-    for (; pg < pg_end; pg += W) {
-        u32x4 kn[QC], vn[LPP];
-        if (pg + W < pg_end) load(pg + W, kn, vn);
-        // V rows to LDS (rows past kv_end as zeros: stale halves must not
+    for (; pg < pg_end; pg += STRIDE) {
+        Regs nxt;
+        if (pg + STRIDE < pg_end) load(pg + STRIDE, nxt);
+        // V rows to LDS; rows past kv_end as zeros (stale halves must not
         // reach the product even with p = 0).
 #pragma unroll
-        for (int i = 0; i < LPP; i++) {
-            const uint32_t key = i * KPL + lane / LPK;
-            const u32x4 val = pg * kPage + key < it.kv_end ? vr[i] : u32x4{0, 0, 0, 0};
-            *reinterpret_cast<u32x4*>(my_vt + key * VROW + (lane % LPK) * 8) = val;
-        }
-        // S^T = K Q^T.
-        float4_t st = {0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < PB; b++) {
 #pragma unroll
-        for (int c = 0; c < QC; c++) {
-            const half8_t kh = __builtin_bit_cast(half8_t, kr[c]);
-            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], st, 0, 0, 0);
+            for (int i = 0; i < LPP; i++) {
+                const uint32_t key = i * KPL + lane / LPK;
+                const u32x4 val = (pg + b) * kPage + key < it.kv_end ? cur.v[b][i] : u32x4{0, 0, 0, 0};
+                *reinterpret_cast<u32x4*>(my_vt + (b * kPage + key) * VROW + (lane % LPK) * 8) = val;
+            }
         }
-        float s[4];
+        // S^T = K Q^T per page; scores of keys 4*rg+j of each page.
+        float s[PB][4];
         float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t kp = pg * kPage + 4 * rg + j;
-            const bool ok = col < (int)it.nq && kp < it.kv_end && kp <= qpos;
-            s[j] = ok ? st[j] : -INFINITY;
-            mx = fmaxf(mx, s[j]);
+        for (int b = 0; b < PB; b++) {
+            float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < QC; c++) {
+                const half8_t kh = __builtin_bit_cast(half8_t, cur.k[b][c]);
+                st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t kp = (pg + b) * kPage + 4 * rg + j;
+                const bool ok = qok && kp < it.kv_end && kp <= qpos;
+                s[b][j] = ok ? st[j] + sl[j] * kLoUnscale : -INFINITY;
+                mx = fmaxf(mx, s[b][j]);
+            }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float mn = fmaxf(m, mx);
         const float alpha = fast_exp2(m - mn);
         m = mn;
-        half4_t ph, pl;
+        half4_t ph[PB], pl[PB];
         float ps = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float p = fast_exp2(s[j] - mn);
-            ps += p;
-            _Float16 h, l;
-            split_f16(p, h, l);
-            ph[j] = h;
-            pl[j] = l;
+        for (int b = 0; b < PB; b++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float p = fast_exp2(s[b][j] - mn);
+                ps += p;
+                _Float16 h, l;
+                split_f16(p * kPScale, h, l);
+                ph[b][j] = h;
+                pl[b][j] = l;
+            }
         }
         lsum = lsum * alpha + ps;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -624,27 +651,26 @@ __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, c
         // O^T += V^T P^T, 16 dims per product.
 #pragma unroll
         for (int c = 0; c < VC; c++) {
-            half4_t vt4;
-#pragma unroll
-            for (int j = 0; j < 4; j++) vt4[j] = my_vt[(4 * rg + j) * VROW + c * 16 + col];
             o[c] *= alpha;
-            o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, ph, o[c], 0, 0, 0);
-            o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl, o[c], 0, 0, 0);
+            ol[c] *= alpha;
+#pragma unroll
+            for (int b = 0; b < PB; b++) {
+                half4_t vt4;
+#pragma unroll
+                for (int j = 0; j < 4; j++) vt4[j] = my_vt[(b * kPage + 4 * rg + j) * VROW + c * 16 + col];
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, ph[b], o[c], 0, 0, 0);
+                ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl[b], ol[c], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (pg + W < pg_end) {
-#pragma unroll
-            for (int c = 0; c < QC; c++) kr[c] = kn[c];
-#pragma unroll
-            for (int i = 0; i < LPP; i++) vr[i] = vn[i];
-        }
+        if (pg + STRIDE < pg_end) cur = nxt;
     }
     // Lanes q, q+16, q+32, q+48 hold partial sums of query q's softmax.
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-    if (col < (int)it.nq) {
+    if (qok) {
         if (rg == 0) {
             red[wave][col][0] = m;
             red[wave][col][1] = lsum;
@@ -652,7 +678,8 @@ __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, c
 #pragma unroll
         for (int c = 0; c < VC; c++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) red[wave][col][2 + c * 16 + 4 * rg + j] = o[c][j];
+            for (int j = 0; j < 4; j++)
+                red[wave][col][2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * kPUnscale;
     }
     __syncthreads();
     for (uint32_t t = threadIdx.x; t < it.nq * D; t += 64 * W) {
@@ -710,6 +737,10 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(const AttnLaunch a, const
 
 constexpr int kWaves = NI_ATTN_WAVES;
 constexpr int kPagesPerIter = NI_ATTN_PAGES;
+#ifndef NI_MFMA_PAGES
+#define NI_MFMA_PAGES 1
+#endif
+constexpr int kMfmaPages = NI_MFMA_PAGES;  // pages per wave iteration of the matrix-core kernel
 
 // Launch `kern<INL>` with the plan inline (kInlinePlanBytes of arguments) or
 // through the device pointer in the launch struct.
@@ -764,11 +795,11 @@ hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         if (a.napp_total || a.n_orphan_blocks)
-            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, true, INL>), dim3((uint32_t)blocks), dim3(64 * kWaves), 0,
-                               s, a, pa);
+            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, kMfmaPages, true, INL>), dim3((uint32_t)blocks),
+                               dim3(64 * kWaves), 0, s, a, pa);
         else
-            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, false, INL>), dim3((uint32_t)blocks), dim3(64 * kWaves), 0,
-                               s, a, pa);
+            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, kMfmaPages, false, INL>), dim3((uint32_t)blocks),
+                               dim3(64 * kWaves), 0, s, a, pa);
         return hipGetLastError();
     });
 }
