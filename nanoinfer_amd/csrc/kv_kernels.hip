@@ -806,16 +806,24 @@ hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
 
 template <int D>
 hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
+#define NI_NQ_CASE(N) \
+    case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s) : attn_launch_t<D, N>(a, ip, ib, s);
+#if NI_ATTN_MFMA
+    // Groups of several rows always take the 16-row matrix tile.
     if (a.nq_tile == kMfmaTile)
         return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s) : mfma_launch_t<D>(a, ip, ib, s);
     switch (a.nq_tile) {
-#define NI_NQ_CASE(N) \
-    case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s) : attn_launch_t<D, N>(a, ip, ib, s);
-        NI_NQ_CASE(1) NI_NQ_CASE(2) NI_NQ_CASE(3) NI_NQ_CASE(4)
-        NI_NQ_CASE(5) NI_NQ_CASE(6) NI_NQ_CASE(7) NI_NQ_CASE(8)
-#undef NI_NQ_CASE
+        NI_NQ_CASE(1)
         default: return hipErrorInvalidValue;
     }
+#else
+    switch (a.nq_tile) {
+        NI_NQ_CASE(1) NI_NQ_CASE(2) NI_NQ_CASE(3) NI_NQ_CASE(4)
+        NI_NQ_CASE(5) NI_NQ_CASE(6) NI_NQ_CASE(7) NI_NQ_CASE(8)
+        default: return hipErrorInvalidValue;
+    }
+#endif
+#undef NI_NQ_CASE
 }
 
 hipError_t attn_dispatch(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
