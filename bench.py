@@ -96,6 +96,7 @@ def calibrate_copy():
 
 # ------------------------------------------------------------------ config 3
 
+SPEC_WINDOW = 64  # config 5: rows a sequence may grow past its drawn context before it restarts
 CFG3 = dict(max_batch=64, prompt=(32, 512), out=(16, 256), rate=1.0, budget=256, max_rows=512, n_ctx=1024)
 
 
@@ -453,21 +454,23 @@ def run_config4(args):
 def run_config5(args):
     """Config 5: speculative verify, 32 sequences with contexts U[128,1024];
     each step appends g + 4 drafts (5 rows, 5 causal queries per sequence),
-    accepts U[0,4] and truncates to tlen + 1 + accepted."""
+    accepts U[0,4] and truncates to tlen + 1 + accepted.  A sequence that
+    has grown SPEC_WINDOW rows past its drawn context goes back to it, so
+    any number of steps stays at the drawn contexts."""
     import torch
 
     import nanoinfer_amd as na
     from nanoinfer_amd import workloads
 
     ctx, _ = workloads.config5_contexts()
-    n_ctx = 2048  # room for the contexts to grow over the timed steps
+    n_ctx = 2048
     kv = na.PagedKv(na.BatchOpts(**workloads.GPT2, kv_blocks=32 * n_ctx // 16, max_seqs=32, n_ctx=n_ctx))
     c = 768
     g = torch.Generator(device="cuda").manual_seed(args.seed)
     seqs = [kv.add_seq() for _ in ctx]
     for s, L in zip(seqs, ctx):
         _fill(kv, s, L, c, 12, 1.0, 512, g)
-    spec = workloads.SpecVerify(kv, seqs, k=4, seed=args.seed)
+    spec = workloads.SpecVerify(kv, seqs, k=4, seed=args.seed, window=SPEC_WINDOW)
     n = 5 * len(seqs)
     q, k, v = (torch.randn((12, n, c), device="cuda", generator=g) for _ in range(3))
     out = torch.zeros_like(q)
@@ -488,7 +491,7 @@ def run_config5(args):
     args_w.warmup = 0
     t, prof = _timed_steps(kv, args_w, one_step)
     return _result(args, "config5: spec verify, 32 seqs, ctx U[128,1024], append g + 4 drafts, 5 causal queries, "
-                         "accept U[0,4], truncate", {"draft_k": 4}, t, prof, acc_bytes[0] / args.steps,
+                         "accept U[0,4], truncate", {"draft_k": 4, "reset_window": SPEC_WINDOW}, t, prof, acc_bytes[0] / args.steps,
                    acc_bytes[1] / args.steps, 12)
 
 

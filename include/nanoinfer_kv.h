@@ -154,6 +154,20 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
                int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
                int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream);
 
+/* Batch::decode_resident's KV part (batch.rs:322-363): `steps` decode steps
+ * of the sequences seqs[0..n), enqueued at once with no host wait.  Pages
+ * for every step are reserved first (each sequence to seq_len + steps; the
+ * reference's errors, nothing enqueued on error); step t then appends one
+ * row per sequence at position seq_len + t and runs its attention, and
+ * seq_len += 1 after each step.  Row i of step t, layer l is at
+ * base + t*step_stride + l*layer_stride + i*row_stride in q/k/v (out with
+ * the out_ strides).  In a model, step t's q/k/v come from step t-1's
+ * output; here the caller provides them. */
+int ni_kv_decode_steps(ni_kv* kv, const uint32_t* seqs, uint32_t n, uint32_t steps, const float* q, const float* k,
+                       const float* v, int64_t row_stride, int64_t layer_stride, int64_t step_stride, float* out,
+                       int64_t out_row_stride, int64_t out_layer_stride, int64_t out_step_stride,
+                       uint32_t split_tokens, ni_stream stream);
+
 /* Wait for all work this handle enqueued on `stream`. */
 int ni_kv_sync(ni_kv* kv, ni_stream stream);
 

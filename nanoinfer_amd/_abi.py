@@ -102,6 +102,9 @@ def _declare(L):
                                             _i64, _u32, _vp]
     L.ni_kv_step.restype = C.c_int
     L.ni_kv_step.argtypes = [_vp, C.POINTER(ni_work), _u32, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _u32, _vp]
+    L.ni_kv_decode_steps.restype = C.c_int
+    L.ni_kv_decode_steps.argtypes = [_vp, C.POINTER(_u32), _u32, _u32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
+                                     _i64, _u32, _vp]
     L.ni_kv_sync.restype = C.c_int
     L.ni_kv_sync.argtypes = [_vp, _vp]
     L.ni_kv_pools.restype = C.c_int

@@ -15,6 +15,7 @@ reference              here                                        batch.rs
 ``free_block_count``   ``free_block_count()``                      :238-240
 ``ensure_blocks``      ``reserve(s, len)``                         :243-254
 ``step``               ``step(work, q, k, v, out)``                :259-315
+``decode_resident``    ``decode_steps(seqs, q, k, v, out)``        :322-363
 ``kv_block_bytes``     ``kv_block_bytes()``                        :107-109
 =====================  ==========================================  ==================
 
@@ -254,6 +255,26 @@ class PagedKv:
         op, ors, ols = _f32_arg(out, "out", True)
         self._check(self._L.ni_kv_step(self._h, wp, w.shape[0], qp, kp, vp, rs, ls, op, ors, ols, split_tokens,
                                        _stream_ptr(stream)))
+        return out
+
+    def decode_steps(self, seqs, q, k, v, out=None, split_tokens: int = 0, stream=None):
+        """decode_resident's KV part: q/k/v are [steps, n_layer, len(seqs), C];
+        step t appends and attends position seq_len + t of every sequence."""
+        import torch
+
+        s = np.ascontiguousarray(np.asarray(seqs, dtype=np.uint32).reshape(-1))
+        sp = s.ctypes.data_as(C.POINTER(C.c_uint32))
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32 or t.dim() != 4 \
+                    or t.stride(3) != 1:
+                raise ValueError(f"{name} must be a float32 CUDA tensor [steps, n_layer, rows, C] with unit stride in C")
+        if not (q.stride() == k.stride() == v.stride()) or not (q.shape == k.shape == v.shape):
+            raise ValueError("q, k and v must share shapes and strides")
+        if out is None:
+            out = torch.zeros_like(q)
+        self._check(self._L.ni_kv_decode_steps(self._h, sp, s.size, q.shape[0], q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                               q.stride(2), q.stride(1), q.stride(0), out.data_ptr(), out.stride(2),
+                                               out.stride(1), out.stride(0), split_tokens, _stream_ptr(stream)))
         return out
 
     def sync(self, stream=None):

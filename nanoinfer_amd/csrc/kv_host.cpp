@@ -8,9 +8,11 @@
 //
 // Each data-path call builds a compact plan (kv_plan.h) from its rows -- the
 // destination slot of every appended row, attention work items sorted
-// longest first, merge items, and the page lists those items read -- copies
-// it into a pinned staging slot, uploads it with one async copy on the
-// caller's stream and launches the kernels over it.  Staging slots are
+// longest first, merge items, and the page lists those items read -- and
+// launches the kernels over it.  A plan of up to 32 KB travels inside the
+// kernel arguments (the runtime copies them with the dispatch); a larger one
+// is copied into a pinned staging slot and uploaded on the handle's copy
+// stream, the caller's stream waiting on an event.  Staging slots are
 // recycled through events, so bookkeeping calls after a data call never
 // race with the work it enqueued.
 #include <hip/hip_runtime_api.h>
@@ -548,6 +550,10 @@ void reset_plan(ni_kv* kv) {
 
 }  // namespace
 
+static int enqueue_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
+                        const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
+                        int64_t out_layer_stride, uint32_t split_tokens, hipStream_t stream);
+
 // ============================================================= C ABI
 
 extern "C" {
@@ -903,6 +909,66 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
     }
     if (n_rows > kv->o.max_rows)
         return kv->fail(NI_ERR_TOO_MANY_ROWS, "%llu rows > max_rows %u", (unsigned long long)n_rows, kv->o.max_rows);
+    return enqueue_step(kv, work, n_work, q, k, v, row_stride, layer_stride, out, out_row_stride, out_layer_stride,
+                        split_tokens, (hipStream_t)stream);
+}
+
+int ni_kv_decode_steps(ni_kv* kv, const uint32_t* seqs, uint32_t n, uint32_t steps, const float* q, const float* k,
+                       const float* v, int64_t row_stride, int64_t layer_stride, int64_t step_stride, float* out,
+                       int64_t out_row_stride, int64_t out_layer_stride, int64_t out_step_stride,
+                       uint32_t split_tokens, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    if (n == 0 || steps == 0) return NI_OK;
+    if (!seqs) return kv->fail(NI_ERR_BAD_ARG, "seqs is NULL");
+    // batch.rs:335-337
+    if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "batch %u too large", n);
+    if (step_stride % 4 || out_step_stride % 4)
+        return kv->fail(NI_ERR_BAD_ARG, "step strides must be multiples of 4 floats");
+    for (const char* name : {"q", "k", "v", "out"}) {
+        const bool is_out = name[0] == 'o';
+        const void* p = name[0] == 'q' ? (const void*)q : name[0] == 'k' ? (const void*)k
+                      : name[0] == 'v' ? (const void*)v : (const void*)out;
+        if (int rc = check_f32_operand(kv, name, p, is_out ? out_row_stride : row_stride,
+                                       is_out ? out_layer_stride : layer_stride, true))
+            return rc;
+    }
+    if (++kv->step_stamp == 0) {
+        std::fill(kv->step_mark.begin(), kv->step_mark.end(), 0u);
+        kv->step_stamp = 1;
+    }
+    // batch.rs:341-349: every sequence's pages for all steps first; an error
+    // leaves earlier sequences' pages reserved, as the reference does.
+    for (uint32_t i = 0; i < n; i++) {
+        const uint32_t s = seqs[i];
+        if (int rc = check_seq(kv, s)) return rc;
+        if (!kv->live[s]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", s);
+        if (kv->step_mark[s] == kv->step_stamp)
+            return kv->fail(NI_ERR_BAD_ARG, "sequence %u appears twice in one call", s);
+        kv->step_mark[s] = kv->step_stamp;
+        if (int rc = ensure_pages(kv, s, (uint64_t)kv->seq_len[s] + steps)) return rc;
+    }
+    // batch.rs:351-357: every step enqueued at once; step t appends and
+    // attends position seq_len + t of each sequence.
+    std::vector<ni_work> work(n);
+    for (uint32_t i = 0; i < n; i++) work[i] = ni_work{seqs[i], 1, 1};
+    for (uint32_t t = 0; t < steps; t++) {
+        const int64_t o = (int64_t)t * step_stride, oo = (int64_t)t * out_step_stride;
+        if (int rc = enqueue_step(kv, work.data(), n, q + o, k + o, v + o, row_stride, layer_stride, out + oo,
+                                  out_row_stride, out_layer_stride, split_tokens, (hipStream_t)stream))
+            return rc;
+    }
+    return NI_OK;
+}
+
+}  // extern "C"
+
+// The launch half of ni_kv_step: lay out the validated, reserved work's rows,
+// plan, launch, and commit seq_len += n_new (batch.rs:270).
+static int enqueue_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
+                        const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
+                        int64_t out_layer_stride, uint32_t split_tokens, hipStream_t stream) {
+    reset_plan(kv);
     // Fuse the append into the attention launch when every sequence has a
     // single query group: then exactly one workgroup per (layer, head, page)
     // touches this step's new rows.
@@ -925,12 +991,14 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
     }
     if (int rc = plan_attention(kv, split_tokens, kv->o.n_layer)) return rc;
     int rc = run_plan(kv, 0, kv->o.n_layer, k, v, row_stride, layer_stride, q, row_stride, layer_stride, out,
-                      out_row_stride, out_layer_stride, (hipStream_t)stream);
+                      out_row_stride, out_layer_stride, stream);
     if (rc) return rc;
     // batch.rs:270: the step's rows now belong to their sequences.
     for (uint32_t w = 0; w < n_work; w++) kv->seq_len[work[w].seq] += work[w].n_new;
     return NI_OK;
 }
+
+extern "C" {
 
 int ni_kv_sync(ni_kv* kv, ni_stream stream) {
     if (!kv) return NI_ERR_BAD_ARG;

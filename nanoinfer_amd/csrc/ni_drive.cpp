@@ -1,0 +1,85 @@
+// ni_drive -- command-line front end of ni_drive_run (nanoinfer_drivers.h):
+// the config-3 continuous-batching trace (`serve`) or the config-5 verify
+// loop (`spec`) on the device, launched per step or per layer, printed as
+// one JSON line.
+//
+//   ni_drive [serve|spec] [--per-layer] [--steps K] [--warmup W] [--split T]
+//            [--all-prompt-rows] [--seed S]
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "nanoinfer_drivers.h"
+
+static uint32_t pages(uint32_t n) { return (n + NI_KV_BLOCK - 1) / NI_KV_BLOCK; }
+
+int main(int argc, char** argv) {
+    ni_drive_opts o{};
+    std::string workload = "serve";
+    o.launch = NI_DRIVE_STEP;
+    o.steps = 2000;
+    o.warmup = 300;
+    o.data_seed = 7;
+    o.serve = ni_serve_opts{7, 1.0, 100000, 64, 32, 512, 16, 256, 256, 512, 0};
+    for (int i = 1; i < argc; i++) {
+        const char* a = argv[i];
+        auto val = [&](const char* name) -> const char* {
+            if (i + 1 >= argc) {
+                fprintf(stderr, "ni_drive: %s needs a value\n", name);
+                exit(2);
+            }
+            return argv[++i];
+        };
+        if (!strcmp(a, "serve") || !strcmp(a, "spec")) workload = a;
+        else if (!strcmp(a, "--per-layer")) o.launch = NI_DRIVE_PER_LAYER;
+        else if (!strcmp(a, "--all-prompt-rows")) o.serve.query_all_prompt_rows = 1;
+        else if (!strcmp(a, "--steps")) o.steps = (uint32_t)atoi(val(a));
+        else if (!strcmp(a, "--warmup")) o.warmup = (uint32_t)atoi(val(a));
+        else if (!strcmp(a, "--split")) o.split_tokens = (uint32_t)atoi(val(a));
+        else if (!strcmp(a, "--seed")) o.data_seed = o.serve.seed = strtoull(val(a), nullptr, 10);
+        else {
+            fprintf(stderr, "usage: ni_drive [serve|spec] [--per-layer] [--steps K] [--warmup W] [--split T] "
+                            "[--all-prompt-rows] [--seed S]\n");
+            return 2;
+        }
+    }
+    o.kv.n_layer = 12;
+    o.kv.n_head = 12;
+    o.kv.head_dim = 64;
+    if (workload == "serve") {
+        // metal_serve.rs:485: max_batch * pages(prompt_max + out_max) + 8 pages.
+        o.workload = NI_DRIVE_SERVE;
+        o.kv.kv_pages = o.serve.max_batch * pages(o.serve.prompt_max + o.serve.out_max) + 8;
+        o.kv.max_seqs = o.serve.max_batch;
+        o.kv.max_ctx = 1024;
+        o.kv.max_rows = o.serve.max_rows;
+    } else {
+        o.workload = NI_DRIVE_SPEC;
+        o.spec_seqs = 32;
+        o.spec_ctx_min = 128;
+        o.spec_ctx_max = 1024;
+        o.spec_k = 4;
+        o.spec_seed = 5;
+        o.spec_window = 64;
+        o.kv.max_ctx = 2048;
+        o.kv.kv_pages = o.spec_seqs * pages(o.kv.max_ctx);
+        o.kv.max_seqs = o.spec_seqs;
+        o.kv.max_rows = 512;
+    }
+    ni_drive_result r{};
+    if (int rc = ni_drive_run(&o, &r)) {
+        fprintf(stderr, "ni_drive: %s (status %d)\n", ni_drive_last_error(), rc);
+        return 1;
+    }
+    const double gbs = r.bytes / r.seconds / 1e9;
+    printf("{\"driver\": \"ni_drive\", \"workload\": \"%s\", \"launch\": \"%s\", \"steps\": %u, \"warmup\": %u, "
+           "\"value\": %.2f, \"unit\": \"GB/s\", \"pct_of_peak\": %.2f, \"ms_per_step\": %.5f, "
+           "\"gpu_ms_per_step\": %.5f, \"host_us_per_step\": %.1f, \"abi_calls_per_step\": %.1f, "
+           "\"seq_tokens_per_s\": %.1f, \"algorithmic_bytes_per_step\": %.0f, \"mean_live\": %.2f, "
+           "\"mean_context\": %.1f}\n",
+           workload.c_str(), o.launch == NI_DRIVE_STEP ? "step" : "per-layer", r.steps, o.warmup, gbs,
+           100.0 * gbs / 8000.0, r.seconds / r.steps * 1e3, r.gpu_seconds / r.steps * 1e3, r.host_us_per_step,
+           (double)r.launches / r.steps, r.seq_tokens / r.seconds, r.bytes / r.steps, r.mean_live, r.mean_context);
+    return 0;
+}

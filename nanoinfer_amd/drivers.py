@@ -1,0 +1,166 @@
+"""ctypes binding of ``include/nanoinfer_drivers.h``: the C++ restatements
+of the reference's serving harnesses (``metal_serve.rs:255-363``,
+``metal_spec.rs:118-169``) over the KV C ABI, and ``ni_drive_run``.
+
+``Serve`` and ``Spec`` drive a :class:`~nanoinfer_amd.batch.PagedKv` (a
+device handle or a host-only one); :func:`drive` runs a whole synthetic
+workload on the device with the C++ host loop.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from . import _abi
+from . import build as _build
+
+_lib = None
+_vp = C.c_void_p
+_u32 = C.c_uint32
+
+
+class ni_serve_opts(C.Structure):
+    _fields_ = [("seed", C.c_uint64), ("rate", C.c_double), ("n_requests", _u32), ("max_batch", _u32),
+                ("prompt_min", _u32), ("prompt_max", _u32), ("out_min", _u32), ("out_max", _u32),
+                ("budget", _u32), ("max_rows", _u32), ("query_all_prompt_rows", _u32)]
+
+
+class ni_serve_iter(C.Structure):
+    _fields_ = [("work", C.POINTER(_abi.ni_work)), ("n_work", _u32), ("ctx_after", C.POINTER(_u32)),
+                ("admitted", C.POINTER(_u32)), ("n_admitted", _u32), ("retired", C.POINTER(_u32)),
+                ("n_retired", _u32)]
+
+
+class ni_drive_opts(C.Structure):
+    _fields_ = [("workload", _u32), ("launch", _u32), ("kv", _abi.ni_kv_opts), ("serve", ni_serve_opts),
+                ("spec_seqs", _u32), ("spec_ctx_min", _u32), ("spec_ctx_max", _u32), ("spec_k", _u32),
+                ("spec_seed", C.c_uint64), ("spec_window", _u32), ("warmup", _u32), ("steps", _u32),
+                ("split_tokens", _u32), ("data_seed", C.c_uint64)]
+
+
+class ni_drive_result(C.Structure):
+    _fields_ = [("seconds", C.c_double), ("gpu_seconds", C.c_double), ("bytes", C.c_double),
+                ("seq_tokens", C.c_double), ("host_us_per_step", C.c_double), ("steps", _u32),
+                ("launches", C.c_uint64), ("mean_live", C.c_double), ("mean_context", C.c_double)]
+
+
+NI_DRIVE_SERVE, NI_DRIVE_SPEC = 0, 1
+NI_DRIVE_STEP, NI_DRIVE_PER_LAYER = 0, 1
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    _abi.lib()  # the KV library first (the drivers link against it)
+    if not os.path.exists(_build.DRIVERS_LIB):
+        _build.build()
+    L = C.CDLL(_build.DRIVERS_LIB)
+    L.ni_serve_create.argtypes = [_vp, C.POINTER(ni_serve_opts), C.POINTER(_vp)]
+    L.ni_serve_destroy.argtypes = [_vp]
+    L.ni_serve_destroy.restype = None
+    L.ni_serve_plan.argtypes = [_vp, C.POINTER(ni_serve_iter)]
+    L.ni_serve_commit.argtypes = [_vp]
+    L.ni_serve_done.argtypes = [_vp]
+    L.ni_serve_done.restype = _u32
+    L.ni_spec_create.argtypes = [_vp, C.POINTER(_u32), _u32, _u32, C.c_uint64, C.POINTER(_vp)]
+    L.ni_spec_destroy.argtypes = [_vp]
+    L.ni_spec_destroy.restype = None
+    L.ni_spec_plan.argtypes = [_vp, C.POINTER(C.POINTER(_abi.ni_work)), C.POINTER(_u32), C.POINTER(C.POINTER(_u32))]
+    L.ni_spec_commit.argtypes = [_vp, C.POINTER(C.POINTER(_u32))]
+    L.ni_spec_set_window.argtypes = [_vp, _u32]
+    L.ni_drive_run.argtypes = [C.POINTER(ni_drive_opts), C.POINTER(ni_drive_result)]
+    L.ni_drive_last_error.restype = C.c_char_p
+    L.ni_drive_last_error.argtypes = []
+    _lib = L
+    return L
+
+
+def declared_functions() -> list[str]:
+    import re
+
+    text = open(os.path.join(_build.INCLUDE, "nanoinfer_drivers.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ni_[a-z0-9_]+)\s*\(", text)))
+
+
+def _work(ptr, n) -> np.ndarray:
+    return np.asarray([(ptr[i].seq, ptr[i].n_new, ptr[i].n_query) for i in range(n)], np.uint32).reshape(-1, 3)
+
+
+def _check(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what}: {lib().ni_drive_last_error().decode()} (status {rc})")
+
+
+class Serve:
+    """ni_serve over a PagedKv handle: plan() -> (work, ctx_after, admitted,
+    retired); commit() after the step ran."""
+
+    def __init__(self, kv, seed=7, rate=1.0, n_requests=100000, max_batch=64, prompt=(32, 512), out=(16, 256),
+                 budget=256, max_rows=512, query_all_prompt_rows=False):
+        L = lib()
+        o = ni_serve_opts(seed, rate, n_requests, max_batch, prompt[0], prompt[1], out[0], out[1], budget, max_rows,
+                          int(query_all_prompt_rows))
+        h = _vp()
+        _check(L.ni_serve_create(kv.handle, C.byref(o), C.byref(h)), "ni_serve_create")
+        self._h, self._L, self.kv = h, L, kv
+
+    def plan(self):
+        it = ni_serve_iter()
+        _check(self._L.ni_serve_plan(self._h, C.byref(it)), "ni_serve_plan")
+        work = _work(it.work, it.n_work)
+        ctx = np.asarray([it.ctx_after[i] for i in range(it.n_work)], np.int64)
+        adm = [int(it.admitted[i]) for i in range(it.n_admitted)]
+        ret = [int(it.retired[i]) for i in range(it.n_retired)]
+        return work, ctx, adm, ret
+
+    def commit(self):
+        _check(self._L.ni_serve_commit(self._h), "ni_serve_commit")
+
+    def done(self) -> int:
+        return int(self._L.ni_serve_done(self._h))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self._L.ni_serve_destroy(self._h)
+            self._h = None
+
+
+class Spec:
+    """ni_spec over a PagedKv handle."""
+
+    def __init__(self, kv, seqs, k=4, seed=55, window=0):
+        L = lib()
+        s = np.ascontiguousarray(np.asarray(seqs, np.uint32))
+        h = _vp()
+        _check(L.ni_spec_create(kv.handle, s.ctypes.data_as(C.POINTER(_u32)), s.size, k, seed, C.byref(h)),
+               "ni_spec_create")
+        self._h, self._L, self.kv, self.n = h, L, kv, s.size
+        _check(L.ni_spec_set_window(h, window), "ni_spec_set_window")
+
+    def plan(self):
+        w = C.POINTER(_abi.ni_work)()
+        n = _u32()
+        ctx = C.POINTER(_u32)()
+        _check(self._L.ni_spec_plan(self._h, C.byref(w), C.byref(n), C.byref(ctx)), "ni_spec_plan")
+        return _work(w, n.value), np.asarray([ctx[i] for i in range(n.value)], np.int64)
+
+    def commit(self):
+        acc = C.POINTER(_u32)()
+        _check(self._L.ni_spec_commit(self._h, C.byref(acc)), "ni_spec_commit")
+        return [int(acc[i]) for i in range(self.n)]
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self._L.ni_spec_destroy(self._h)
+            self._h = None
+
+
+def drive(opts: ni_drive_opts) -> dict:
+    """ni_drive_run: a whole synthetic run on the device (C++ host loop)."""
+    r = ni_drive_result()
+    _check(lib().ni_drive_run(C.byref(opts), C.byref(r)), "ni_drive_run")
+    return {f: getattr(r, f) for f, _ in ni_drive_result._fields_}

@@ -254,9 +254,16 @@ class SpecVerify:
     [g, d1..dk] (k+1 rows, all queried) to every sequence, then keeps
     g + acc accepted drafts with acc ~ U[0, k] (seeded) and truncates."""
 
-    def __init__(self, kv, seqs, k: int = 4, seed: int = 55):
+    def __init__(self, kv, seqs, k: int = 4, seed: int = 55, window=None):
+        """``window``: once a sequence has grown more than ``window`` rows
+        past its context at construction, it is truncated back to that
+        context after the round (a request ends and the next one with the
+        same prompt length takes its slot), so a long run stays at the
+        drawn contexts.  None: sequences grow without bound."""
         self.kv, self.seqs, self.k = kv, list(seqs), k
         self.rng = XorShift.seeded(seed)
+        self.window = window
+        self._base = [kv.seq_len(s) for s in self.seqs]
         self._tlen = None
 
     def plan(self) -> Step:
@@ -269,8 +276,10 @@ class SpecVerify:
         """Roll back the rejected drafts: truncate(seq, tlen + 1 + acc).
         Returns the accepted counts."""
         accs = []
-        for s, t in zip(self.seqs, self._tlen):
+        for s, t, b in zip(self.seqs, self._tlen, self._base):
             acc = self.rng.range(0, self.k)
             self.kv.truncate(s, t + 1 + acc)
+            if self.window is not None and t + 1 + acc > b + self.window:
+                self.kv.truncate(s, b)
             accs.append(acc)
         return accs
