@@ -12,12 +12,17 @@ and budgeted prefill chunks) and run decode attention for every running
 sequence (the last prompt row of a finished prefill included).  The first
 W steps (the ramp-up) are warmup; K steps are timed.
 
-Prints ONE JSON line.  ``value`` is algorithmic HBM bytes per second over the
-timed steps (bytes formula in nanoinfer_amd/workloads.py, each KV byte once
-per step); ``roofline`` prices the attention kernel alone, timed by HIP
-events the library records around each of its launches on the caller's
-stream; ``cpu_baseline`` times the oracle's restatement of the reference's
-CPU path (threaded, paged) on a bounded sample of the same trace.
+The host loop is the C++ serving driver (ni_drive_run: the scheduler of
+metal_serve.rs restated in C++, calling the C ABI), as a compiled caller of
+the library runs it.  Prints ONE JSON line.  ``value`` is algorithmic HBM
+bytes per second over the timed steps (bytes formula in
+nanoinfer_amd/workloads.py, each KV byte once per step), from a run without
+per-launch events; ``roofline`` prices the attention launch alone, timed by
+HIP events the library records around each of its launches on the caller's
+stream in a second run of the same trace; ``per_layer_launches`` runs the
+trace a third time through per-layer append + attention calls, the way the
+reference dispatches; ``cpu_baseline`` times the oracle's restatement of the
+reference's CPU path (threaded, paged) on a bounded sample of the same trace.
 """
 from __future__ import annotations
 
@@ -70,7 +75,8 @@ def parse():
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = automatic)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (0 = skip)")
     ap.add_argument("--threads", type=int, default=0, help="CPU baseline threads (0 = min(cpus, 16))")
-    ap.add_argument("--no-profile", action="store_true", help="time without the per-launch HIP events")
+    ap.add_argument("--no-profile", action="store_true", help="skip the run timed by per-launch HIP events")
+    ap.add_argument("--skip-per-layer", action="store_true", help="config 3: skip the per-layer launch run")
     ap.add_argument("--seed", type=int, default=7)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only plain 256 MiB device copies (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -137,39 +143,6 @@ def cfg3_trace(n_steps, seed):
     return steps
 
 
-def replay_gpu(kv, steps, bufs, split, profile):
-    """Run steps on the device handle; returns (seconds, attention ms, attention launches)."""
-    import torch
-
-    q, k, v, out = bufs
-    if profile:
-        kv.profile([1])  # the attention launch only: events around every launch cost time
-        for kid in range(3):
-            kv.profile_read(kid)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    in_step = 0.0
-    for st in steps:
-        for s in st.retire:
-            kv.free_seq(s)
-        for s in st.admit:
-            got = kv.add_seq()
-            assert got == s, (got, s)
-        t1 = time.perf_counter()
-        kv.step(st.work, q, k, v, out=out, split_tokens=split)
-        in_step += time.perf_counter() - t1
-    t_loop = time.perf_counter() - t0
-    torch.cuda.synchronize()
-    t = time.perf_counter() - t0
-    log(f"bench: host loop {t_loop / len(steps) * 1e6:.1f} us/step (inside ni_kv_step {in_step / len(steps) * 1e6:.1f}), "
-        f"wall {t / len(steps) * 1e6:.1f} us/step")
-    prof = None
-    if profile:
-        prof = {name: kv.profile_read(i) for i, name in enumerate(["append", "attention", "merge"])}
-        kv.profile([])
-    return t, prof
-
-
 def cpu_baseline_cfg3(steps, warmup, seconds, threads):
     """The oracle's restatement of the reference CPU path on the same trace:
     warmup steps append only (untimed), then whole steps until `seconds`."""
@@ -227,90 +200,86 @@ def cpu_baseline_cfg3(steps, warmup, seconds, threads):
     return {"seconds": t_cpu, "bytes": done_bytes, "tokens": done_tokens, "steps": n_timed, "threads": runner.threads}
 
 
-def run_config3(args):
-    import torch
+def _drive(name, args, launch=None, profile_mask=0):
+    """One ni_drive_run of a preset: the C++ driver's host loop (the
+    scheduler, ni_kv_step and its bookkeeping) with inputs resident in HBM."""
+    from nanoinfer_amd import drivers
 
-    import nanoinfer_amd as na
-    from nanoinfer_amd import workloads
+    launch = drivers.NI_DRIVE_STEP if launch is None else launch
+    o = drivers.preset(name, args.steps, args.warmup, launch=launch, split=args.split, seed=args.seed,
+                       profile_mask=profile_mask)
+    r = drivers.drive(o)
+    gbs = r["bytes"] / r["seconds"] / 1e9
+    log(f"bench: {name} launch {launch}{' (profiled)' if profile_mask else ''}: {gbs:.1f} GB/s, "
+        f"{r['seconds'] / r['steps'] * 1e6:.1f} us/step, host {r['host_us_per_step']:.1f} us/step")
+    return r
 
-    n_total = args.warmup + args.steps
-    log(f"bench: planning {n_total} steps of the config-3 trace")
-    steps = cfg3_trace(n_total, args.seed)
-    opts = cfg3_opts()
-    kv = na.PagedKv(opts)
-    c = opts.n_head * opts.head_dim
-    g = torch.Generator(device="cuda").manual_seed(args.seed)
-    shape = (opts.n_layer, CFG3["max_rows"], c)
-    q = torch.randn(shape, device="cuda", generator=g)
-    k = torch.randn(shape, device="cuda", generator=g)
-    v = torch.randn(shape, device="cuda", generator=g)
-    out = torch.zeros(shape, device="cuda")
-    bufs = (q, k, v, out)
-    log(f"bench: warmup {args.warmup} steps")
-    replay_gpu(kv, steps[: args.warmup], bufs, args.split, profile=False)
-    log(f"bench: timing {args.steps} steps")
-    t, prof = replay_gpu(kv, steps[args.warmup:], bufs, args.split, profile=not args.no_profile)
-    timed = steps[args.warmup:]
-    tot = {"append": 0, "attention": 0, "total": 0, "seq_tokens": 0}
-    ctx_sum = 0
-    live_sum = 0
-    for st in timed:
-        b = workloads.step_bytes(st.work, st.ctx_after, opts.n_layer, c)
-        for key in tot:
-            tot[key] += b[key]
-        q_mask = st.work[:, 2] > 0
-        ctx_sum += int(st.ctx_after[q_mask].sum())
-        live_sum += int(q_mask.sum())
-    gbs = tot["total"] / t / 1e9
-    res = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(t / args.steps * 1e3, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "kv_dtype": "f16",
-        "data": "synthetic (seeded N(0,1) q/k/v, seeded Poisson trace)",
-        "config": {
-            "workload": "config3: continuous batching, 64 slots, Poisson arrivals 1/step, prompt U[32,512], "
-                        "output U[16,256], GPT-2 12x12x64, 16-token pages, 3080-page pool",
-            "n_layer": opts.n_layer, "n_head": opts.n_head, "head_dim": opts.head_dim,
-            "kv_pages": opts.kv_blocks, "max_batch": CFG3["max_batch"], "prefill_budget": CFG3["budget"],
-            "prefill_attention": "last prompt row only",
-            "split_tokens": args.split, "launches_per_step": "append + attention (+ merge when split), all layers",
-            "mean_live_seqs": round(live_sum / len(timed), 2),
-            "mean_context": round(ctx_sum / max(live_sum, 1), 1),
-            "algorithmic_bytes_per_step": int(tot["total"] / len(timed)),
-        },
-        "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
-        "seq_tokens_per_s": round(tot["seq_tokens"] / t, 1),
+
+def _line(args, r, workload, cfg, data):
+    """The JSON fields every workload shares, from an unprofiled run."""
+    gbs = r["bytes"] / r["seconds"] / 1e9
+    return {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(r["seconds"] / r["steps"] * 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "kv_dtype": "f16", "data": data,
+        "config": dict(workload=workload, **cfg), "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+        "seq_tokens_per_s": round(r["seq_tokens"] / r["seconds"], 1),
     }
-    if prof:
-        ms, n = prof["attention"]
+
+
+def _roofline(rp, kernel, with_merge):
+    """Algorithmic bytes of the profiled run / the attention (+ merge)
+    launches' event time."""
+    ms, n = rp["kernel_ms"][1], rp["kernel_launches"][1]
+    mm, mn = rp["kernel_ms"][2], rp["kernel_launches"][2]
+    kernel_ms = ms + (mm if with_merge else 0.0)
+    ach = rp["bytes"] / (kernel_ms / 1e3) / 1e9
+    out = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4),
+           "traffic": None, "kernel": kernel, "avg_launch_us": round(ms / n * 1e3, 3), "launches": n,
+           "algorithmic_bytes_per_launch": int(rp["bytes"] / n)}
+    if with_merge:
+        out["avg_merge_us"] = round(mm / mn * 1e3, 3) if mn else 0.0
+    return out
+
+
+def run_config3(args):
+    from nanoinfer_amd import drivers
+
+    r = _drive("config3", args)
+    res = _line(args, r, "config3: continuous batching, 64 slots, Poisson arrivals 1/step, prompt U[32,512], "
+                         "output U[16,256], GPT-2 12x12x64, 16-token pages, 3080-page pool",
+                dict(n_layer=12, n_head=12, head_dim=64, kv_pages=cfg3_pages(), max_batch=CFG3["max_batch"],
+                     prefill_budget=CFG3["budget"], prefill_attention="last prompt row only",
+                     split_tokens=args.split, host_loop="C++ driver (ni_drive_run: ni_serve + ni_kv_step)",
+                     launches_per_step="one ni_kv_step: append fused into the attention launch, all layers",
+                     mean_live_seqs=round(r["mean_live"], 2), mean_context=round(r["mean_context"], 1),
+                     algorithmic_bytes_per_step=int(r["bytes"] / r["steps"])),
+                "synthetic (seeded N(0,1) q/k/v resident in HBM, seeded Poisson request trace)")
+    if not args.no_profile:
         # ni_kv_step fuses the append into the attention launch whenever every
-        # sequence has one query group (always here): its bytes are then the
-        # step's append bytes too.
-        kbytes = tot["total"]
-        ach = kbytes / (ms / 1e3) / 1e9
-        res["roofline"] = {
-            "bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / PEAK_GBS, 4), "traffic": None,
-            "kernel": "attn_split_kernel<64,1,4,2,fused>", "avg_launch_us": round(ms / n * 1e3, 3), "launches": n,
-            "algorithmic_bytes_per_launch": int(kbytes / n),
-        }
+        # sequence has one query group (always here): the launch's bytes are
+        # the whole step's.
+        rp = _drive("config3", args, profile_mask=1 << 1)
+        res["roofline"] = _roofline(rp, "attn_split_kernel<64,1,4,2,fused>", with_merge=False)
         tr = measured_traffic()
         if tr:
             res["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
             res["roofline"]["traffic_vs_algorithmic"] = round(
                 tr["traffic_bytes_per_launch"] / tr["algorithmic_bytes_per_launch_same_steps"], 3)
             res["roofline"]["traffic_source"] = "profiles/attn_split_fused_config3.md (rocprofv3 --pmc, scaled)"
+    # The reference dispatches append and attention per layer; the same trace
+    # through ni_kv_append + ni_paged_decode_attention per layer.
+    if not args.skip_per_layer:
+        rl = _drive("config3", args, launch=drivers.NI_DRIVE_PER_LAYER)
+        gbs = rl["bytes"] / rl["seconds"] / 1e9
+        res["per_layer_launches"] = {"value": round(gbs, 2), "unit": "GB/s",
+                                     "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+                                     "ms_per_step": round(rl["seconds"] / rl["steps"] * 1e3, 5),
+                                     "abi_calls_per_step": round(rl["launches"] / rl["steps"], 1)}
     if args.cpu_seconds > 0:
         threads = args.threads or min(os.cpu_count() or 1, 16)
+        log(f"bench: planning the trace for the CPU baseline")
+        steps = cfg3_trace(args.warmup + args.steps, args.seed)
         log(f"bench: CPU baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
         cb = cpu_baseline_cfg3(steps, args.warmup, args.cpu_seconds, threads)
         res["cpu_baseline"] = {
@@ -325,174 +294,28 @@ def run_config3(args):
 
 # ------------------------------------------------- secondary configurations
 
-def _fill(kv, seq, length, c, n_layer, std, chunk, gen):
-    """Reserve and append positions 0..length-1 of `seq` with random K/V
-    (untimed set-up)."""
-    import torch
-
-    kv.reserve(seq, length)
-    for p0 in range(0, length, chunk):
-        n = min(chunk, length - p0)
-        kk = torch.randn((n_layer, n, c), device="cuda", generator=gen) * std
-        vv = torch.randn((n_layer, n, c), device="cuda", generator=gen) * std
-        kv.append([(seq, p) for p in range(p0, p0 + n)], kk, vv)
-    kv.commit(seq, length)
+SECONDARY = {
+    "config2": ("config2: 16 seqs, ctx U[64,1024], 1024-page pool, seeded page permutation, append 1 + attention, "
+                "GPT-2 12x12x64; each step rolled back", {}),
+    "config4": ("config4: batch 4, 32 heads x 128, context 32768, random page tables, 512-token partitions + LSE "
+                "merge, k/v ~ N(0, 0.5); each step rolled back", {"split_tokens": 512}),
+    "config5": ("config5: spec verify, 32 seqs, ctx U[128,1024], append g + 4 drafts, 5 causal queries, accept U[0,4], "
+                "truncate", {"draft_k": 4, "reset_window": SPEC_WINDOW}),
+}
 
 
-def _timed_steps(kv, args, one_step):
-    """Warm up, then time args.steps calls of one_step() with the attention
-    launch bracketed by the library's events."""
-    import torch
-
-    for _ in range(args.warmup):
-        one_step()
-    kv.profile([1])
-    for kid in range(3):
-        kv.profile_read(kid)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        one_step()
-    torch.cuda.synchronize()
-    t = time.perf_counter() - t0
-    prof = {name: kv.profile_read(i) for i, name in enumerate(["append", "attention", "merge"])}
-    kv.profile([])
-    return t, prof
-
-
-def _result(args, workload, cfg, t, prof, step_bytes, seq_tokens, n_layer):
-    gbs = step_bytes * args.steps / t / 1e9
-    ms, n = prof["attention"]
-    mm, mn = prof["merge"]
-    res = {"metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-           "warmup": args.warmup, "ms_per_step": round(t / args.steps * 1e3, 5), "higher_is_better": True,
-           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "kv_dtype": "f16",
-           "data": "synthetic (seeded normal q/k/v)", "config": dict(workload=workload, **cfg),
-           "pct_of_peak": round(100 * gbs / PEAK_GBS, 2), "seq_tokens_per_s": round(seq_tokens * args.steps / t, 1)}
-    if n:
-        kernel_s = (ms + mm) / 1e3
-        ach = step_bytes * args.steps / kernel_s / 1e9
-        res["roofline"] = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_GBS, "unit": "GB/s",
-                           "frac": round(ach / PEAK_GBS, 4), "traffic": None,
-                           "kernel": "attn_split_kernel (+ attn_merge_kernel when split)",
-                           "avg_launch_us": round(ms / n * 1e3, 3),
-                           "avg_merge_us": round(mm / mn * 1e3, 3) if mn else 0.0,
-                           "algorithmic_bytes_per_launch": int(step_bytes)}
+def run_secondary(args):
+    desc, cfg = SECONDARY[args.workload]
+    r = _drive(args.workload, args)
+    res = _line(args, r, desc, dict(cfg, mean_context=round(r["mean_context"], 1),
+                                    algorithmic_bytes_per_step=int(r["bytes"] / r["steps"]),
+                                    host_loop="C++ driver (ni_drive_run)"),
+                "synthetic (seeded normal q/k/v resident in HBM)")
+    if not args.no_profile:
+        rp = _drive(args.workload, args, profile_mask=(1 << 1) | (1 << 2))
+        res["roofline"] = _roofline(rp, "attn_split_kernel / attn_mfma_kernel (+ attn_merge_kernel when split)",
+                                    with_merge=True)
     return res
-
-
-def run_config2(args):
-    """Config 2: 16 sequences, contexts U[64,1024] (after the append), pages
-    from a seeded permutation of a 1024-page pool; one step appends a token
-    per sequence and runs attention.  Each timed step is rolled back
-    (truncate) so every step sees the same state."""
-    import torch
-
-    import nanoinfer_amd as na
-    from nanoinfer_amd import workloads
-
-    ctx, order = workloads.config2_contexts()
-    kv = na.PagedKv(na.BatchOpts(**workloads.GPT2, kv_blocks=1024, max_seqs=16, n_ctx=1024, page_order=order))
-    c = 768
-    g = torch.Generator(device="cuda").manual_seed(args.seed)
-    seqs = [kv.add_seq() for _ in ctx]
-    for s, L in zip(seqs, ctx):
-        _fill(kv, s, L - 1, c, 12, 1.0, 512, g)
-    n = len(seqs)
-    q, k, v = (torch.randn((12, n, c), device="cuda", generator=g) for _ in range(3))
-    out = torch.zeros_like(q)
-    work = [(s, 1, 1) for s in seqs]
-
-    def one_step():
-        kv.step(work, q, k, v, out=out, split_tokens=args.split)
-        for s, L in zip(seqs, ctx):
-            kv.truncate(s, L - 1)
-
-    t, prof = _timed_steps(kv, args, one_step)
-    b = workloads.step_bytes(np.asarray(work), np.asarray(ctx), 12, c)
-    return _result(args, "config2: 16 seqs, ctx U[64,1024], 1024-page pool, seeded page permutation, "
-                         "append 1 + attention, GPT-2 12x12x64", {"mean_context": float(np.mean(ctx))},
-                   t, prof, b["total"], b["seq_tokens"], 12)
-
-
-def run_config4(args):
-    """Config 4: batch 4, 32 heads x 128, context 32768, random page tables,
-    512-token partitions + LSE merge; q ~ N(0,1), k/v ~ N(0,0.5).  One step
-    appends a token per sequence (rolled back after each step)."""
-    import torch
-
-    import nanoinfer_amd as na
-    from nanoinfer_amd import workloads
-
-    B, L = 4, 32768
-    order = workloads.XorShift.seeded(4).permutation(B * L // 16)
-    kv = na.PagedKv(na.BatchOpts(**workloads.LONG, kv_blocks=B * L // 16, max_seqs=B, n_ctx=L, max_rows=4096,
-                                 page_order=order))
-    c = 4096
-    g = torch.Generator(device="cuda").manual_seed(args.seed)
-    seqs = [kv.add_seq() for _ in range(B)]
-    for s in seqs:
-        _fill(kv, s, L - 1, c, 1, 0.5, 4096, g)
-    q = torch.randn((1, B, c), device="cuda", generator=g)
-    k, v = (torch.randn((1, B, c), device="cuda", generator=g) * 0.5 for _ in range(2))
-    out = torch.zeros_like(q)
-    work = [(s, 1, 1) for s in seqs]
-    split = args.split or 512
-
-    def one_step():
-        kv.step(work, q, k, v, out=out, split_tokens=split)
-        for s in seqs:
-            kv.truncate(s, L - 1)
-
-    t, prof = _timed_steps(kv, args, one_step)
-    b = workloads.step_bytes(np.asarray(work), np.full(B, L), 1, c)
-    return _result(args, "config4: batch 4, 32 heads x 128, context 32768, random page tables, "
-                         "512-token partitions + LSE merge", {"split_tokens": split}, t, prof, b["total"],
-                   b["seq_tokens"], 1)
-
-
-def run_config5(args):
-    """Config 5: speculative verify, 32 sequences with contexts U[128,1024];
-    each step appends g + 4 drafts (5 rows, 5 causal queries per sequence),
-    accepts U[0,4] and truncates to tlen + 1 + accepted.  A sequence that
-    has grown SPEC_WINDOW rows past its drawn context goes back to it, so
-    any number of steps stays at the drawn contexts."""
-    import torch
-
-    import nanoinfer_amd as na
-    from nanoinfer_amd import workloads
-
-    ctx, _ = workloads.config5_contexts()
-    n_ctx = 2048
-    kv = na.PagedKv(na.BatchOpts(**workloads.GPT2, kv_blocks=32 * n_ctx // 16, max_seqs=32, n_ctx=n_ctx))
-    c = 768
-    g = torch.Generator(device="cuda").manual_seed(args.seed)
-    seqs = [kv.add_seq() for _ in ctx]
-    for s, L in zip(seqs, ctx):
-        _fill(kv, s, L, c, 12, 1.0, 512, g)
-    spec = workloads.SpecVerify(kv, seqs, k=4, seed=args.seed, window=SPEC_WINDOW)
-    n = 5 * len(seqs)
-    q, k, v = (torch.randn((12, n, c), device="cuda", generator=g) for _ in range(3))
-    out = torch.zeros_like(q)
-    acc_bytes = [0, 0]
-
-    def one_step():
-        st = spec.plan()
-        kv.step(st.work, q, k, v, out=out, split_tokens=args.split)
-        accs = spec.commit()
-        b = workloads.step_bytes(st.work, st.ctx_after, 12, c)
-        acc_bytes[0] += b["total"]
-        acc_bytes[1] += sum(a + 1 for a in accs)
-
-    for _ in range(args.warmup):
-        one_step()
-    acc_bytes[:] = [0, 0]
-    args_w = argparse.Namespace(**vars(args))
-    args_w.warmup = 0
-    t, prof = _timed_steps(kv, args_w, one_step)
-    return _result(args, "config5: spec verify, 32 seqs, ctx U[128,1024], append g + 4 drafts, 5 causal queries, "
-                         "accept U[0,4], truncate", {"draft_k": 4, "reset_window": SPEC_WINDOW}, t, prof, acc_bytes[0] / args.steps,
-                   acc_bytes[1] / args.steps, 12)
 
 
 def main():
@@ -510,8 +333,7 @@ def main():
         calibrate_copy()
         return
     # The headline line is config 3; the others are secondary measurements.
-    res = {"config3": run_config3, "config2": run_config2, "config4": run_config4,
-           "config5": run_config5}[args.workload](args)
+    res = run_config3(args) if args.workload == "config3" else run_secondary(args)
     print(json.dumps(res), flush=True)
 
 

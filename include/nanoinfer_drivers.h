@@ -92,7 +92,14 @@ int ni_spec_commit(ni_spec* s, const uint32_t** accepted);
 int ni_spec_set_window(ni_spec* s, uint32_t window);
 
 /* ---- a whole synthetic run on the device ---- */
-enum ni_drive_workload { NI_DRIVE_SERVE = 0, NI_DRIVE_SPEC = 1 };
+enum ni_drive_workload {
+    NI_DRIVE_SERVE = 0, /* ni_serve over the trace (config 3) */
+    NI_DRIVE_SPEC = 1,  /* ni_spec verify rounds (config 5) */
+    /* Fixed contexts (configs 2 and 4): sequence i holds fixed_ctx[i] - 1
+     * positions; every iteration appends one row to each and attends it,
+     * then truncates back, so every iteration does the same work. */
+    NI_DRIVE_FIXED = 2
+};
 enum ni_drive_launch {
     NI_DRIVE_STEP = 0,     /* one ni_kv_step per iteration (all layers per launch) */
     NI_DRIVE_PER_LAYER = 1 /* ni_kv_append + ni_paged_decode_attention per layer */
@@ -112,6 +119,10 @@ typedef struct ni_drive_opts {
     uint32_t steps;         /* timed iterations */
     uint32_t split_tokens;  /* 0 = automatic */
     uint64_t data_seed;     /* q/k/v contents */
+    const uint32_t* fixed_ctx; /* NI_DRIVE_FIXED: context of each sequence after the append */
+    uint32_t fixed_n;
+    float kv_std;           /* k/v data ~ N(0, kv_std^2); 0 = 1 (q is always N(0,1)) */
+    uint32_t profile_mask;  /* ni_kv_profile mask over the timed iterations; 0 = none */
 } ni_drive_opts;
 
 typedef struct ni_drive_result {
@@ -124,6 +135,8 @@ typedef struct ni_drive_result {
     uint64_t launches;      /* data-path ABI calls in the timed region */
     double mean_live;       /* mean queried sequences per iteration */
     double mean_context;    /* mean context of queried sequences */
+    double kernel_ms[3];    /* per ni_kernel_id over the timed iterations, when profiled */
+    uint64_t kernel_launches[3];
 } ni_drive_result;
 
 int ni_drive_run(const ni_drive_opts* opts, ni_drive_result* result);

@@ -180,11 +180,13 @@ int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes);
 /* quant.rs:25-54 on the device, elementwise (the conversion the append uses). */
 int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream);
 
-/* ---- measurement: HIP events around this handle's kernel launches ---- */
+/* ---- measurement: HIP event timestamps of this handle's kernel launches ---- */
 enum ni_kernel_id { NI_K_APPEND = 0, NI_K_ATTN = 1, NI_K_MERGE = 2, NI_K_COUNT = 3 };
-/* Bit k of kernel_mask brackets every launch of kernel k (ni_kernel_id) with
- * a pair of HIP events on the launch's stream; 0 stops.  NI_K_ATTN is the
- * attention launch (with the append fused into it when ni_kv_step fuses). */
+/* Bit k of kernel_mask times every launch of kernel k (ni_kernel_id): the
+ * dispatch itself records the kernel's start and end into a pair of HIP
+ * events (hipExtLaunchKernelGGL), so the time is the kernel's own, with no
+ * extra commands in the stream; 0 stops.  NI_K_ATTN is the attention launch
+ * (with the append fused into it when ni_kv_step fuses). */
 int ni_kv_profile(ni_kv* kv, uint32_t kernel_mask);
 /* Total milliseconds and launches of one kernel since the last read (waits). */
 int ni_kv_profile_read(ni_kv* kv, int kernel, double* total_ms, uint64_t* launches);

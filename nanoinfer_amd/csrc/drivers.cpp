@@ -359,9 +359,11 @@ struct Runner {
         const size_t n = (size_t)L * ls;
         std::vector<float> host(n);
         XorShift g = XorShift::seeded(o.data_seed);
+        const float kv_std = o.kv_std > 0 ? o.kv_std : 1.f;
         for (float** p : {&d.q, &d.k, &d.v, &d.out}) {
             if (hipMalloc(p, n * sizeof(float)) != hipSuccess) return drive_fail(NI_ERR_HIP, "hipMalloc failed");
-            for (auto& x : host) x = g.normal();
+            const float scale = (p == &d.k || p == &d.v) ? kv_std : 1.f;
+            for (auto& x : host) x = g.normal() * scale;
             if (hipMemcpy(*p, host.data(), n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
                 return drive_fail(NI_ERR_HIP, "hipMemcpy failed");
         }
@@ -433,6 +435,10 @@ int timed_run(Runner& r, ni_drive_result* res, Fn&& iterate) {
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
         return drive_fail(NI_ERR_HIP, "hipEventCreate failed");
     if (hipStreamSynchronize(r.stream) != hipSuccess) return drive_fail(NI_ERR_HIP, "hipStreamSynchronize failed");
+    if (r.o.profile_mask) {
+        if (int rc = ni_kv_profile(r.kv, r.o.profile_mask)) return r.kv_fail(rc, "ni_kv_profile");
+        for (int k = 0; k < NI_K_COUNT; k++) ni_kv_profile_read(r.kv, k, nullptr, nullptr);
+    }
     r.calls = 0;
     double host = 0;
     const auto t0 = Clock::now();
@@ -453,6 +459,12 @@ int timed_run(Runner& r, ni_drive_result* res, Fn&& iterate) {
     res->host_us_per_step = host / std::max(1u, r.o.steps) * 1e6;
     res->steps = r.o.steps;
     res->launches = r.calls;
+    if (r.o.profile_mask) {
+        for (int k = 0; k < NI_K_COUNT; k++)
+            if (int rc = ni_kv_profile_read(r.kv, k, &res->kernel_ms[k], &res->kernel_launches[k]))
+                return r.kv_fail(rc, "ni_kv_profile_read");
+        ni_kv_profile(r.kv, 0);
+    }
     return NI_OK;
 }
 
@@ -518,6 +530,39 @@ int run_spec(Runner& r, ni_drive_result* res) {
     return rc;
 }
 
+int run_fixed(Runner& r, ni_drive_result* res) {
+    if (!r.o.fixed_ctx || r.o.fixed_n == 0) return drive_fail(NI_ERR_BAD_ARG, "fixed workload without contexts");
+    std::vector<uint32_t> seqs;
+    std::vector<ni_work> work;
+    for (uint32_t i = 0; i < r.o.fixed_n; i++) {
+        const uint32_t ctx = r.o.fixed_ctx[i];
+        if (ctx == 0) return drive_fail(NI_ERR_BAD_ARG, "fixed context 0");
+        uint32_t s = 0;
+        if (int rc = ni_kv_add_seq(r.kv, &s)) return r.kv_fail(rc, "add_seq");
+        if (ctx > 1)
+            if (int rc = r.fill(s, ctx - 1)) return rc;
+        seqs.push_back(s);
+        work.push_back({s, 1, 1});
+    }
+    const double bytes = step_bytes(work.data(), (uint32_t)work.size(), r.o.fixed_ctx, r.L, r.C);
+    int rc = timed_run(r, res, [&](bool timed) -> int {
+        if (int e = r.launch(work.data(), (uint32_t)work.size())) return e;
+        // Roll back, so the next iteration appends the same positions.
+        for (uint32_t i = 0; i < r.o.fixed_n; i++)
+            if (int e = ni_kv_truncate(r.kv, seqs[i], r.o.fixed_ctx[i] - 1)) return r.kv_fail(e, "truncate");
+        if (timed) {
+            res->bytes += bytes;
+            res->seq_tokens += r.o.fixed_n;
+        }
+        return NI_OK;
+    });
+    double ctx = 0;
+    for (uint32_t i = 0; i < r.o.fixed_n; i++) ctx += r.o.fixed_ctx[i];
+    res->mean_live = r.o.fixed_n;
+    res->mean_context = ctx / r.o.fixed_n;
+    return rc;
+}
+
 }  // namespace
 
 extern "C" int ni_drive_run(const ni_drive_opts* o, ni_drive_result* res) {
@@ -530,6 +575,7 @@ extern "C" int ni_drive_run(const ni_drive_opts* o, ni_drive_result* res) {
     switch (o->workload) {
         case NI_DRIVE_SERVE: return run_serve(r, res);
         case NI_DRIVE_SPEC: return run_spec(r, res);
+        case NI_DRIVE_FIXED: return run_fixed(r, res);
         default: return drive_fail(NI_ERR_BAD_ARG, "unknown workload %u", o->workload);
     }
 }

@@ -338,21 +338,20 @@ hipEvent_t take_event(ni_kv* kv) {
     return e;
 }
 
+// Timing of one launch of kernel `k` when profiling is on: the events go to
+// the launch, whose dispatch records the kernel's start and end in them.
 struct ProfileScope {
     ni_kv* kv;
     int kernel;
-    hipStream_t s;
-    hipEvent_t a = nullptr, b = nullptr;
-    ProfileScope(ni_kv* kv_, int k, hipStream_t s_) : kv(kv_), kernel(k), s(s_) {
+    LaunchTiming t;
+    ProfileScope(ni_kv* kv_, int k) : kv(kv_), kernel(k) {
         if (!(kv->profile & (1u << k))) return;
-        a = take_event(kv);
-        b = take_event(kv);
-        if (a) (void)hipEventRecord(a, s);
+        t.start = take_event(kv);
+        t.stop = take_event(kv);
+        if (!t.start || !t.stop) t = LaunchTiming{};
     }
     ~ProfileScope() {
-        if (!a || !b) return;
-        (void)hipEventRecord(b, s);
-        kv->prof_ev[kernel].push_back({a, b});
+        if (t.start) kv->prof_ev[kernel].push_back({t.start, t.stop});
     }
 };
 
@@ -496,8 +495,8 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
         a.n_rows = (uint32_t)P.app.size();
         a.layer0 = layer0;
         a.n_lay = n_lay;
-        ProfileScope ps(kv, NI_K_APPEND, s);
-        hipError_t e = launch_append(a, ref.inl, ref.inl_bytes, s);
+        ProfileScope ps(kv, NI_K_APPEND);
+        hipError_t e = launch_append(a, ref.inl, ref.inl_bytes, s, ps.t);
         if (e != hipSuccess) return kv->hip_fail(e, "append kernel");
     }
     if (!P.items.empty() || !P.orphans.empty()) {
@@ -530,13 +529,13 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
         a.n_orphan_blocks = P.fused ? orphan_blocks(a) : 0;
         {
-            ProfileScope ps(kv, NI_K_ATTN, s);
-            hipError_t e = launch_attention(a, ref.inl, ref.inl_bytes, s);
+            ProfileScope ps(kv, NI_K_ATTN);
+            hipError_t e = launch_attention(a, ref.inl, ref.inl_bytes, s, ps.t);
             if (e != hipSuccess) return kv->hip_fail(e, "attention kernel");
         }
         if (!P.merges.empty()) {
-            ProfileScope ps(kv, NI_K_MERGE, s);
-            hipError_t e = launch_merge(a, ref.inl, ref.inl_bytes, s);
+            ProfileScope ps(kv, NI_K_MERGE);
+            hipError_t e = launch_merge(a, ref.inl, ref.inl_bytes, s, ps.t);
             if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
         }
     }

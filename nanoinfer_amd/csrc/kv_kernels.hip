@@ -1,21 +1,26 @@
 // kv_kernels.hip -- gfx950 (MI355X) kernels of the paged f16 KV-cache path.
 //
-// Pool layout (device): K and V each [n_layer][kv_pages][n_head][16][D] f16.
-// One (page, head) block of K is 16*D halves contiguous (2 KB at D = 64), so a
-// wave64 reading it with 16-byte lanes moves 1 KB per load instruction with
-// every lane on consecutive bytes.  The reference keeps [page][16][C]
-// (crates/metal/src/batch.rs:166); values are identical per (seq, pos, head, d),
-// only the placement differs.
+// Pool layout (device): one allocation [n_layer][kv_pages][n_head][K|V][16][D]
+// f16.  One (page, head) block of K is 16*D halves contiguous (2 KB at D = 64)
+// and its V block follows it, so a wave64 reading a block with 16-byte lanes
+// moves 1 KB per load instruction with every lane on consecutive bytes.  The
+// reference keeps [page][16][C] (crates/metal/src/batch.rs:166); values are
+// identical per (seq, pos, head, d), only the placement differs.
 //
 // Kernels:
 //   kv_append_kernel   f32 K/V rows -> f16 page slots (b_kv_write, batch.metal:329-344)
 //   kv_gather_kernel   page slots -> f16 rows in the reference layout (kv_slot reads, :24-26)
-//   attn_split_kernel  paged flash-decoding, one workgroup per (item, layer, head)
-//                      (b_attn_split, batch.metal:349-400)
+//   attn_split_kernel  paged flash-decoding of single query rows, one workgroup
+//                      per (item, layer, head) (b_attn_split, batch.metal:349-400),
+//                      with the step's append fused into its prologue
+//   attn_mfma_kernel   the same for groups of 2..16 causal query rows of one
+//                      sequence, on the matrix cores
 //   attn_merge_kernel  log-sum-exp merge of partitions (b_attn_merge, :403-424)
 //
-// Everything is HBM-bound streaming of f16 K/V: no MFMA.  Arithmetic is f32;
+// Everything is HBM-bound streaming of f16 K/V.  Arithmetic is f32 (the
+// matrix-core kernel carries f32 operands as f16 hi + scaled lo parts);
 // softmax runs in the base-2 domain (scores pre-scaled by log2(e)/sqrt(D)).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -707,10 +712,20 @@ __global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, c
     }
 }
 
-// One workgroup of D threads per (merge item, layer, head); thread d owns
-// output dimension d of every query row of the group.
+// One workgroup per (merge item, layer, head).  Thread t owns output unit
+// u = (row, dim) of the group and partitions j, j+G, j+2G, ... where G =
+// kMergeThreads / (rows * D) groups of threads split the partitions; each
+// keeps a running log-sum-exp state (m, l, o) over its partitions, whose
+// loads do not depend on earlier arithmetic, so they stream back to back
+// (batch.metal:403-424 merges the same (m, l, o) partials).  The G states of
+// a unit are combined through LDS.  A partition where a row has no key holds
+// m = kMinScore, l = 0, o = 0 and weighs nothing.
+constexpr int kMergeThreads = 512;
+
 template <int D, int NQ, int INL>
-__global__ __launch_bounds__(D) void attn_merge_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+    constexpr uint32_t T = kMergeThreads;
+    __shared__ float sm[T], sl[T], so[T];
     const uint32_t H = a.pool.n_head;
     const uint32_t lh = a.n_lay * H;
     const uint32_t mi = blockIdx.x / lh;
@@ -718,20 +733,50 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(const AttnLaunch a, const
     const uint32_t lay = rem / H;
     const uint32_t head = rem - lay * H;
     const MergeItem g = reinterpret_cast<const MergeItem*>(plan_base(pa, a.plan) + a.off_merges)[mi];
-    const uint32_t d = threadIdx.x;
     const uint64_t slot_stride = (uint64_t)a.n_lay * H * NQ * (D + 2);
-    for (uint32_t r = 0; r < g.nq; r++) {
-        const float* p0 = a.partials + ((((uint64_t)g.slot0 * a.n_lay + lay) * H + head) * NQ + r) * (D + 2);
-        float M = p0[0];
-        for (uint32_t s = 1; s < g.n_parts; s++) M = fmaxf(M, p0[s * slot_stride]);
-        float L = 0.f, O = 0.f;
-        for (uint32_t s = 0; s < g.n_parts; s++) {
-            const float* p = p0 + s * slot_stride;
-            const float wt = fast_exp2(p[0] - M);
-            L += p[1] * wt;
-            O += p[2 + d] * wt;
+    const float* base = a.partials + (((uint64_t)g.slot0 * a.n_lay + lay) * H + head) * NQ * (D + 2);
+    const uint32_t units = g.nq * D;
+    const uint32_t G = units >= T ? 1u : T / units;
+    const uint32_t t = threadIdx.x;
+    for (uint32_t u0 = 0; u0 < units; u0 += T) {  // several passes only when G == 1
+        const uint32_t j = G > 1 ? t / units : 0u;
+        const uint32_t u = G > 1 ? t - j * units : u0 + t;
+        const bool active = j < G && u < units;
+        const uint32_t r = u / D, d = u - r * D;
+        float m = kMinScore, l = 0.f, o = 0.f;
+        if (active) {
+            const float* p = base + r * (D + 2);
+#pragma unroll 4
+            for (uint32_t s = j; s < g.n_parts; s += G) {
+                const float* ps = p + s * slot_stride;
+                const float ms = ps[0], ls = ps[1], os = ps[2 + d];
+                const float mn = fmaxf(m, ms);
+                const float a1 = fast_exp2(m - mn), a2 = fast_exp2(ms - mn);
+                l = l * a1 + ls * a2;
+                o = o * a1 + os * a2;
+                m = mn;
+            }
         }
-        a.out[(int64_t)lay * a.out_layer_stride + (int64_t)(g.row0 + r) * a.out_row_stride + head * D + d] = O / L;
+        float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)(g.row0 + r) * a.out_row_stride + head * D + d;
+        if (G == 1) {
+            if (active) *dst = o / l;
+            continue;
+        }
+        sm[t] = m;
+        sl[t] = l;
+        so[t] = o;
+        __syncthreads();
+        if (t < units) {
+            float M = sm[t];
+            for (uint32_t k = 1; k < G; k++) M = fmaxf(M, sm[k * units + t]);
+            float L = 0.f, O = 0.f;
+            for (uint32_t k = 0; k < G; k++) {
+                const float w = fast_exp2(sm[k * units + t] - M);
+                L += sl[k * units + t] * w;
+                O += so[k * units + t] * w;
+            }
+            *dst = O / L;
+        }
     }
 }
 
@@ -741,6 +786,14 @@ constexpr int kPagesPerIter = NI_ATTN_PAGES;
 #define NI_MFMA_PAGES 1
 #endif
 constexpr int kMfmaPages = NI_MFMA_PAGES;  // pages per wave iteration of the matrix-core kernel
+
+// One kernel launch; with timing events the dispatch packet itself records
+// the kernel's start and end (no separate event commands in the stream).
+template <typename K, typename... Args>
+hipError_t go(K kern, uint64_t blocks, uint32_t threads, hipStream_t s, const LaunchTiming& t, const Args&... args) {
+    hipExtLaunchKernelGGL(kern, dim3((uint32_t)blocks), dim3(threads), 0, s, t.start, t.stop, 0, args...);
+    return hipGetLastError();
+}
 
 // Launch `kern<INL>` with the plan inline (kInlinePlanBytes of arguments) or
 // through the device pointer in the launch struct.
@@ -756,7 +809,7 @@ hipError_t with_plan(const L& a, const void* inline_plan, uint32_t inline_bytes,
 }
 
 template <int D, int NQ>
-hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     // Several queries per item hold NQ times the softmax state: one page per
     // iteration keeps their registers (and occupancy) in check.
 #ifndef NI_ATTN_PAGES_D128
@@ -768,50 +821,42 @@ hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         if (a.napp_total || a.n_orphan_blocks)
-            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, PB, true, INL>), dim3((uint32_t)blocks),
-                               dim3(64 * kWaves), 0, s, a, pa);
-        else
-            hipLaunchKernelGGL((attn_split_kernel<D, NQ, kWaves, PB, false, INL>), dim3((uint32_t)blocks),
-                               dim3(64 * kWaves), 0, s, a, pa);
-        return hipGetLastError();
+            return go(attn_split_kernel<D, NQ, kWaves, PB, true, INL>, blocks, 64 * kWaves, s, t, a, pa);
+        return go(attn_split_kernel<D, NQ, kWaves, PB, false, INL>, blocks, 64 * kWaves, s, t, a, pa);
     });
 }
 
 template <int D, int NQ>
-hipError_t merge_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+hipError_t merge_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t blocks = (uint64_t)a.n_merges * a.n_lay * a.pool.n_head;
     if (blocks == 0) return hipSuccess;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-        hipLaunchKernelGGL((attn_merge_kernel<D, NQ, INL>), dim3((uint32_t)blocks), dim3(D), 0, s, a, pa);
-        return hipGetLastError();
+        return go(attn_merge_kernel<D, NQ, INL>, blocks, kMergeThreads, s, t, a, pa);
     });
 }
 
 template <int D>
-hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         if (a.napp_total || a.n_orphan_blocks)
-            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, kMfmaPages, true, INL>), dim3((uint32_t)blocks),
-                               dim3(64 * kWaves), 0, s, a, pa);
-        else
-            hipLaunchKernelGGL((attn_mfma_kernel<D, kWaves, kMfmaPages, false, INL>), dim3((uint32_t)blocks),
-                               dim3(64 * kWaves), 0, s, a, pa);
-        return hipGetLastError();
+            return go(attn_mfma_kernel<D, kWaves, kMfmaPages, true, INL>, blocks, 64 * kWaves, s, t, a, pa);
+        return go(attn_mfma_kernel<D, kWaves, kMfmaPages, false, INL>, blocks, 64 * kWaves, s, t, a, pa);
     });
 }
 
 template <int D>
-hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
+hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge,
+                            const LaunchTiming& t) {
 #define NI_NQ_CASE(N) \
-    case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s) : attn_launch_t<D, N>(a, ip, ib, s);
+    case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s, t) : attn_launch_t<D, N>(a, ip, ib, s, t);
 #if NI_ATTN_MFMA
     // Groups of several rows always take the 16-row matrix tile.
     if (a.nq_tile == kMfmaTile)
-        return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s) : mfma_launch_t<D>(a, ip, ib, s);
+        return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s, t) : mfma_launch_t<D>(a, ip, ib, s, t);
     switch (a.nq_tile) {
         NI_NQ_CASE(1)
         default: return hipErrorInvalidValue;
@@ -826,10 +871,11 @@ hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hi
 #undef NI_NQ_CASE
 }
 
-hipError_t attn_dispatch(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge) {
+hipError_t attn_dispatch(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge,
+                          const LaunchTiming& t) {
     switch (a.pool.head_dim) {
-        case 64: return attn_dispatch_nq<64>(a, ip, ib, s, merge);
-        case 128: return attn_dispatch_nq<128>(a, ip, ib, s, merge);
+        case 64: return attn_dispatch_nq<64>(a, ip, ib, s, merge, t);
+        case 128: return attn_dispatch_nq<128>(a, ip, ib, s, merge, t);
         default: return hipErrorInvalidValue;
     }
 }
@@ -838,13 +884,12 @@ hipError_t attn_dispatch(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
 
 bool attention_supported(uint32_t head_dim) { return head_dim == 64 || head_dim == 128; }
 
-hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
+hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t threads = (uint64_t)a.n_lay * a.n_rows * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
     if (threads == 0) return hipSuccess;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-        hipLaunchKernelGGL(kv_append_kernel<INL>, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a, pa);
-        return hipGetLastError();
+        return go(kv_append_kernel<INL>, (threads + 255) / 256, 256, s, t, a, pa);
     });
 }
 
@@ -858,8 +903,8 @@ hipError_t launch_gather(const GatherLaunch& a, const void* ip, uint32_t ib, hip
     });
 }
 
-hipError_t launch_attention(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
-    return attn_dispatch(a, ip, ib, s, false);
+hipError_t launch_attention(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
+    return attn_dispatch(a, ip, ib, s, false, t);
 }
 
 uint32_t orphan_blocks(const AttnLaunch& a) {
@@ -867,8 +912,8 @@ uint32_t orphan_blocks(const AttnLaunch& a) {
     return (uint32_t)((threads + 64 * kWaves - 1) / (64 * kWaves));
 }
 
-hipError_t launch_merge(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s) {
-    return attn_dispatch(a, ip, ib, s, true);
+hipError_t launch_merge(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
+    return attn_dispatch(a, ip, ib, s, true, t);
 }
 
 hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s) {

@@ -137,10 +137,20 @@ constexpr uint32_t kInlinePlanBytes = 32768;
 // every index the plan holds before calling them.
 // `inline_plan` (nullptr: the plan is at a.plan on the device) holds
 // `inline_bytes` <= kInlinePlanBytes of plan passed with the arguments.
-hipError_t launch_append(const AppendLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
+// Events the dispatch itself records at the kernel's start and end (both
+// null: no timing).
+struct LaunchTiming {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+
+hipError_t launch_append(const AppendLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
+                         const LaunchTiming& t = {});
 hipError_t launch_gather(const GatherLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
-hipError_t launch_attention(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
-hipError_t launch_merge(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
+hipError_t launch_attention(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
+                            const LaunchTiming& t = {});
+hipError_t launch_merge(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
+                        const LaunchTiming& t = {});
 hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s);
 // Blocks a fused launch needs for its orphan rows (n_orphans set).
 uint32_t orphan_blocks(const AttnLaunch& a);

@@ -37,16 +37,18 @@ class ni_drive_opts(C.Structure):
     _fields_ = [("workload", _u32), ("launch", _u32), ("kv", _abi.ni_kv_opts), ("serve", ni_serve_opts),
                 ("spec_seqs", _u32), ("spec_ctx_min", _u32), ("spec_ctx_max", _u32), ("spec_k", _u32),
                 ("spec_seed", C.c_uint64), ("spec_window", _u32), ("warmup", _u32), ("steps", _u32),
-                ("split_tokens", _u32), ("data_seed", C.c_uint64)]
+                ("split_tokens", _u32), ("data_seed", C.c_uint64), ("fixed_ctx", C.POINTER(_u32)),
+                ("fixed_n", _u32), ("kv_std", C.c_float), ("profile_mask", _u32)]
 
 
 class ni_drive_result(C.Structure):
     _fields_ = [("seconds", C.c_double), ("gpu_seconds", C.c_double), ("bytes", C.c_double),
                 ("seq_tokens", C.c_double), ("host_us_per_step", C.c_double), ("steps", _u32),
-                ("launches", C.c_uint64), ("mean_live", C.c_double), ("mean_context", C.c_double)]
+                ("launches", C.c_uint64), ("mean_live", C.c_double), ("mean_context", C.c_double),
+                ("kernel_ms", C.c_double * 3), ("kernel_launches", C.c_uint64 * 3)]
 
 
-NI_DRIVE_SERVE, NI_DRIVE_SPEC = 0, 1
+NI_DRIVE_SERVE, NI_DRIVE_SPEC, NI_DRIVE_FIXED = 0, 1, 2
 NI_DRIVE_STEP, NI_DRIVE_PER_LAYER = 0, 1
 
 
@@ -163,4 +165,60 @@ def drive(opts: ni_drive_opts) -> dict:
     """ni_drive_run: a whole synthetic run on the device (C++ host loop)."""
     r = ni_drive_result()
     _check(lib().ni_drive_run(C.byref(opts), C.byref(r)), "ni_drive_run")
-    return {f: getattr(r, f) for f, _ in ni_drive_result._fields_}
+    out = {f: getattr(r, f) for f, _ in ni_drive_result._fields_}
+    out["kernel_ms"] = list(r.kernel_ms)
+    out["kernel_launches"] = list(r.kernel_launches)
+    return out
+
+
+# ------------------------------------------------------- configuration presets
+# The benchmark configurations as ni_drive_opts; contexts and page orders come
+# from nanoinfer_amd.workloads, the same definitions the tests use.
+
+def _kv(o, shape, kv_pages, max_seqs, max_ctx, max_rows, order=None):
+    o.kv.n_layer, o.kv.n_head, o.kv.head_dim = shape["n_layer"], shape["n_head"], shape["head_dim"]
+    o.kv.kv_pages, o.kv.max_seqs, o.kv.max_ctx, o.kv.max_rows = kv_pages, max_seqs, max_ctx, max_rows
+    if order is not None:
+        arr = np.ascontiguousarray(np.asarray(order, np.uint32))
+        o._keep.append(arr)
+        o.kv.page_order = arr.ctypes.data_as(C.POINTER(_u32))
+
+
+def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, split: int = 0, seed: int = 7,
+           profile_mask: int = 0, query_all_prompt_rows: bool = False) -> ni_drive_opts:
+    """ni_drive_opts of config 2, 3, 4 or 5."""
+    from . import workloads
+
+    o = ni_drive_opts()
+    o._keep = []  # arrays the struct points into
+    o.launch, o.steps, o.warmup, o.split_tokens, o.data_seed, o.profile_mask = launch, steps, warmup, split, seed, \
+        profile_mask
+    if name == "config3":
+        o.workload = NI_DRIVE_SERVE
+        o.serve = ni_serve_opts(seed, 1.0, 100000, 64, 32, 512, 16, 256, 256, 512, int(query_all_prompt_rows))
+        # metal_serve.rs:485: max_batch * pages(prompt_max + out_max) + 8
+        _kv(o, workloads.GPT2, 64 * workloads.pages(512 + 256) + 8, 64, 1024, 512)
+    elif name == "config5":
+        o.workload = NI_DRIVE_SPEC
+        o.spec_seqs, o.spec_ctx_min, o.spec_ctx_max, o.spec_k, o.spec_seed = 32, 128, 1024, 4, 5
+        o.spec_window = 64
+        _kv(o, workloads.GPT2, 32 * 2048 // 16, 32, 2048, 512)
+    elif name == "config2":
+        ctx, order = workloads.config2_contexts()
+        o.workload = NI_DRIVE_FIXED
+        arr = np.ascontiguousarray(np.asarray(ctx, np.uint32))
+        o._keep.append(arr)
+        o.fixed_ctx, o.fixed_n = arr.ctypes.data_as(C.POINTER(_u32)), arr.size
+        _kv(o, workloads.GPT2, 1024, 16, 1024, 512, order)
+    elif name == "config4":
+        B, L = 4, 32768
+        o.workload = NI_DRIVE_FIXED
+        arr = np.full(B, L, np.uint32)
+        o._keep.append(arr)
+        o.fixed_ctx, o.fixed_n = arr.ctypes.data_as(C.POINTER(_u32)), B
+        o.kv_std = 0.5
+        o.split_tokens = split or 512
+        _kv(o, workloads.LONG, B * L // 16, B, L, 4096, workloads.XorShift.seeded(4).permutation(B * L // 16))
+    else:
+        raise ValueError(name)
+    return o
