@@ -246,21 +246,30 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         }
         groups.push_back({r.seq, r.row, r.pos, 1, r.new_begin, r.new_end, r.app_first});
     }
-    // Partition size: the caller's, or (0) the largest of 1024/512/256/128
-    // tokens that still yields >= 4096 workgroups, so that every CU has
-    // work and the ragged tail is short.
+    // Partition size: the caller's, or (0) automatic.  Splitting costs a
+    // merge launch (~5-7 us) and the partials' round trip, so it pays only
+    // when the unsplit items cannot keep the GPU busy: 256 CUs hold 1024
+    // workgroups at once, and with >= 2048 of them, sorted longest first,
+    // the tail is short -- only items longer than kLongItem keys are split
+    // then.  Below that, the largest of 1024/512/256/128 tokens that yields
+    // >= 2048 workgroups.
     uint32_t part = split_tokens;
     if (part == 0) {
+        constexpr uint64_t kFillWorkgroups = 2048;
+        constexpr uint32_t kLongItem = 4096;
         static const uint32_t kChoices[] = {1024, 512, 256, 128};
-        const uint64_t target = 4096;
         const uint64_t per_unit = (uint64_t)n_lay * kv->o.n_head;
-        part = kChoices[3];
-        for (uint32_t c : kChoices) {
-            uint64_t items = 0;
-            for (const Group& g : groups) items += ((uint64_t)g.pos0 + g.nq + c - 1) / c;
-            if (items * per_unit >= target) {
-                part = c;
-                break;
+        if ((uint64_t)groups.size() * per_unit >= kFillWorkgroups) {
+            part = kLongItem;
+        } else {
+            part = kChoices[3];
+            for (uint32_t c : kChoices) {
+                uint64_t items = 0;
+                for (const Group& g : groups) items += ((uint64_t)g.pos0 + g.nq + c - 1) / c;
+                if (items * per_unit >= kFillWorkgroups) {
+                    part = c;
+                    break;
+                }
             }
         }
     } else if (part % kPage != 0 || part < kMinSplit) {

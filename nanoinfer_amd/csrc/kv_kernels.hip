@@ -489,8 +489,14 @@ constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
 // layout), so the softmax state of a query lives in lanes q, q+16, q+32, q+48.
 // Waves take the item's pages round-robin and merge through LDS at the end,
 // as in attn_split_kernel.
+// Waves per SIMD the register allocation must allow: 4 (<= 128 registers,
+// no spills) measured 3.9% faster on config 5 than the unconstrained 3.
+#ifndef NI_MFMA_MIN_WAVES
+#define NI_MFMA_MIN_WAVES 4
+#endif
 template <int D, int W, int PB, bool FUSED, int INL>
-__global__ __launch_bounds__(64 * W) void attn_mfma_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+__global__ __launch_bounds__(64 * W, NI_MFMA_MIN_WAVES) void attn_mfma_kernel(const AttnLaunch a,
+                                                                              const PlanArg<INL> pa) {
     constexpr int QC = D / 32;      // 32-dim chunks of the QK product
     constexpr int VC = D / 16;      // 16-dim chunks of the PV product
     constexpr int LPK = D / 8;      // lanes per key row in a coalesced V load
