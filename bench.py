@@ -71,7 +71,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--workload", default="config3", choices=["config3", "config2", "config4", "config5"])
+    ap.add_argument("--workload", default="config3",
+                    help="config3 (default), config2, config4, config5, or qkv[ROWS] (the QKV projection with "
+                         "the append in its epilogue, ROWS rows per layer, default 64)")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = automatic)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (0 = skip)")
     ap.add_argument("--threads", type=int, default=0, help="CPU baseline threads (0 = min(cpus, 16))")
@@ -318,6 +320,46 @@ def run_secondary(args):
     return res
 
 
+PEAK_F32_TFLOPS = 157.3  # MI355X dense f32 matrix throughput, AMD's published figure
+
+
+def run_qkv(args):
+    """The QKV projection of GPT-2 (d_in 768 -> 3C = 2304) per layer with K/V
+    appended to pages in its epilogue (ni_kv_qkv_append, the reference's
+    BEPI_QKV path), against the unfused path (f32 projection, then
+    ni_kv_append).  Both are timed on the same algorithmic bytes: W, bias,
+    x, q out and the f16 K/V stores."""
+    from nanoinfer_amd import drivers
+
+    rows = int(args.workload[3:] or 64)
+    r = _drive(args.workload, args)
+    ru = _drive(args.workload, args, launch=drivers.NI_DRIVE_PER_LAYER)
+    res = _line(args, r, f"qkv: GPT-2 QKV projection, {rows} rows x 12 layers (768 -> 2304, f32 weights) with K/V "
+                         f"appended as f16 in the epilogue", {"rows": rows, "d_in": 768, "n_feat": 2304},
+                "synthetic (seeded normal x, W ~ N(0, 1/768), bias, resident in HBM)")
+    res["metric"] = "fused QKV projection + KV append, algorithmic GB/s, 1 MI355X"
+    res["tflops"] = round(r["flops"] / r["seconds"] / 1e12, 2)
+    gu = ru["bytes"] / ru["seconds"] / 1e9
+    res["unfused"] = {"value": round(gu, 2), "unit": "GB/s", "ms_per_step": round(ru["seconds"] / ru["steps"] * 1e3, 5),
+                      "path": "ni_kv_qkv_project (f32 [n][3C]) + ni_kv_append per layer"}
+    if not args.no_profile:
+        rp = _drive(args.workload, args, profile_mask=1 << 3)
+        ms, n = rp["kernel_ms"][3], rp["kernel_launches"][3]
+        t = ms / 1e3
+        gbs, tfl = rp["bytes"] / t / 1e9, rp["flops"] / t / 1e12
+        mfma_bound = rp["flops"] / (PEAK_F32_TFLOPS * 1e12) > rp["bytes"] / (PEAK_GBS * 1e9)
+        res["roofline"] = {"bound": "mfma" if mfma_bound else "hbm",
+                           "achieved": round(tfl if mfma_bound else gbs, 2),
+                           "peak": PEAK_F32_TFLOPS if mfma_bound else PEAK_GBS,
+                           "unit": "TFLOP/s" if mfma_bound else "GB/s",
+                           "frac": round(tfl / PEAK_F32_TFLOPS if mfma_bound else gbs / PEAK_GBS, 4), "traffic": None,
+                           "kernel": "qkv_kernel (fused epilogue)", "avg_launch_us": round(ms / n * 1e3, 3),
+                           "launches": n, "algorithmic_bytes_per_launch": int(rp["bytes"] / n),
+                           "flops_per_launch": int(rp["flops"] / n), "achieved_gbs": round(gbs, 2),
+                           "achieved_tflops": round(tfl, 2)}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -333,7 +375,15 @@ def main():
         calibrate_copy()
         return
     # The headline line is config 3; the others are secondary measurements.
-    res = run_config3(args) if args.workload == "config3" else run_secondary(args)
+    if args.workload == "config3":
+        res = run_config3(args)
+    elif args.workload.startswith("qkv"):
+        res = run_qkv(args)
+    elif args.workload in SECONDARY:
+        res = run_secondary(args)
+    else:
+        log(f"bench: unknown workload {args.workload}")
+        sys.exit(2)
     print(json.dumps(res), flush=True)
 
 

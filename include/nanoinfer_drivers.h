@@ -98,7 +98,13 @@ enum ni_drive_workload {
     /* Fixed contexts (configs 2 and 4): sequence i holds fixed_ctx[i] - 1
      * positions; every iteration appends one row to each and attends it,
      * then truncates back, so every iteration does the same work. */
-    NI_DRIVE_FIXED = 2
+    NI_DRIVE_FIXED = 2,
+    /* The QKV projection of qkv_rows rows (d_in = C, random W and bias per
+     * layer) with K/V appended, every layer per iteration: launch
+     * NI_DRIVE_STEP runs ni_kv_qkv_append (the fused epilogue),
+     * NI_DRIVE_PER_LAYER ni_kv_qkv_project + ni_kv_append (f32 K/V through
+     * memory).  Rows i of qkv_rows go to sequence i % max_seqs. */
+    NI_DRIVE_QKV = 3
 };
 enum ni_drive_launch {
     NI_DRIVE_STEP = 0,     /* one ni_kv_step per iteration (all layers per launch) */
@@ -123,6 +129,7 @@ typedef struct ni_drive_opts {
     uint32_t fixed_n;
     float kv_std;           /* k/v data ~ N(0, kv_std^2); 0 = 1 (q is always N(0,1)) */
     uint32_t profile_mask;  /* ni_kv_profile mask over the timed iterations; 0 = none */
+    uint32_t qkv_rows;      /* NI_DRIVE_QKV: rows per projection */
 } ni_drive_opts;
 
 typedef struct ni_drive_result {
@@ -135,8 +142,9 @@ typedef struct ni_drive_result {
     uint64_t launches;      /* data-path ABI calls in the timed region */
     double mean_live;       /* mean queried sequences per iteration */
     double mean_context;    /* mean context of queried sequences */
-    double kernel_ms[3];    /* per ni_kernel_id over the timed iterations, when profiled */
-    uint64_t kernel_launches[3];
+    double flops;           /* NI_DRIVE_QKV: matrix flops of the timed iterations */
+    double kernel_ms[NI_K_COUNT]; /* per ni_kernel_id over the timed iterations, when profiled */
+    uint64_t kernel_launches[NI_K_COUNT];
 } ni_drive_result;
 
 int ni_drive_run(const ni_drive_opts* opts, ni_drive_result* result);

@@ -126,6 +126,25 @@ uint32_t ni_kv_free_block_count(const ni_kv* kv); /* Batch::free_block_count, :2
 int ni_kv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* k, const float* v,
                  int64_t row_stride, int64_t layer_stride, ni_stream stream);
 
+/* The QKV projection with the append in its epilogue (the reference's
+ * matvec_batch<..., BEPI_QKV>, batch.metal:94-165, dispatched per layer at
+ * batch.rs:396-415): for row i, y = x_i W^T + bias with W [3C][d_in] f32
+ * row-major (the reference's weight layout) and bias [3C] (NULL = none);
+ * q = y[0, C) goes to q_out row i (f32), k = y[C, 2C) and v = y[2C, 3C) are
+ * stored as f16 (round to nearest even) in rows[i]'s page slot of `layer`
+ * (0 <= layer < n_layer) without passing through memory as f32.  Positions
+ * must be reserved; d_in must be a multiple of 16; x, w and q_out 16-byte
+ * aligned with strides that are multiples of 4 floats. */
+int ni_kv_qkv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* x,
+                     int64_t x_row_stride, uint32_t d_in, const float* w, const float* bias, float* q_out,
+                     int64_t q_row_stride, ni_stream stream);
+
+/* The same projection with every output to `out` ([n][3C] f32; the
+ * reference's BEPI_PLAIN epilogue): the same kernel and arithmetic, so the
+ * K/V bits ni_kv_qkv_append stores equal f32->f16 of out[:, C:3C]. */
+int ni_kv_qkv_project(ni_kv* kv, const float* x, int64_t x_row_stride, uint32_t n, uint32_t d_in, const float* w,
+                      const float* bias, float* out, int64_t out_row_stride, ni_stream stream);
+
 /* Block-table gather: f16 bits of K and V at (seq, pos) for each row, in the
  * reference's row layout [C] = [head][head_dim] (the reads of b_attn_split,
  * batch.metal:377,392, through kv_slot, :24-26).  Strides in halves. */
@@ -181,7 +200,7 @@ int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes);
 int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream);
 
 /* ---- measurement: HIP event timestamps of this handle's kernel launches ---- */
-enum ni_kernel_id { NI_K_APPEND = 0, NI_K_ATTN = 1, NI_K_MERGE = 2, NI_K_COUNT = 3 };
+enum ni_kernel_id { NI_K_APPEND = 0, NI_K_ATTN = 1, NI_K_MERGE = 2, NI_K_QKV = 3, NI_K_COUNT = 4 };
 /* Bit k of kernel_mask times every launch of kernel k (ni_kernel_id): the
  * dispatch itself records the kernel's start and end into a pair of HIP
  * events (hipExtLaunchKernelGGL), so the time is the kernel's own, with no

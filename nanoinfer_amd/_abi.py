@@ -31,7 +31,7 @@ NI_ERR_TOO_MANY_ROWS = 9
 NI_ERR_NOT_RESERVED = 10
 NI_ERR_NO_DEVICE = 11
 
-NI_K_APPEND, NI_K_ATTN, NI_K_MERGE = 0, 1, 2
+NI_K_APPEND, NI_K_ATTN, NI_K_MERGE, NI_K_QKV, NI_K_COUNT = 0, 1, 2, 3, 4
 
 
 class ni_kv_opts(C.Structure):
@@ -95,6 +95,10 @@ def _declare(L):
     L.ni_kv_free_block_count.argtypes = [_vp]
     L.ni_kv_append.restype = C.c_int
     L.ni_kv_append.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _vp, _i64, _i64, _vp]
+    L.ni_kv_qkv_append.restype = C.c_int
+    L.ni_kv_qkv_append.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _i64, _u32, _vp, _vp, _vp, _i64, _vp]
+    L.ni_kv_qkv_project.restype = C.c_int
+    L.ni_kv_qkv_project.argtypes = [_vp, _vp, _i64, _u32, _u32, _vp, _vp, _vp, _i64, _vp]
     L.ni_kv_gather.restype = C.c_int
     L.ni_kv_gather.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _vp, _i64, _i64, _vp]
     L.ni_paged_decode_attention.restype = C.c_int

@@ -98,6 +98,20 @@ def _f32_arg(t, name, layered):
     return t.data_ptr(), t.stride(0), 0
 
 
+def _weights(w, bias, c, d_in):
+    """Check W [3C, d_in] (contiguous float32 CUDA) and bias; the bias pointer."""
+    import torch
+
+    if not isinstance(w, torch.Tensor) or not w.is_cuda or w.dtype != torch.float32 or not w.is_contiguous() \
+            or tuple(w.shape) != (3 * c, d_in):
+        raise ValueError(f"w must be a contiguous float32 CUDA tensor [{3 * c}, {d_in}]")
+    if bias is None:
+        return None
+    if not bias.is_cuda or bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != 3 * c:
+        raise ValueError(f"bias must be a contiguous float32 CUDA tensor of {3 * c} values")
+    return bias.data_ptr()
+
+
 class PagedKv:
     """The KV cache and block tables of a batch of sequences on one MI355X."""
 
@@ -208,6 +222,35 @@ class PagedKv:
         if (rs, ls) != (rs2, ls2):
             raise ValueError("k and v must share strides")
         self._check(self._L.ni_kv_append(self._h, layer, rp, n, kp, vp, rs, ls, _stream_ptr(stream)))
+
+    def qkv_append(self, rows, x, w, bias=None, q_out=None, layer: int = 0, stream=None):
+        """The QKV projection with the append in its epilogue (BEPI_QKV):
+        x [n, d_in], w [3C, d_in], bias [3C] float32 CUDA tensors; k/v go to
+        the rows' page slots of `layer` as f16, q is returned [n, C]."""
+        import torch
+
+        arr, rp, n = _rows(rows)
+        xp, xs, _ = _f32_arg(x, "x", False)
+        wt = _weights(w, bias, self.opts.n_embd, x.shape[1])
+        if q_out is None:
+            q_out = torch.zeros((n, self.opts.n_embd), dtype=torch.float32, device=x.device)
+        qp, qs, _ = _f32_arg(q_out, "q_out", False)
+        self._check(self._L.ni_kv_qkv_append(self._h, layer, rp, n, xp, xs, x.shape[1], w.data_ptr(), wt, qp, qs,
+                                             _stream_ptr(stream)))
+        return q_out
+
+    def qkv_project(self, x, w, bias=None, out=None, stream=None):
+        """The same projection, every output column to out [n, 3C] (f32)."""
+        import torch
+
+        xp, xs, _ = _f32_arg(x, "x", False)
+        wt = _weights(w, bias, self.opts.n_embd, x.shape[1])
+        if out is None:
+            out = torch.zeros((x.shape[0], 3 * self.opts.n_embd), dtype=torch.float32, device=x.device)
+        op, os_, _ = _f32_arg(out, "out", False)
+        self._check(self._L.ni_kv_qkv_project(self._h, xp, xs, x.shape[0], x.shape[1], w.data_ptr(), wt, op, os_,
+                                              _stream_ptr(stream)))
+        return out
 
     def gather(self, rows, layer: int = ALL_LAYERS, stream=None):
         """f16 bits (int16 tensors) of K and V at each (seq, pos) row."""

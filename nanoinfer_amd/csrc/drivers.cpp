@@ -563,6 +563,77 @@ int run_fixed(Runner& r, ni_drive_result* res) {
     return rc;
 }
 
+int run_qkv(Runner& r, ni_drive_result* res) {
+    const uint32_t n = r.o.qkv_rows, C = r.C, L = r.L, d_in = C, F = 3 * C;
+    if (n == 0 || n > r.o.kv.max_rows) return drive_fail(NI_ERR_BAD_ARG, "qkv_rows must be 1..max_rows");
+    if (L < 3) return drive_fail(NI_ERR_BAD_ARG, "the unfused path keeps [n][3C] in the k buffer: n_layer >= 3");
+    // Rows spread over the sequences, one page-aligned position block each.
+    const uint32_t S = std::min(n, r.o.kv.max_seqs);
+    std::vector<uint32_t> seqs(S);
+    for (uint32_t i = 0; i < S; i++) {
+        if (int rc = ni_kv_add_seq(r.kv, &seqs[i])) return r.kv_fail(rc, "add_seq");
+        if (int rc = ni_kv_reserve(r.kv, seqs[i], (n + S - 1) / S)) return r.kv_fail(rc, "reserve");
+    }
+    std::vector<ni_row> rows(n);
+    for (uint32_t i = 0; i < n; i++) rows[i] = {seqs[i % S], i / S};
+    // W [L][3C][d_in] ~ N(0, 1/d_in), bias [L][3C] ~ N(0, 0.01).
+    float* w = nullptr;
+    float* bias = nullptr;
+    const size_t wn = (size_t)L * F * d_in;
+    if (hipMalloc(&w, wn * sizeof(float)) != hipSuccess || hipMalloc(&bias, (size_t)L * F * sizeof(float)) != hipSuccess)
+        return drive_fail(NI_ERR_HIP, "hipMalloc(weights) failed");
+    struct Free {
+        float* p[2];
+        ~Free() {
+            for (float* q : p)
+                if (q) (void)hipFree(q);
+        }
+    } guard{{w, bias}};
+    {
+        XorShift g = XorShift::seeded(r.o.data_seed + 1);
+        std::vector<float> host(wn);
+        const float sc = 1.f / std::sqrt((float)d_in);
+        for (auto& x : host) x = g.normal() * sc;
+        if (hipMemcpy(w, host.data(), wn * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            return drive_fail(NI_ERR_HIP, "hipMemcpy(weights) failed");
+        host.resize((size_t)L * F);
+        for (auto& x : host) x = g.normal() * 0.1f;
+        if (hipMemcpy(bias, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            return drive_fail(NI_ERR_HIP, "hipMemcpy(bias) failed");
+    }
+    const double bytes = (double)L * ((double)F * d_in * 4 + F * 4.0 + (double)n * d_in * 4 + (double)n * C * 4 +
+                                      (double)n * 2 * C * 2);
+    const double flops = 2.0 * L * n * (double)d_in * F;
+    float* x = r.d.q;    // [n][d_in]
+    float* y = r.d.k;    // unfused: [n][3C]
+    int rc = timed_run(r, res, [&](bool timed) -> int {
+        for (uint32_t l = 0; l < L; l++) {
+            const float* wl = w + (size_t)l * F * d_in;
+            const float* bl = bias + (size_t)l * F;
+            if (r.o.launch == NI_DRIVE_STEP) {
+                r.calls++;
+                if (int e = ni_kv_qkv_append(r.kv, (int32_t)l, rows.data(), n, x, d_in, d_in, wl, bl, r.d.out, C,
+                                             r.stream))
+                    return r.kv_fail(e, "ni_kv_qkv_append");
+            } else {
+                r.calls += 2;
+                if (int e = ni_kv_qkv_project(r.kv, x, d_in, n, d_in, wl, bl, y, F, r.stream))
+                    return r.kv_fail(e, "ni_kv_qkv_project");
+                if (int e = ni_kv_append(r.kv, (int32_t)l, rows.data(), n, y + C, y + 2 * C, F, 0, r.stream))
+                    return r.kv_fail(e, "ni_kv_append");
+            }
+        }
+        if (timed) {
+            res->bytes += bytes;
+            res->flops += flops;
+            res->seq_tokens += n;
+        }
+        return NI_OK;
+    });
+    res->mean_live = n;
+    return rc;
+}
+
 }  // namespace
 
 extern "C" int ni_drive_run(const ni_drive_opts* o, ni_drive_result* res) {
@@ -576,6 +647,7 @@ extern "C" int ni_drive_run(const ni_drive_opts* o, ni_drive_result* res) {
         case NI_DRIVE_SERVE: return run_serve(r, res);
         case NI_DRIVE_SPEC: return run_spec(r, res);
         case NI_DRIVE_FIXED: return run_fixed(r, res);
+        case NI_DRIVE_QKV: return run_qkv(r, res);
         default: return drive_fail(NI_ERR_BAD_ARG, "unknown workload %u", o->workload);
     }
 }

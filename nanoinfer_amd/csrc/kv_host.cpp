@@ -815,6 +815,75 @@ int ni_kv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const
                     (hipStream_t)stream);
 }
 
+// Shared checks and launch of the QKV projection; rows == NULL: plain.
+static int qkv_run(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* x, int64_t x_row_stride,
+                   uint32_t d_in, const float* w, const float* bias, float* out, int64_t out_row_stride,
+                   hipStream_t s) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    const bool fused = rows != nullptr;
+    const uint32_t C = kv->o.n_head * kv->o.head_dim, n_feat = 3 * C;
+    if (fused && (layer < 0 || (uint32_t)layer >= kv->o.n_layer))
+        return kv->fail(NI_ERR_BAD_ARG, "layer %d out of range (%u layers)", layer, kv->o.n_layer);
+    if (n == 0) return NI_OK;
+    if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "%u rows > max_rows %u", n, kv->o.max_rows);
+    if (d_in == 0 || d_in % kQkvK != 0) return kv->fail(NI_ERR_BAD_ARG, "d_in %u must be a positive multiple of %u", d_in, kQkvK);
+    if (n_feat % kQkvTileFeat != 0)
+        return kv->fail(NI_ERR_BAD_ARG, "3 * n_head * head_dim = %u must be a multiple of %u", n_feat, kQkvTileFeat);
+    if (int rc = check_f32_operand(kv, "x", x, x_row_stride, 0, false)) return rc;
+    if (x_row_stride < (int64_t)d_in) return kv->fail(NI_ERR_BAD_ARG, "x row stride %lld < d_in %u", (long long)x_row_stride, d_in);
+    if (!w || !aligned16(w)) return kv->fail(NI_ERR_BAD_ARG, "w must be a 16-byte aligned [3C][d_in] f32 matrix");
+    if (bias && (reinterpret_cast<uintptr_t>(bias) & 3u)) return kv->fail(NI_ERR_BAD_ARG, "bias must be 4-byte aligned");
+    if (int rc = check_f32_operand(kv, fused ? "q_out" : "out", out, out_row_stride, 0, false)) return rc;
+    if (out_row_stride < (int64_t)(fused ? C : n_feat))
+        return kv->fail(NI_ERR_BAD_ARG, "output row stride %lld < %u", (long long)out_row_stride, fused ? C : n_feat);
+    reset_plan(kv);
+    if (fused)
+        for (uint32_t i = 0; i < n; i++) {
+            if (int rc = check_row(kv, rows[i])) return rc;
+            const ni_row& r = rows[i];
+            kv->plan.app.push_back({i, kv->pages[r.seq][r.pos / kPage], r.pos % kPage, 0});
+        }
+    Offsets off;
+    PlanRef ref;
+    if (int rc = place_plan(kv, s, &off, &ref)) return rc;
+    QkvLaunch q;
+    q.pool = kv->geom();
+    q.x = x;
+    q.x_row_stride = x_row_stride;
+    q.w = w;
+    q.bias = bias;
+    q.out = out;
+    q.out_row_stride = out_row_stride;
+    q.plan = ref.dev;
+    q.off_entries = (uint32_t)off.app;
+    q.n_rows = n;
+    q.d_in = d_in;
+    q.n_feat = n_feat;
+    q.layer = fused ? (uint32_t)layer : 0u;
+    q.fused = fused;
+    {
+        ProfileScope ps(kv, NI_K_QKV);
+        hipError_t e = launch_qkv(q, ref.inl, ref.inl_bytes, s, ps.t);
+        if (e != hipSuccess) return kv->hip_fail(e, "qkv kernel");
+    }
+    return release_plan(kv, ref, s);
+}
+
+int ni_kv_qkv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* x,
+                     int64_t x_row_stride, uint32_t d_in, const float* w, const float* bias, float* q_out,
+                     int64_t q_row_stride, ni_stream stream) {
+    if (kv && n && !rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
+    static const ni_row none{0, 0};
+    return qkv_run(kv, layer, rows ? rows : &none, n, x, x_row_stride, d_in, w, bias, q_out, q_row_stride,
+                   (hipStream_t)stream);
+}
+
+int ni_kv_qkv_project(ni_kv* kv, const float* x, int64_t x_row_stride, uint32_t n, uint32_t d_in, const float* w,
+                      const float* bias, float* out, int64_t out_row_stride, ni_stream stream) {
+    return qkv_run(kv, 0, nullptr, n, x, x_row_stride, d_in, w, bias, out, out_row_stride, (hipStream_t)stream);
+}
+
 int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint16_t* k_out, uint16_t* v_out,
                  int64_t row_stride, int64_t layer_stride, ni_stream stream) {
     if (!kv) return NI_ERR_BAD_ARG;

@@ -461,6 +461,101 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
     }
 }
 
+// ------------------------------------------------------- QKV projection
+
+// y = x W^T + b on the matrix cores in f32 (v_mfma_f32_16x16x4f32), the
+// reference's QKV matvec with its epilogue
+// (matvec_batch<..., BEPI_QKV>, batch.metal:94-165): q to `out`, k/v as f16
+// straight into the rows' page slots, so f32 K/V never travel through HBM.
+//
+// A workgroup computes a 32-row x 16- or 32-feature tile; its 4 waves take
+// every 4th 16-wide slice of d_in and add their partial tiles in LDS in wave
+// order, so the result does not depend on scheduling.  In a slice, lane l
+// loads 4 consecutive x values of row l%16 and 4 of W's feature l%16 at
+// offset 4*(l/16); product c of the slice uses component c of both, so
+// lane group g supplies k = 4g + c to A and B alike.
+// FB feature blocks of 16 per tile (the tile is 32 rows x 16*FB features).
+// 4 waves take every 4th 16-wide slice of d_in.
+template <int FB, int INL>
+__global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int NW = 4;
+    __shared__ float red[NW][2][FB][4][64];  // [wave][row block][feature block][element][lane]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t m0 = blockIdx.x * kQkvTileRows, n0 = blockIdx.y * (16 * FB);
+    const int i = lane & 15, g = lane >> 4;
+    // Rows past n_rows read the last row (their results are not stored).
+    const float* xr[2];
+    const float* wr[FB];
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const uint32_t row = min(m0 + 16 * b + i, a.n_rows - 1);
+        xr[b] = a.x + (int64_t)row * a.x_row_stride + 4 * g;
+    }
+#pragma unroll
+    for (int b = 0; b < FB; b++) wr[b] = a.w + (uint64_t)(n0 + 16 * b + i) * a.d_in + 4 * g;
+    f4 acc[2][FB];
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) acc[tb][fb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t k0 = wave * kQkvK; k0 < a.d_in; k0 += NW * kQkvK) {
+        float4 xv[2], wv[FB];
+#pragma unroll
+        for (int b = 0; b < 2; b++) xv[b] = *reinterpret_cast<const float4*>(xr[b] + k0);
+#pragma unroll
+        for (int b = 0; b < FB; b++) wv[b] = *reinterpret_cast<const float4*>(wr[b] + k0);
+#pragma unroll
+        for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) {
+                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].x, wv[fb].x, acc[tb][fb], 0, 0, 0);
+                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].y, wv[fb].y, acc[tb][fb], 0, 0, 0);
+                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].z, wv[fb].z, acc[tb][fb], 0, 0, 0);
+                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].w, wv[fb].w, acc[tb][fb], 0, 0, 0);
+            }
+    }
+#pragma unroll
+    for (int tb = 0; tb < 2; tb++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) red[wave][tb][fb][e][lane] = acc[tb][fb][e];
+    __syncthreads();
+    // Thread t: feature n0 + t%(16FB) of rows t/(16FB), + RSTEP, ...  Output
+    // (row r, feature f) sits at lane f%16 + 16*((r%16)/4), element r%4 of
+    // block (r/16, f/16); the waves' partials are added in wave order.
+    constexpr uint32_t TF = 16 * FB, RSTEP = 64 * NW / TF;
+    const uint32_t fcol = threadIdx.x % TF, r0 = threadIdx.x / TF;
+    const uint32_t f = n0 + fcol;
+    const float b = a.bias ? a.bias[f] : 0.f;
+    const uint32_t C = a.n_feat / 3, D = a.pool.head_dim;
+    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
+#pragma unroll
+    for (uint32_t r = r0; r < kQkvTileRows; r += RSTEP) {
+        const uint32_t row = m0 + r;
+        if (row >= a.n_rows) break;
+        const int tb = r >> 4, ri = r & 15, fb = fcol >> 4;
+        const int src_lane = (fcol & 15) + 16 * (ri >> 2), el = ri & 3;
+        float y = red[0][tb][fb][el][src_lane];
+#pragma unroll
+        for (int w = 1; w < NW; w++) y += red[w][tb][fb][el][src_lane];
+        y += b;
+        if (!a.fused || f < C) {
+            a.out[(int64_t)row * a.out_row_stride + f] = y;
+        } else {
+            const AppendEntry en = entries[row];
+            const uint32_t is_v = f >= 2 * C;
+            const uint32_t c = f - C - is_v * C, head = c / D, d = c - head * D;
+            uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)a.layer * a.pool.layer_halves +
+                            (uint64_t)en.page * a.pool.page_halves + (uint64_t)head * a.pool.head_halves +
+                            en.slot * D + d;
+            *dst = (uint16_t)f16_bits(y);
+        }
+    }
+}
+
 // ------------------------------------------------ attention, several queries
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
@@ -489,14 +584,15 @@ constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
 // layout), so the softmax state of a query lives in lanes q, q+16, q+32, q+48.
 // Waves take the item's pages round-robin and merge through LDS at the end,
 // as in attn_split_kernel.
-// Waves per SIMD the register allocation must allow: 4 (<= 128 registers,
-// no spills) measured 3.9% faster on config 5 than the unconstrained 3.
+// Waves per SIMD the register allocation must allow at head_dim 64: 4 (<= 128
+// registers, no spills) measured 3.9% faster on config 5 than the
+// unconstrained 3.  (head_dim 128 needs ~250 registers: 2 waves.)
 #ifndef NI_MFMA_MIN_WAVES
 #define NI_MFMA_MIN_WAVES 4
 #endif
 template <int D, int W, int PB, bool FUSED, int INL>
-__global__ __launch_bounds__(64 * W, NI_MFMA_MIN_WAVES) void attn_mfma_kernel(const AttnLaunch a,
-                                                                              const PlanArg<INL> pa) {
+__global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_mfma_kernel(const AttnLaunch a,
+                                                                                            const PlanArg<INL> pa) {
     constexpr int QC = D / 32;      // 32-dim chunks of the QK product
     constexpr int VC = D / 16;      // 16-dim chunks of the PV product
     constexpr int LPK = D / 8;      // lanes per key row in a coalesced V load
@@ -896,6 +992,31 @@ hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hip
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         return go(kv_append_kernel<INL>, (threads + 255) / 256, 256, s, t, a, pa);
+    });
+}
+
+#ifndef NI_QKV_NARROW_ROWS
+#define NI_QKV_NARROW_ROWS 64
+#endif
+// The kernel is limited by the scattered W rows each load instruction
+// touches (16 rows, 64 B each, 3 KB apart at d_in 768), not by how many
+// slices a wave keeps in flight: 8 or 16 waves per tile with 4 slices
+// loaded ahead measured slower (0.145 vs 0.131 ms for 12 layers of 64 rows).
+
+hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
+    if (a.n_rows == 0) return hipSuccess;
+    const uint32_t row_tiles = (a.n_rows + kQkvTileRows - 1) / kQkvTileRows;
+    // Few rows: 16-feature tiles, twice the workgroups to stream W with.
+    const bool narrow = a.n_rows <= NI_QKV_NARROW_ROWS;
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        if (narrow)
+            hipExtLaunchKernelGGL(qkv_kernel<1, INL>, dim3(row_tiles, a.n_feat / 16), dim3(256), 0, s, t.start,
+                                  t.stop, 0, a, pa);
+        else
+            hipExtLaunchKernelGGL(qkv_kernel<2, INL>, dim3(row_tiles, a.n_feat / 32), dim3(256), 0, s, t.start,
+                                  t.stop, 0, a, pa);
+        return hipGetLastError();
     });
 }
 

@@ -94,6 +94,28 @@ struct GatherLaunch {
     uint32_t n_lay;
 };
 
+// The QKV projection y = x W^T + b of n rows (W [n_feat][d_in] row-major, the
+// reference's weight layout, n_feat = 3C).  Fused: q columns to `out`
+// ([n][C]), k/v columns as f16 to each row's page slot of `layer` (entries
+// in the plan, src_row = x row).  Plain: every column to `out` ([n][3C]).
+struct QkvLaunch {
+    PoolGeom pool;
+    const float* x;
+    int64_t x_row_stride;
+    const float* w;
+    const float* bias;  // [n_feat] or null
+    float* out;
+    int64_t out_row_stride;
+    const uint8_t* plan;
+    uint32_t off_entries;
+    uint32_t n_rows;
+    uint32_t d_in;
+    uint32_t n_feat;
+    uint32_t layer;
+    uint32_t fused;
+};
+constexpr uint32_t kQkvTileRows = 32, kQkvTileFeat = 32, kQkvK = 16;  // d_in must be a multiple of kQkvK
+
 struct AttnLaunch {
     PoolGeom pool;
     // Fused append (0 rows when the step's rows were appended beforehand):
@@ -152,6 +174,8 @@ hipError_t launch_attention(const AttnLaunch& a, const void* inline_plan, uint32
 hipError_t launch_merge(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
                         const LaunchTiming& t = {});
 hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s);
+hipError_t launch_qkv(const QkvLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
+                      const LaunchTiming& t = {});
 // Blocks a fused launch needs for its orphan rows (n_orphans set).
 uint32_t orphan_blocks(const AttnLaunch& a);
 bool attention_supported(uint32_t head_dim);

@@ -3,8 +3,11 @@
 // loop (`spec`) on the device, launched per step or per layer, printed as
 // one JSON line.
 //
-//   ni_drive [serve|spec] [--per-layer] [--steps K] [--warmup W] [--split T]
-//            [--all-prompt-rows] [--seed S]
+//   ni_drive [serve|spec|qkv] [--per-layer] [--steps K] [--warmup W] [--split T]
+//            [--all-prompt-rows] [--seed S] [--rows N]
+//
+// qkv: the QKV projection of N rows per layer with K/V appended in its
+// epilogue; --per-layer runs the unfused path (f32 projection + append).
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -31,7 +34,8 @@ int main(int argc, char** argv) {
             }
             return argv[++i];
         };
-        if (!strcmp(a, "serve") || !strcmp(a, "spec")) workload = a;
+        if (!strcmp(a, "serve") || !strcmp(a, "spec") || !strcmp(a, "qkv")) workload = a;
+        else if (!strcmp(a, "--rows")) o.qkv_rows = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--per-layer")) o.launch = NI_DRIVE_PER_LAYER;
         else if (!strcmp(a, "--all-prompt-rows")) o.serve.query_all_prompt_rows = 1;
         else if (!strcmp(a, "--steps")) o.steps = (uint32_t)atoi(val(a));
@@ -39,8 +43,8 @@ int main(int argc, char** argv) {
         else if (!strcmp(a, "--split")) o.split_tokens = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--seed")) o.data_seed = o.serve.seed = strtoull(val(a), nullptr, 10);
         else {
-            fprintf(stderr, "usage: ni_drive [serve|spec] [--per-layer] [--steps K] [--warmup W] [--split T] "
-                            "[--all-prompt-rows] [--seed S]\n");
+            fprintf(stderr, "usage: ni_drive [serve|spec|qkv] [--per-layer] [--steps K] [--warmup W] [--split T] "
+                            "[--all-prompt-rows] [--seed S] [--rows N]\n");
             return 2;
         }
     }
@@ -54,6 +58,13 @@ int main(int argc, char** argv) {
         o.kv.max_seqs = o.serve.max_batch;
         o.kv.max_ctx = 1024;
         o.kv.max_rows = o.serve.max_rows;
+    } else if (workload == "qkv") {
+        o.workload = NI_DRIVE_QKV;
+        if (o.qkv_rows == 0) o.qkv_rows = 64;
+        o.kv.kv_pages = 64 * 64;
+        o.kv.max_seqs = 64;
+        o.kv.max_ctx = 1024;
+        o.kv.max_rows = 512;
     } else {
         o.workload = NI_DRIVE_SPEC;
         o.spec_seqs = 32;
@@ -73,6 +84,9 @@ int main(int argc, char** argv) {
         return 1;
     }
     const double gbs = r.bytes / r.seconds / 1e9;
+    if (workload == "qkv")
+        fprintf(stderr, "ni_drive: qkv %u rows: %.2f TFLOP/s, %.3f ms per iteration (12 layers)\n", o.qkv_rows,
+                r.flops / r.seconds / 1e12, r.seconds / r.steps * 1e3);
     printf("{\"driver\": \"ni_drive\", \"workload\": \"%s\", \"launch\": \"%s\", \"steps\": %u, \"warmup\": %u, "
            "\"value\": %.2f, \"unit\": \"GB/s\", \"pct_of_peak\": %.2f, \"ms_per_step\": %.5f, "
            "\"gpu_ms_per_step\": %.5f, \"host_us_per_step\": %.1f, \"abi_calls_per_step\": %.1f, "

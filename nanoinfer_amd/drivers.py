@@ -38,17 +38,18 @@ class ni_drive_opts(C.Structure):
                 ("spec_seqs", _u32), ("spec_ctx_min", _u32), ("spec_ctx_max", _u32), ("spec_k", _u32),
                 ("spec_seed", C.c_uint64), ("spec_window", _u32), ("warmup", _u32), ("steps", _u32),
                 ("split_tokens", _u32), ("data_seed", C.c_uint64), ("fixed_ctx", C.POINTER(_u32)),
-                ("fixed_n", _u32), ("kv_std", C.c_float), ("profile_mask", _u32)]
+                ("fixed_n", _u32), ("kv_std", C.c_float), ("profile_mask", _u32), ("qkv_rows", _u32)]
 
 
 class ni_drive_result(C.Structure):
     _fields_ = [("seconds", C.c_double), ("gpu_seconds", C.c_double), ("bytes", C.c_double),
                 ("seq_tokens", C.c_double), ("host_us_per_step", C.c_double), ("steps", _u32),
                 ("launches", C.c_uint64), ("mean_live", C.c_double), ("mean_context", C.c_double),
-                ("kernel_ms", C.c_double * 3), ("kernel_launches", C.c_uint64 * 3)]
+                ("flops", C.c_double),
+                ("kernel_ms", C.c_double * _abi.NI_K_COUNT), ("kernel_launches", C.c_uint64 * _abi.NI_K_COUNT)]
 
 
-NI_DRIVE_SERVE, NI_DRIVE_SPEC, NI_DRIVE_FIXED = 0, 1, 2
+NI_DRIVE_SERVE, NI_DRIVE_SPEC, NI_DRIVE_FIXED, NI_DRIVE_QKV = 0, 1, 2, 3
 NI_DRIVE_STEP, NI_DRIVE_PER_LAYER = 0, 1
 
 
@@ -219,6 +220,11 @@ def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, spli
         o.kv_std = 0.5
         o.split_tokens = split or 512
         _kv(o, workloads.LONG, B * L // 16, B, L, 4096, workloads.XorShift.seeded(4).permutation(B * L // 16))
+    elif name.startswith("qkv"):
+        # qkv<rows>: the projection of <rows> rows per layer, GPT-2 shape
+        o.workload = NI_DRIVE_QKV
+        o.qkv_rows = int(name[3:] or 64)
+        _kv(o, workloads.GPT2, 64 * 64, 64, 1024, 512)
     else:
         raise ValueError(name)
     return o

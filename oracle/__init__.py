@@ -82,6 +82,7 @@ def lib():
     L.or_paged_attention.argtypes = [_f32p, _sz, _f32p, _sz, _u16p, _u16p, _u32p, C.c_uint32, _u32p, _u32p, _sz,
                                      _sz, _sz, _f32p]
     L.or_split_attention_f64.argtypes = [_f64p, _f32p, _f32p, _f32p, _sz, _sz, _sz]
+    L.or_matvec_f64.argtypes = [_f64p, _f32p, _sz, _f32p, C.c_void_p, _sz, _sz, _sz]
     L.or_alloc_new.restype = C.c_void_p
     L.or_alloc_new.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p]
     L.or_alloc_free.argtypes = [C.c_void_p]
@@ -220,6 +221,19 @@ def split_attention_f64(q, k, v, part):
     n_kv = k.size // hd
     out = np.zeros(hd, np.float64)
     lib().or_split_attention_f64(out, q, k.reshape(-1), v.reshape(-1), hd, n_kv, part)
+    return out
+
+
+def matvec_f64(x, w, bias=None):
+    """batch.metal:94-165 in double: x [n][d_in] f32, w [d_out][d_in] f32,
+    bias [d_out] or None -> [n][d_out] float64."""
+    x, w = _f32(x), _f32(w)
+    n, d_in = x.shape
+    d_out = w.shape[0]
+    assert w.shape[1] == d_in
+    out = np.zeros((n, d_out), np.float64)
+    b = None if bias is None else _f32(bias)
+    lib().or_matvec_f64(out, x.reshape(-1), d_in, w.reshape(-1), None if b is None else b.ctypes.data, n, d_in, d_out)
     return out
 
 

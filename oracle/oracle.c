@@ -713,3 +713,22 @@ void or_cpu_step(or_pool* pool, uint16_t* kp, uint16_t* vp, size_t kv_blocks, co
             for (size_t ch = 0; ch < chunks; ch++) attn_chunk(&j, ch);
     }
 }
+
+/* ------------------------------------------------------------------------- */
+/* QKV projection (the matvec whose epilogue appends K/V)                     */
+/* ------------------------------------------------------------------------- */
+
+/* crates/metal/src/shaders/batch.metal:94-165 (matvec_batch): for each token t
+ * and output row f, s = sum_j w[f][j] * x[t][j] (+ bias[f]) with W stored
+ * [d_out][d_in] row-major.  The reference sums in f32 in its lanes' order;
+ * this restatement sums in double, the ground truth an f32 kernel is held to
+ * within f32 rounding.  out [n][d_out]. */
+void or_matvec_f64(double* out, const float* x, size_t x_stride, const float* w, const float* bias, size_t n,
+                   size_t d_in, size_t d_out) {
+    for (size_t t = 0; t < n; t++)
+        for (size_t f = 0; f < d_out; f++) {
+            double s = 0;
+            for (size_t j = 0; j < d_in; j++) s += (double)w[f * d_in + j] * (double)x[t * x_stride + j];
+            out[t * d_out + f] = s + (bias ? (double)bias[f] : 0.0);
+        }
+}

@@ -1,0 +1,138 @@
+"""The QKV projection with the append in its epilogue (ni_kv_qkv_append,
+the reference's BEPI_QKV epilogue, batch.metal:94-165) on the device.
+
+* ni_kv_qkv_project (the same kernel, every column to f32) is within f32
+  rounding of the oracle's double-precision matvec.
+* ni_kv_qkv_append stores exactly f32_to_f16 of those f32 k/v columns in the
+  rows' page slots (bit for bit, through the gather), returns the same q
+  columns bit for bit, and attention over the stored K/V matches the oracle.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import nanoinfer_amd as na
+from nanoinfer_amd import workloads
+from paged_mirror import assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+def make(shape, n_ctx=1024, kv_blocks=256, max_rows=512):
+    return na.PagedKv(na.BatchOpts(**shape, kv_blocks=kv_blocks, max_seqs=8, n_ctx=n_ctx, max_rows=max_rows))
+
+
+def weights(rng, c, d_in, bias=True):
+    # GPT-2-like scale: W ~ N(0, 0.02^2) would make q/k tiny; 1/sqrt(d_in)
+    # keeps outputs ~N(0,1) so f16 rounding is exercised at full range.
+    w = (rng.standard_normal((3 * c, d_in)) / np.sqrt(d_in)).astype(np.float32)
+    b = (rng.standard_normal(3 * c) * 0.1).astype(np.float32) if bias else None
+    return w, b
+
+
+@pytest.mark.parametrize("shape", [workloads.GPT2, dict(n_layer=2, n_head=4, head_dim=128)], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("n", [1, 37, 512])
+def test_project_matches_f64(gpu, oracle_lib, shape, n):
+    rng = np.random.default_rng(60 + n)
+    kv = make(shape)
+    c = kv.opts.n_embd
+    d_in = 768
+    x = rng.standard_normal((n, d_in)).astype(np.float32)
+    w, b = weights(rng, c, d_in)
+    got = kv.qkv_project(torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda())
+    torch.cuda.synchronize()
+    got = got.cpu().numpy().astype(np.float64)
+    want = oracle.matvec_f64(x, w, b)
+    err = np.abs(got - want)
+    # f32 sums of 768 products of N(0,1/768)-scaled terms: ~1e-6 absolute
+    assert err.max() < 2e-5, err.max()
+    say(f"{shape} n {n}: max abs err vs f64 {err.max():.2e}")
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_fused_append_is_f16_of_projection(gpu, oracle_lib, bias):
+    shape = workloads.GPT2
+    rng = np.random.default_rng(70)
+    kv = make(shape)
+    c = kv.opts.n_embd
+    d_in = 768
+    # two sequences, rows at arbitrary positions spanning pages
+    a, b_ = kv.add_seq(), kv.add_seq()
+    kv.reserve(a, 300)
+    kv.reserve(b_, 40)
+    rows = [(a, p) for p in (0, 15, 16, 17, 255, 299)] + [(b_, p) for p in range(3, 40, 4)]
+    n = len(rows)
+    x = rng.standard_normal((n, d_in)).astype(np.float32)
+    w, bb = weights(rng, c, d_in, bias)
+    xd, wd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+    bd = torch.from_numpy(bb).cuda() if bias else None
+    for layer in (0, 11):
+        y = kv.qkv_project(xd, wd, bd)
+        q = kv.qkv_append(rows, xd, wd, bd, layer=layer)
+        torch.cuda.synchronize()
+        y = y.cpu().numpy()
+        assert np.array_equal(q.cpu().numpy(), y[:, :c])
+        kg, vg = kv.gather(rows, layer=layer)
+        assert np.array_equal(kg.cpu().numpy().view(np.uint16), oracle.f32_to_f16(y[:, c:2 * c]))
+        assert np.array_equal(vg.cpu().numpy().view(np.uint16), oracle.f32_to_f16(y[:, 2 * c:]))
+
+
+def test_attention_over_projected_kv(gpu, oracle_lib):
+    """Prefill a sequence through the fused projection (per layer), then
+    decode-attend its last row: within the north star's bound of the oracle
+    over the same f16 K/V."""
+    shape = dict(n_layer=2, n_head=12, head_dim=64)
+    rng = np.random.default_rng(71)
+    kv = make(shape)
+    c, d_in, L = 768, 768, 200
+    s = kv.add_seq()
+    kv.reserve(s, L)
+    rows = [(s, p) for p in range(L)]
+    pools = oracle.PagedPools(2, 256, c)
+    qs = []
+    for layer in range(2):
+        x = rng.standard_normal((L, d_in)).astype(np.float32)
+        w, b = weights(rng, c, d_in)
+        xd, wd, bd = (torch.from_numpy(t).cuda() for t in (x, w, b))
+        y = kv.qkv_project(xd, wd, bd).cpu().numpy()
+        qs.append(kv.qkv_append(rows, xd, wd, bd, layer=layer).cpu().numpy())
+        table = np.zeros((8, kv.max_blocks), np.uint32)
+        bt = kv.block_table(s)
+        table[s, :len(bt)] = bt
+        r = np.asarray(rows, np.uint32)
+        oracle.paged_append(pools, layer, table, kv.max_blocks, r[:, 0], r[:, 1], y[:, c:2 * c], y[:, 2 * c:])
+    kv.commit(s, L)
+    q = np.stack([qs[l][-1:] for l in range(2)])
+    got = kv.attention(torch.from_numpy(q).cuda(), [(s, L - 1)]).cpu().numpy()
+    table = np.zeros((8, kv.max_blocks), np.uint32)
+    bt = kv.block_table(s)
+    table[s, :len(bt)] = bt
+    want = np.stack([oracle.paged_attention(pools, l, table, kv.max_blocks, np.array([s], np.uint32),
+                                            np.array([L - 1], np.uint32), q[l], 12, 64) for l in range(2)])
+    err = assert_close(got, want, "attention over projected K/V")
+    say(f"attention over projected K/V: max abs err {err:.2e}")
+
+
+def test_qkv_errors(gpu):
+    kv = make(dict(n_layer=2, n_head=2, head_dim=64), kv_blocks=8, n_ctx=64, max_rows=16)
+    s = kv.add_seq()
+    kv.reserve(s, 4)
+    c = 128
+    w = torch.zeros((3 * c, 64), device="cuda")
+    x = torch.zeros((2, 64), device="cuda")
+    with pytest.raises(na.KvError, match="layer 2 out of range"):
+        kv.qkv_append([(s, 0), (s, 1)], x, w, layer=2)
+    with pytest.raises(na.KvError, match="has no page"):
+        kv.qkv_append([(s, 0), (s, 16)], x, w)
+    w40 = torch.zeros((3 * c, 40), device="cuda")
+    with pytest.raises(na.KvError, match="multiple of 16"):
+        kv.qkv_project(torch.zeros((2, 40), device="cuda"), w40)
+    with pytest.raises(na.KvError, match="max_rows"):
+        kv.qkv_project(torch.zeros((17, 64), device="cuda"), w)
