@@ -304,6 +304,12 @@ SECONDARY = {
     "config5": ("config5: spec verify, 32 seqs, ctx U[128,1024], append g + 4 drafts, 5 causal queries, accept U[0,4], "
                 "truncate", {"draft_k": 4, "reset_window": SPEC_WINDOW}),
 }
+# The same workloads on a Q8 cache (NI_KV_Q8: int8 + an f32 scale per position and head); algorithmic
+# bytes count the Q8 bytes, so compare formats by seq_tokens_per_s.
+for _name in list(SECONDARY):
+    SECONDARY[_name + "q8"] = (SECONDARY[_name][0] + "; Q8 KV cache", dict(SECONDARY[_name][1], kv_format="q8"))
+SECONDARY["config3q8"] = ("config3: continuous batching (bench default trace); Q8 KV cache",
+                          {"kv_format": "q8", "prefill_attention": "last prompt row only"})
 
 
 def run_secondary(args):
@@ -315,8 +321,11 @@ def run_secondary(args):
                 "synthetic (seeded normal q/k/v resident in HBM)")
     if not args.no_profile:
         rp = _drive(args.workload, args, profile_mask=(1 << 1) | (1 << 2))
-        res["roofline"] = _roofline(rp, "attn_split_kernel / attn_mfma_kernel (+ attn_merge_kernel when split)",
+        res["roofline"] = _roofline(rp, "attn_q8_kernel (+ attn_merge_kernel when split)" if args.workload.endswith("q8")
+                                    else "attn_split_kernel / attn_mfma_kernel (+ attn_merge_kernel when split)",
                                     with_merge=True)
+    if args.workload.endswith("q8"):
+        res["kv_dtype"] = "int8 + f32 scale per (position, head)"
     return res
 
 

@@ -60,6 +60,14 @@ enum ni_status {
 /* ni_kv_opts.flags: keep only the host bookkeeping (no device memory); the
  * data-path calls then fail with NI_ERR_NO_DEVICE.  For tests without a GPU. */
 #define NI_KV_HOST_ONLY 1u
+/* ni_kv_opts.flags: the Q8 cache (crates/metal/src/shaders/kv8.metal:1-95):
+ * each (position, head) of K and V is stored as head_dim int8 values and one
+ * f32 scale = amax / 127 (68 bytes per 64 values instead of 128).  Appends
+ * quantise (kv_quant8, :15-48; inputs must be finite), attention dequantises
+ * (attn_decode_split_q8, :50-95); query rows are attended one by one (no
+ * shared K/V reads for groups); ni_kv_gather and ni_kv_qkv_append are
+ * refused (ni_kv_gather_q8 returns the stored bytes). */
+#define NI_KV_Q8 2u
 
 /* Sizes and policies (the KV fields of BatchOpts, batch.rs:44-76, plus the
  * model shape the reference takes from Config, crates/core/src/config.rs:23). */
@@ -151,6 +159,12 @@ int ni_kv_qkv_project(ni_kv* kv, const float* x, int64_t x_row_stride, uint32_t 
 int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint16_t* k_out, uint16_t* v_out,
                  int64_t row_stride, int64_t layer_stride, ni_stream stream);
 
+/* Q8 handles: the stored int8 values [n_lay][n][C] (n_lay = n_layer for
+ * NI_ALL_LAYERS, else 1) and scales [n_lay][n][n_head] of each row, dense;
+ * k_out/v_out 16-byte aligned. */
+int ni_kv_gather_q8(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, int8_t* k_out, int8_t* v_out,
+                    float* k_scale, float* v_scale, ni_stream stream);
+
 /* Paged decode attention (b_attn_split + b_attn_merge, batch.metal:349-424;
  * math of kv16.rs:144-164): row i attends causally to keys 0..rows[i].pos
  * of rows[i].seq; out row i = softmax(q.K^T / sqrt(head_dim)) V.  Keys are
@@ -191,9 +205,9 @@ int ni_kv_decode_steps(ni_kv* kv, const uint32_t* seqs, uint32_t n, uint32_t ste
 int ni_kv_sync(ni_kv* kv, ni_stream stream);
 
 /* The device pool, for inspection: one allocation of `bytes`, laid out
- * [n_layer][kv_pages][n_head][K|V][16][head_dim] f16; *k_pool is its start
- * and *v_pool = *k_pool + 16*head_dim halves (V follows K in every
- * (page, head) block). */
+ * [n_layer][kv_pages][n_head][K block][V block]; *k_pool is its start and
+ * *v_pool the first V block.  f16: a block is [16][head_dim] f16.  Q8: a
+ * block is [16][head_dim] int8 then 16 f32 scales. */
 int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes);
 
 /* quant.rs:25-54 on the device, elementwise (the conversion the append uses). */

@@ -17,6 +17,7 @@ HEADER = os.path.join(_build.INCLUDE, "nanoinfer_kv.h")
 NI_KV_BLOCK = 16
 NI_ALL_LAYERS = -1
 NI_KV_HOST_ONLY = 1
+NI_KV_Q8 = 2
 
 NI_OK = 0
 NI_ERR_NO_SLOT = 1
@@ -99,6 +100,8 @@ def _declare(L):
     L.ni_kv_qkv_append.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _i64, _u32, _vp, _vp, _vp, _i64, _vp]
     L.ni_kv_qkv_project.restype = C.c_int
     L.ni_kv_qkv_project.argtypes = [_vp, _vp, _i64, _u32, _u32, _vp, _vp, _vp, _i64, _vp]
+    L.ni_kv_gather_q8.restype = C.c_int
+    L.ni_kv_gather_q8.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _vp, _vp, _vp, _vp]
     L.ni_kv_gather.restype = C.c_int
     L.ni_kv_gather.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _vp, _i64, _i64, _vp]
     L.ni_paged_decode_attention.restype = C.c_int

@@ -63,6 +63,7 @@ class BatchOpts:
     max_rows: int = 512
     host_only: bool = False
     page_order: Optional[Sequence[int]] = None  # order in which pages are handed out
+    q8: bool = False  # int8 K/V + f32 scale per (position, head) (kv8.metal)
 
     @property
     def n_embd(self) -> int:
@@ -121,7 +122,7 @@ class PagedKv:
         o = _abi.ni_kv_opts()
         o.n_layer, o.n_head, o.head_dim = opts.n_layer, opts.n_head, opts.head_dim
         o.kv_pages, o.max_seqs, o.max_ctx, o.max_rows = opts.kv_blocks, opts.max_seqs, opts.n_ctx, opts.max_rows
-        o.flags = _abi.NI_KV_HOST_ONLY if opts.host_only else 0
+        o.flags = (_abi.NI_KV_HOST_ONLY if opts.host_only else 0) | (_abi.NI_KV_Q8 if opts.q8 else 0)
         self._order = None
         if opts.page_order is not None:
             self._order = np.ascontiguousarray(np.asarray(opts.page_order, dtype=np.uint32))
@@ -265,6 +266,22 @@ class PagedKv:
         self._check(self._L.ni_kv_gather(self._h, layer, rp, n, ko.data_ptr(), vo.data_ptr(), c, ls,
                                          _stream_ptr(stream)))
         return ko, vo
+
+    def gather_q8(self, rows, layer: int = ALL_LAYERS, stream=None):
+        """Q8 handles: (k int8, v int8) [n_lay, n, C] and (k scale, v scale)
+        float32 [n_lay, n, n_head] of each (seq, pos) row."""
+        import torch
+
+        arr, rp, n = _rows(rows)
+        n_lay = self.opts.n_layer if layer == ALL_LAYERS else 1
+        c, h = self.opts.n_embd, self.opts.n_head
+        ko = torch.empty((n_lay, n, c), dtype=torch.int8, device="cuda")
+        vo = torch.empty_like(ko)
+        ks = torch.empty((n_lay, n, h), dtype=torch.float32, device="cuda")
+        vs = torch.empty_like(ks)
+        self._check(self._L.ni_kv_gather_q8(self._h, layer, rp, n, ko.data_ptr(), vo.data_ptr(), ks.data_ptr(),
+                                            vs.data_ptr(), _stream_ptr(stream)))
+        return (ko, vo), (ks, vs)
 
     def attention(self, q, rows, out=None, layer: int = ALL_LAYERS, split_tokens: int = 0, stream=None):
         """Paged decode attention of each row over keys 0..pos of its sequence."""

@@ -41,6 +41,8 @@ def command(out: str = LIB) -> list[str]:
         hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
         # Packed-FP32 VALU forms stay off: ordinary f32 code only.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # Q8 scales: amax / 127 and its inverse must be IEEE divisions.
+        "-fhip-fp32-correctly-rounded-divide-sqrt",
         "-Wall", "-Wno-unused-function",
         f"-I{INCLUDE}", f"-I{CSRC}",
         *SOURCES, "-o", out,

@@ -323,11 +323,13 @@ struct DeviceBufs {
 };
 
 // Algorithmic bytes of one step: each KV byte once, append and q/out rows.
-double step_bytes(const ni_work* w, uint32_t n, const uint32_t* ctx, uint32_t n_layer, uint32_t c) {
+// kvb = stored bytes of one position's K (or V) in one layer: 2C for f16,
+// C + 4 * n_head for Q8 (int8 values and a scale per head).
+double step_bytes(const ni_work* w, uint32_t n, const uint32_t* ctx, uint32_t n_layer, uint32_t c, double kvb) {
     double b = 0;
     for (uint32_t i = 0; i < n; i++) {
-        b += (double)w[i].n_new * c * 12;
-        if (w[i].n_query) b += (double)w[i].n_query * c * 8 + 2.0 * ctx[i] * c * 2 + pages(ctx[i]) * 4.0;
+        b += (double)w[i].n_new * (c * 8.0 + 2 * kvb);
+        if (w[i].n_query) b += (double)w[i].n_query * c * 8 + 2.0 * ctx[i] * kvb + pages(ctx[i]) * 4.0;
     }
     return b * n_layer;
 }
@@ -342,8 +344,11 @@ struct Runner {
     std::vector<ni_row> rows, qrows;
     uint64_t calls = 0;
 
+    double kvb;  // stored bytes of one position's K (or V) in one layer
+
     explicit Runner(const ni_drive_opts& opts) : o(opts), C(opts.kv.n_head * opts.kv.head_dim), L(opts.kv.n_layer) {
         ls = (int64_t)opts.kv.max_rows * C;
+        kvb = (opts.kv.flags & NI_KV_Q8) ? (double)C + 4.0 * opts.kv.n_head : 2.0 * C;
     }
     ~Runner() {
         if (stream) (void)hipStreamDestroy(stream);
@@ -477,7 +482,7 @@ int run_serve(Runner& r, ni_drive_result* res) {
         if (int e = ni_serve_plan(sv, &it)) return e;
         if (int e = r.launch(it.work, it.n_work)) return e;
         if (timed) {
-            res->bytes += step_bytes(it.work, it.n_work, it.ctx_after, r.L, r.C);
+            res->bytes += step_bytes(it.work, it.n_work, it.ctx_after, r.L, r.C, r.kvb);
             for (uint32_t i = 0; i < it.n_work; i++)
                 if (it.work[i].n_query) {
                     res->seq_tokens += 1;
@@ -516,7 +521,7 @@ int run_spec(Runner& r, ni_drive_result* res) {
         const uint32_t* acc = nullptr;
         if (int e = ni_spec_commit(sp, &acc)) return e;
         if (timed) {
-            res->bytes += step_bytes(w, n, ca, r.L, r.C);
+            res->bytes += step_bytes(w, n, ca, r.L, r.C, r.kvb);
             for (uint32_t i = 0; i < n; i++) {
                 res->seq_tokens += acc[i] + 1;  // tokens a verify round yields
                 ctx += ca[i];
@@ -544,7 +549,7 @@ int run_fixed(Runner& r, ni_drive_result* res) {
         seqs.push_back(s);
         work.push_back({s, 1, 1});
     }
-    const double bytes = step_bytes(work.data(), (uint32_t)work.size(), r.o.fixed_ctx, r.L, r.C);
+    const double bytes = step_bytes(work.data(), (uint32_t)work.size(), r.o.fixed_ctx, r.L, r.C, r.kvb);
     int rc = timed_run(r, res, [&](bool timed) -> int {
         if (int e = r.launch(work.data(), (uint32_t)work.size())) return e;
         // Roll back, so the next iteration appends the same positions.

@@ -149,6 +149,7 @@ struct ni_kv {
         g.head_halves = head_halves;
         g.n_head = o.n_head;
         g.head_dim = o.head_dim;
+        g.q8 = (o.flags & NI_KV_Q8) ? 1u : 0u;
         return g;
     }
 };
@@ -200,6 +201,17 @@ int check_row(ni_kv* kv, const ni_row& r) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+bool is_q8(const ni_kv_opts& o) { return (o.flags & NI_KV_Q8) != 0; }
+
+// Rows of one sequence that share one pass over the keys: the matrix-core
+// tile for f16 pools; Q8 pools attend rows one by one.
+uint32_t max_group_rows(const ni_kv* kv) { return is_q8(kv->o) ? 1u : kMaxGroupRows; }
+
+// Halves of one K (or V) block of a (page, head).
+uint64_t kv_block_halves(const ni_kv_opts& o) {
+    return is_q8(o) ? (uint64_t)kPage * o.head_dim / 2 + kPage * 2 : (uint64_t)kPage * o.head_dim;
+}
+
 int check_f32_operand(ni_kv* kv, const char* name, const void* p, int64_t row_stride, int64_t layer_stride,
                       bool all_layers) {
     if (!p) return kv->fail(NI_ERR_BAD_ARG, "%s is NULL", name);
@@ -236,10 +248,11 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     };
     std::vector<Group> groups;
     groups.reserve(qr.size());
+    const uint32_t max_group = max_group_rows(kv);
     for (const QRow& r : qr) {
         if (!groups.empty()) {
             Group& g = groups.back();
-            if (g.seq == r.seq && g.row0 + g.nq == r.row && g.pos0 + g.nq == r.pos && g.nq < kMaxGroupRows) {
+            if (g.seq == r.seq && g.row0 + g.nq == r.row && g.pos0 + g.nq == r.pos && g.nq < max_group) {
                 g.nq++;
                 continue;
             }
@@ -584,6 +597,10 @@ int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
         g_create_error = "n_layer, n_head, kv_pages, max_seqs, max_ctx and max_rows must be > 0; head_dim a multiple of 8";
         return NI_ERR_BAD_ARG;
     }
+    if (o.flags & ~(NI_KV_HOST_ONLY | NI_KV_Q8)) {
+        g_create_error = "unknown flags";
+        return NI_ERR_BAD_ARG;
+    }
     const bool host_only = (o.flags & NI_KV_HOST_ONLY) != 0;
     if (!host_only && !attention_supported(o.head_dim)) {
         g_create_error = "head_dim " + std::to_string(o.head_dim) + " unsupported on the device (64 or 128)";
@@ -625,46 +642,17 @@ int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
     if (!host_only) {
         hipError_t e = hipGetDevice(&kv->device);
         if (e == hipSuccess) {
-            // One allocation, [n_layer][kv_pages][n_head][K|V][16][head_dim]:
-            // a (page, head) holds its K block and then its V block, one
-            // contiguous run of 2 * 16 * head_dim halves.
-            const uint64_t block = (uint64_t)kPage * o.head_dim;
-#ifdef NI_KV_SEPARATE_POOLS
-            kv->head_halves = (uint32_t)block;
-            kv->page_halves = block * o.n_head;
-            kv->layer_halves = kv->page_halves * o.kv_pages;
-            kv->pool_bytes = (size_t)(2 * kv->layer_halves * o.n_layer * sizeof(uint16_t));
-            e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
-            if (e == hipSuccess) kv->vpool = kv->kpool + kv->layer_halves * o.n_layer;
-#elif defined(NI_KV_PAGE_OUTER)
-            // [kv_pages][n_layer][n_head][K|V][16][head_dim]: all of a page together.
-            kv->head_halves = (uint32_t)(2 * block);
-            kv->layer_halves = 2 * block * o.n_head;
-            kv->page_halves = kv->layer_halves * o.n_layer;
-            kv->pool_bytes = (size_t)(kv->page_halves * o.kv_pages * sizeof(uint16_t));
-            e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
-            if (e == hipSuccess) kv->vpool = kv->kpool + block;
-#elif defined(NI_KV_HEAD_MAJOR)
-            // [n_layer][n_head][kv_pages][K|V][16][head_dim]: a head's pages adjacent.
-            kv->page_halves = 2 * block;
-            kv->head_halves = (uint32_t)0;  // set below (may exceed 32 bits? checked)
-            {
-                const uint64_t hh = 2 * block * o.kv_pages;
-                if (hh > 0xffffffffull) e = hipErrorInvalidValue;
-                kv->head_halves = (uint32_t)hh;
-            }
-            kv->layer_halves = (uint64_t)kv->head_halves * o.n_head;
-            kv->pool_bytes = (size_t)(kv->layer_halves * o.n_layer * sizeof(uint16_t));
-            if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
-            if (e == hipSuccess) kv->vpool = kv->kpool + block;
-#else
+            // One allocation, [n_layer][kv_pages][n_head][K|V block]: a
+            // (page, head) holds its K block and then its V block.  f16: a
+            // block is [16][head_dim] halves.  Q8: [16][head_dim] int8 then
+            // 16 f32 scales, 16 * head_dim + 64 bytes (kv_block_halves()).
+            const uint64_t block = kv_block_halves(o);
             kv->head_halves = (uint32_t)(2 * block);
             kv->page_halves = 2 * block * o.n_head;
             kv->layer_halves = kv->page_halves * o.kv_pages;
             kv->pool_bytes = (size_t)(kv->layer_halves * o.n_layer * sizeof(uint16_t));
             e = hipMalloc(reinterpret_cast<void**>(&kv->kpool), kv->pool_bytes);
             if (e == hipSuccess) kv->vpool = kv->kpool + block;
-#endif
         }
         // Zero pages: a page that was never written reads as finite zeros.
         if (e == hipSuccess) e = hipMemset(kv->kpool, 0, kv->pool_bytes);
@@ -710,7 +698,7 @@ void ni_kv_destroy(ni_kv* kv) {
 }
 
 size_t ni_kv_page_bytes(const ni_kv* kv) {
-    return kv ? (size_t)2 * kv->o.n_layer * kPage * kv->o.n_head * kv->o.head_dim * 2 : 0;
+    return kv ? (size_t)2 * kv->o.n_layer * kv->o.n_head * kv_block_halves(kv->o) * 2 : 0;
 }
 
 int ni_kv_add_seq(ni_kv* kv, uint32_t* seq) {
@@ -822,6 +810,8 @@ static int qkv_run(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, con
     if (!kv) return NI_ERR_BAD_ARG;
     if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
     const bool fused = rows != nullptr;
+    if (fused && is_q8(kv->o))
+        return kv->fail(NI_ERR_BAD_ARG, "Q8 cache: project with ni_kv_qkv_project and append with ni_kv_append");
     const uint32_t C = kv->o.n_head * kv->o.head_dim, n_feat = 3 * C;
     if (fused && (layer < 0 || (uint32_t)layer >= kv->o.n_layer))
         return kv->fail(NI_ERR_BAD_ARG, "layer %d out of range (%u layers)", layer, kv->o.n_layer);
@@ -893,6 +883,7 @@ int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint1
     if (n == 0) return NI_OK;
     if (!rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
     if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "%u rows > max_rows %u", n, kv->o.max_rows);
+    if (is_q8(kv->o)) return kv->fail(NI_ERR_BAD_ARG, "Q8 cache: use ni_kv_gather_q8");
     const bool all = layer == NI_ALL_LAYERS;
     if (!k_out || !v_out || !aligned16(k_out) || !aligned16(v_out) || row_stride % 8 != 0 || row_stride < 0 ||
         (all && (layer_stride % 8 != 0 || layer_stride < 0)))
@@ -919,6 +910,45 @@ int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint1
     g.layer0 = layer0;
     g.n_lay = n_lay;
     hipError_t e = launch_gather(g, ref.inl, ref.inl_bytes, s);
+    if (e != hipSuccess) return kv->hip_fail(e, "gather kernel");
+    return release_plan(kv, ref, s);
+}
+
+int ni_kv_gather_q8(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, int8_t* k_out, int8_t* v_out,
+                    float* k_scale, float* v_scale, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    if (!is_q8(kv->o)) return kv->fail(NI_ERR_BAD_ARG, "not a Q8 cache: use ni_kv_gather");
+    uint32_t layer0, n_lay;
+    if (int rc = layer_range(kv, layer, &layer0, &n_lay)) return rc;
+    if (n == 0) return NI_OK;
+    if (!rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
+    if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "%u rows > max_rows %u", n, kv->o.max_rows);
+    if (!k_out || !v_out || !k_scale || !v_scale || !aligned16(k_out) || !aligned16(v_out) ||
+        (reinterpret_cast<uintptr_t>(k_scale) & 3u) || (reinterpret_cast<uintptr_t>(v_scale) & 3u))
+        return kv->fail(NI_ERR_BAD_ARG, "k_out/v_out must be 16-byte aligned, scales 4-byte aligned");
+    reset_plan(kv);
+    for (uint32_t i = 0; i < n; i++) {
+        if (int rc = check_row(kv, rows[i])) return rc;
+        const ni_row& r = rows[i];
+        kv->plan.app.push_back({i, kv->pages[r.seq][r.pos / kPage], r.pos % kPage, 0});
+    }
+    Offsets off;
+    PlanRef ref;
+    hipStream_t s = (hipStream_t)stream;
+    if (int rc = place_plan(kv, s, &off, &ref)) return rc;
+    GatherQ8Launch g;
+    g.pool = kv->geom();
+    g.k_out = k_out;
+    g.v_out = v_out;
+    g.k_scale = k_scale;
+    g.v_scale = v_scale;
+    g.plan = ref.dev;
+    g.off_entries = (uint32_t)off.app;
+    g.n_rows = n;
+    g.layer0 = layer0;
+    g.n_lay = n_lay;
+    hipError_t e = launch_gather_q8(g, ref.inl, ref.inl_bytes, s);
     if (e != hipSuccess) return kv->hip_fail(e, "gather kernel");
     return release_plan(kv, ref, s);
 }
@@ -1050,7 +1080,7 @@ static int enqueue_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const f
     // single query group: then exactly one workgroup per (layer, head, page)
     // touches this step's new rows.
     bool fused = true;
-    for (uint32_t w = 0; w < n_work; w++) fused &= work[w].n_query <= kMaxGroupRows;
+    for (uint32_t w = 0; w < n_work; w++) fused &= work[w].n_query <= max_group_rows(kv);
     kv->plan.fused = fused;
     uint32_t row = 0;
     for (uint32_t w = 0; w < n_work; w++) {

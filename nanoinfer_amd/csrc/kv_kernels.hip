@@ -71,13 +71,14 @@ __device__ __forceinline__ float key_sum(float x) {
 
 // (m, l, o) <- (m, l, o) (+) (m2, l2, o2): the log-sum-exp merge of two
 // partial softmax states (batch.metal:415-423), base 2.
-__device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[8], float m2, float l2,
-                                            const float (&o2)[8]) {
+template <int N>
+__device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[N], float m2, float l2,
+                                            const float (&o2)[N]) {
     const float mn = fmaxf(m, m2);
     const float a1 = fast_exp2(m - mn), a2 = fast_exp2(m2 - mn);
     l = l * a1 + l2 * a2;
 #pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = o[e] * a1 + o2[e] * a2;
+    for (int e = 0; e < N; e++) o[e] = o[e] * a1 + o2[e] * a2;
     m = mn;
 }
 
@@ -130,11 +131,100 @@ __device__ __forceinline__ void append_chunk(const PoolGeom& pool, const float* 
     *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
 }
 
+// ----------------------------------------------------------- Q8 cache
+//
+// kv_quant8 (crates/metal/src/shaders/kv8.metal:15-48): each (position,
+// head) of K or V is stored as int8 with one f32 scale, scale = amax / 127,
+// q = clamp(rint(x * (1 / scale)), -127, 127) (inverse 0 when amax is 0);
+// both divisions correctly rounded, rint to nearest even.  Inputs must be
+// finite.
+
+// A (page, head) block of a Q8 pool as bytes: [16][D] int8, then 16 scales.
+__device__ __forceinline__ uint8_t* q8_block(const PoolGeom& pool, bool is_v, uint64_t off_halves) {
+    return reinterpret_cast<uint8_t*>((is_v ? pool.v : pool.k) + off_halves);
+}
+
+__device__ __forceinline__ uint32_t q8_byte(float x, float inv) {
+    return (uint32_t)(int32_t)fminf(fmaxf(rintf(x * inv), -127.f), 127.f) & 0xffu;
+}
+
+// Quantise 8 values of one (position, head) held by a lane whose aligned
+// group of g = D/8 neighbouring lanes holds the rest; stores the 8 bytes at
+// blk + slot*D + d0 and (lane d0 == 0) the scale.
+__device__ __forceinline__ void q8_store8(uint8_t* blk, uint32_t D, uint32_t slot, uint32_t d0, const float4 x0,
+                                          const float4 x1) {
+    float a = fmaxf(fmaxf(fmaxf(fabsf(x0.x), fabsf(x0.y)), fmaxf(fabsf(x0.z), fabsf(x0.w))),
+                    fmaxf(fmaxf(fabsf(x1.x), fabsf(x1.y)), fmaxf(fabsf(x1.z), fabsf(x1.w))));
+    for (uint32_t off = 1; off < D / 8; off <<= 1) a = fmaxf(a, __shfl_xor(a, off));
+    const float scale = a / 127.f;
+    const float inv = scale > 0.f ? 1.f / scale : 0.f;
+    uint2 q;
+    q.x = q8_byte(x0.x, inv) | q8_byte(x0.y, inv) << 8 | q8_byte(x0.z, inv) << 16 | q8_byte(x0.w, inv) << 24;
+    q.y = q8_byte(x1.x, inv) | q8_byte(x1.y, inv) << 8 | q8_byte(x1.z, inv) << 16 | q8_byte(x1.w, inv) << 24;
+    *reinterpret_cast<uint2*>(blk + slot * D + d0) = q;
+    if (d0 == 0) reinterpret_cast<float*>(blk + kPage * D)[slot] = scale;
+}
+
+// append_chunk for a Q8 pool: the same enumeration; the D/8 lanes of one
+// (layer, row, K|V, head) are consecutive and aligned, and whole groups
+// leave together at the end of the grid.
+__device__ __forceinline__ void append_chunk_q8(const PoolGeom& pool, const float* k, const float* v, int64_t row_stride,
+                                                int64_t layer_stride, const AppendEntry* entries, uint32_t n_rows,
+                                                uint32_t layer0, uint32_t n_lay, uint32_t gid) {
+    const uint32_t D = pool.head_dim;
+    const uint32_t chunks = (pool.n_head * D) >> 3;
+    const uint32_t per_row = 2 * chunks;
+    const uint32_t per_layer = per_row * n_rows;
+    if (gid >= per_layer * n_lay) return;
+    const uint32_t lay = gid / per_layer;
+    uint32_t r = gid - lay * per_layer;
+    const uint32_t row = r / per_row;
+    r -= row * per_row;
+    const uint32_t is_v = r >= chunks;
+    const uint32_t c8 = (r - is_v * chunks) * 8;
+    const AppendEntry e = entries[row];
+    const float* src = (is_v ? v : k) + (int64_t)lay * layer_stride + (int64_t)e.src_row * row_stride + c8;
+    const float4 x0 = reinterpret_cast<const float4*>(src)[0];
+    const float4 x1 = reinterpret_cast<const float4*>(src)[1];
+    const uint32_t head = c8 / D, d0 = c8 - head * D;
+    uint8_t* blk = q8_block(pool, is_v, (uint64_t)(layer0 + lay) * pool.layer_halves +
+                                            (uint64_t)e.page * pool.page_halves + (uint64_t)head * pool.head_halves);
+    q8_store8(blk, D, e.slot, d0, x0, x1);
+}
+
 template <int INL>
 __global__ __launch_bounds__(256) void kv_append_kernel(const AppendLaunch a, const PlanArg<INL> pa) {
     const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
-    append_chunk(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
-                 blockIdx.x * 256u + threadIdx.x);
+    if (a.pool.q8)
+        append_chunk_q8(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
+                        blockIdx.x * 256u + threadIdx.x);
+    else
+        append_chunk(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
+                     blockIdx.x * 256u + threadIdx.x);
+}
+
+// One thread per (layer, row, K|V, head): D int8 values and the scale.
+template <int INL>
+__global__ __launch_bounds__(256) void kv_gather_q8_kernel(const GatherQ8Launch a, const PlanArg<INL> pa) {
+    const uint32_t D = a.pool.head_dim, H = a.pool.n_head;
+    const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t per_layer = a.n_rows * 2 * H;
+    if (gid >= per_layer * a.n_lay) return;
+    const uint32_t lay = gid / per_layer;
+    uint32_t r = gid - lay * per_layer;
+    const uint32_t row = r / (2 * H);
+    r -= row * 2 * H;
+    const uint32_t is_v = r >= H;
+    const uint32_t head = r - is_v * H;
+    const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries)[row];
+    const uint8_t* blk = q8_block(a.pool, is_v, (uint64_t)(a.layer0 + lay) * a.pool.layer_halves +
+                                                    (uint64_t)e.page * a.pool.page_halves +
+                                                    (uint64_t)head * a.pool.head_halves);
+    const uint64_t orow = ((uint64_t)lay * a.n_rows + e.src_row);
+    int8_t* dst = (is_v ? a.v_out : a.k_out) + orow * H * D + head * D;
+    for (uint32_t c = 0; c < D; c += 16)
+        *reinterpret_cast<uint4*>(dst + c) = *reinterpret_cast<const uint4*>(blk + e.slot * D + c);
+    (is_v ? a.v_scale : a.k_scale)[orow * H + head] = reinterpret_cast<const float*>(blk + kPage * D)[e.slot];
 }
 
 template <int INL>
@@ -452,6 +542,222 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
             a.out[(int64_t)lay * a.out_layer_stride + (int64_t)(it.row0 + r) * a.out_row_stride + head * D + d] = O / L;
         } else {
             float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * H + head) * NQ + r) * (D + 2);
+            if (d == 0) {
+                p[0] = M;
+                p[1] = L;
+            }
+            p[2 + d] = O;
+        }
+    }
+}
+
+// ------------------------------------------------------- Q8 attention
+
+// Byte j of w as a signed integer, in f32.
+__device__ __forceinline__ float i8f(uint32_t w, int j) { return (float)((int32_t)(w << (24 - 8 * j)) >> 24); }
+
+// item_append for a Q8 pool: each aligned group of D/8 threads quantises one
+// (row, K|V) of the head.
+template <int D>
+__device__ __forceinline__ void item_append_q8(const AttnLaunch& a, const uint8_t* plan, const AttnItem& it,
+                                               uint32_t lay, uint32_t head, uint64_t layer_off, uint64_t page_stride,
+                                               uint32_t nthreads) {
+    constexpr uint32_t CH = D / 8;
+    for (uint32_t t = threadIdx.x; t < it.napp * 2 * CH; t += nthreads) {
+        const uint32_t row = t / (2 * CH);
+        const uint32_t rem2 = t - row * (2 * CH);
+        const uint32_t is_v = rem2 >= CH;
+        const uint32_t c = (rem2 - is_v * CH) * 8;
+        const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan + a.off_app)[it.app0 + row];
+        const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride + (int64_t)e.src_row * a.kv_row_stride +
+                           head * D + c;
+        const float4 x0 = reinterpret_cast<const float4*>(src)[0];
+        const float4 x1 = reinterpret_cast<const float4*>(src)[1];
+        q8_store8(q8_block(a.pool, is_v, layer_off + (uint64_t)e.page * page_stride), D, e.slot, c, x0, x1);
+    }
+}
+
+// Paged decode attention over a Q8 pool (attn_decode_split_q8,
+// kv8.metal:50-95, over pages): score_j = (q . k_j) * ks_j / sqrt(D) with
+// k_j the int8 values, out = sum_j p_j vs_j v_j / sum_j p_j.  One workgroup
+// of W waves per (item, layer, head), one query row per item; lane l reads
+// 16 int8 of key row l / LPK (LPK = D/16 lanes per key) and that key's
+// scale, as attn_split_kernel reads 8 halves.
+template <int D, int W, int PB, bool FUSED, int INL>
+__global__ __launch_bounds__(64 * W) void attn_q8_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+    constexpr int LPK = D / 16;
+    constexpr int KPL = 64 / LPK;
+    constexpr int LPP = kPage / KPL;
+    __shared__ float red[W][D + 2];
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t H = a.pool.n_head;
+    const uint32_t lh = a.n_lay * H;
+    const uint8_t* plan = plan_base(pa, a.plan);
+    if constexpr (FUSED) {
+        const uint32_t n_attn = a.n_items * lh;
+        if (blockIdx.x >= n_attn) {
+            const uint32_t base = (blockIdx.x - n_attn) * (64u * W);
+            append_chunk_q8(a.pool, a.k, a.v, a.kv_row_stride, a.kv_layer_stride,
+                            reinterpret_cast<const AppendEntry*>(plan + a.off_orphans), a.n_orphans, a.layer0,
+                            a.n_lay, base + threadIdx.x);
+            return;
+        }
+    }
+    const uint32_t item_i = blockIdx.x / lh;
+    const uint32_t rem = blockIdx.x - item_i * lh;
+    const uint32_t lay = rem / H;
+    const uint32_t head = rem - lay * H;
+    const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
+    const int kl = lane / LPK;
+    const int ds = lane % LPK;
+
+    const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.pool.k + layer_off);
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.pool.v + layer_off);
+    const uint64_t page_bytes = a.pool.page_halves * 2;
+    const uint32_t* __restrict__ tab = reinterpret_cast<const uint32_t*>(plan + a.off_table) + it.tab;
+    const uint32_t pg_begin = it.kv_begin / kPage;
+    const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
+    constexpr uint32_t STRIDE = W * PB;
+
+    if constexpr (FUSED) {
+        if (it.napp) {
+            item_append_q8<D>(a, plan, it, lay, head, layer_off, a.pool.page_halves, 64 * W);
+            __syncthreads();
+        }
+    }
+
+    struct Regs {
+        u32x4 k[PB][LPP], v[PB][LPP];
+        float ks[PB][LPP], vs[PB][LPP];
+    };
+    auto load = [&](uint32_t pg, Regs& r) {
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+            if (pg + b < pg_end) {
+                const uint64_t phys = tab[pg + b];
+                const uint8_t* kb = kbase + phys * page_bytes;
+                const uint8_t* vb = vbase + phys * page_bytes;
+#pragma unroll
+                for (int i = 0; i < LPP; i++) {
+                    r.k[b][i] = load16(reinterpret_cast<const u32x4*>(kb) + lane + i * 64);
+                    r.v[b][i] = load16(reinterpret_cast<const u32x4*>(vb) + lane + i * 64);
+                    r.ks[b][i] = reinterpret_cast<const float*>(kb + kPage * D)[i * KPL + kl];
+                    r.vs[b][i] = reinterpret_cast<const float*>(vb + kPage * D)[i * KPL + kl];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < LPP; i++) {
+                    r.k[b][i] = r.v[b][i] = u32x4{0, 0, 0, 0};
+                    r.ks[b][i] = r.vs[b][i] = 0.f;
+                }
+            }
+        }
+    };
+    Regs cur;
+    uint32_t pg = pg_begin + wave * PB;
+    if (pg < pg_end) load(pg, cur);
+
+    float q[16];
+    {
+        const float* qb = a.q + (int64_t)lay * a.q_layer_stride + (int64_t)it.row0 * a.q_row_stride + head * D + ds * 16;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float4 x = reinterpret_cast<const float4*>(qb)[c];
+            q[4 * c] = x.x * a.qscale;
+            q[4 * c + 1] = x.y * a.qscale;
+            q[4 * c + 2] = x.z * a.qscale;
+            q[4 * c + 3] = x.w * a.qscale;
+        }
+    }
+    float m = kMinScore, l = 0.f, o[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[e] = 0.f;
+
+    for (; pg < pg_end; pg += STRIDE) {
+        Regs nxt;
+        if (pg + STRIDE < pg_end) load(pg + STRIDE, nxt);
+        float s[PB][LPP];
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+#pragma unroll
+            for (int i = 0; i < LPP; i++) {
+                float acc = 0.f;
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc = fmaf(q[4 * w + j], i8f(cur.k[b][i][w], j), acc);
+                s[b][i] = key_sum<LPK>(acc) * cur.ks[b][i];
+                const uint32_t key = (pg + b) * kPage + i * KPL + kl;
+                if (key > it.pos0 || key >= it.kv_end) {
+                    s[b][i] = -INFINITY;
+                    cur.vs[b][i] = 0.f;
+                }
+            }
+        }
+        float mb = s[0][0];
+#pragma unroll
+        for (int b = 0; b < PB; b++)
+#pragma unroll
+            for (int i = 0; i < LPP; i++) mb = fmaxf(mb, s[b][i]);
+        const float mn = fmaxf(m, mb);
+        const float alpha = fast_exp2(m - mn);
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[e] *= alpha;
+#pragma unroll
+        for (int b = 0; b < PB; b++) {
+#pragma unroll
+            for (int i = 0; i < LPP; i++) {
+                const float p = fast_exp2(s[b][i] - mn);
+                l += p;
+                const float pv = p * cur.vs[b][i];
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) o[4 * w + j] = fmaf(pv, i8f(cur.v[b][i][w], j), o[4 * w + j]);
+            }
+        }
+        cur = nxt;
+    }
+
+    // Merge the KPL key-row groups of the wave (lanes ds, ds+LPK, ...).
+#pragma unroll
+    for (int off = LPK; off < 64; off <<= 1) {
+        const float m2 = __shfl_xor(m, off);
+        const float l2 = __shfl_xor(l, off);
+        float o2[16];
+#pragma unroll
+        for (int e = 0; e < 16; e++) o2[e] = __shfl_xor(o[e], off);
+        merge_state(m, l, o, m2, l2, o2);
+    }
+    if (kl == 0) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) red[wave][2 + ds * 16 + e] = o[e];
+        if (ds == 0) {
+            red[wave][0] = m;
+            red[wave][1] = l;
+        }
+    }
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < D; d += 64 * W) {
+        float M = red[0][0];
+#pragma unroll
+        for (int w = 1; w < W; w++) M = fmaxf(M, red[w][0]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            const float wt = fast_exp2(red[w][0] - M);
+            L += red[w][1] * wt;
+            O += red[w][2 + d] * wt;
+        }
+        if (it.part_slot == kNoSlot) {
+            a.out[(int64_t)lay * a.out_layer_stride + (int64_t)it.row0 * a.out_row_stride + head * D + d] = O / L;
+        } else {
+            float* p = a.partials + (((uint64_t)it.part_slot * a.n_lay + lay) * H + head) * (D + 2);
             if (d == 0) {
                 p[0] = M;
                 p[1] = L;
@@ -951,8 +1257,26 @@ hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
 }
 
 template <int D>
+hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
+    const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
+    if (blocks == 0) return hipSuccess;
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        // head_dim 128 takes two loads per page already; two pages would spill.
+        constexpr int PB = D == 128 ? 1 : kPagesPerIter;
+        if (a.napp_total || a.n_orphan_blocks)
+            return go(attn_q8_kernel<D, kWaves, PB, true, INL>, blocks, 64 * kWaves, s, t, a, pa);
+        return go(attn_q8_kernel<D, kWaves, PB, false, INL>, blocks, 64 * kWaves, s, t, a, pa);
+    });
+}
+
+template <int D>
 hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge,
                             const LaunchTiming& t) {
+    if (a.pool.q8) {  // single query rows only (the host plans no groups on a Q8 pool)
+        if (a.nq_tile != 1) return hipErrorInvalidValue;
+        return merge ? merge_launch_t<D, 1>(a, ip, ib, s, t) : q8_launch_t<D>(a, ip, ib, s, t);
+    }
 #define NI_NQ_CASE(N) \
     case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s, t) : attn_launch_t<D, N>(a, ip, ib, s, t);
 #if NI_ATTN_MFMA
@@ -1016,6 +1340,16 @@ hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream
         else
             hipExtLaunchKernelGGL(qkv_kernel<2, INL>, dim3(row_tiles, a.n_feat / 32), dim3(256), 0, s, t.start,
                                   t.stop, 0, a, pa);
+        return hipGetLastError();
+    });
+}
+
+hipError_t launch_gather_q8(const GatherQ8Launch& a, const void* ip, uint32_t ib, hipStream_t s) {
+    const uint64_t threads = (uint64_t)a.n_lay * a.n_rows * 2 * a.pool.n_head;
+    if (threads == 0) return hipSuccess;
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        hipLaunchKernelGGL(kv_gather_q8_kernel<INL>, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 0, s, a, pa);
         return hipGetLastError();
     });
 }

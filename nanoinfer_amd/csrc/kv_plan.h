@@ -66,6 +66,9 @@ struct PoolGeom {
     uint32_t head_halves;
     uint32_t n_head;
     uint32_t head_dim;
+    // Q8 blocks (kv8.metal:15-48): [16][head_dim] int8, then 16 f32 scales
+    // (amax / 127 per position) at byte 16 * head_dim.
+    uint32_t q8;
 };
 
 struct AppendLaunch {
@@ -115,6 +118,20 @@ struct QkvLaunch {
     uint32_t fused;
 };
 constexpr uint32_t kQkvTileRows = 32, kQkvTileFeat = 32, kQkvK = 16;  // d_in must be a multiple of kQkvK
+
+// Q8 gather: int8 K/V values [n_lay][n][C] and f32 scales [n_lay][n][n_head].
+struct GatherQ8Launch {
+    PoolGeom pool;
+    int8_t* k_out;
+    int8_t* v_out;
+    float* k_scale;
+    float* v_scale;
+    const uint8_t* plan;
+    uint32_t off_entries;  // src_row = output row
+    uint32_t n_rows;
+    uint32_t layer0;
+    uint32_t n_lay;
+};
 
 struct AttnLaunch {
     PoolGeom pool;
@@ -169,6 +186,7 @@ struct LaunchTiming {
 hipError_t launch_append(const AppendLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
                          const LaunchTiming& t = {});
 hipError_t launch_gather(const GatherLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
+hipError_t launch_gather_q8(const GatherQ8Launch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s);
 hipError_t launch_attention(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
                             const LaunchTiming& t = {});
 hipError_t launch_merge(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,

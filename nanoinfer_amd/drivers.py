@@ -194,6 +194,9 @@ def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, spli
     o._keep = []  # arrays the struct points into
     o.launch, o.steps, o.warmup, o.split_tokens, o.data_seed, o.profile_mask = launch, steps, warmup, split, seed, \
         profile_mask
+    q8 = name.endswith("q8")  # the same workload on a Q8 cache
+    if q8:
+        name = name[:-2]
     if name == "config3":
         o.workload = NI_DRIVE_SERVE
         o.serve = ni_serve_opts(seed, 1.0, 100000, 64, 32, 512, 16, 256, 256, 512, int(query_all_prompt_rows))
@@ -227,4 +230,6 @@ def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, spli
         _kv(o, workloads.GPT2, 64 * 64, 64, 1024, 512)
     else:
         raise ValueError(name)
+    if q8:
+        o.kv.flags |= _abi.NI_KV_Q8
     return o

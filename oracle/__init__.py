@@ -83,6 +83,13 @@ def lib():
                                      _sz, _sz, _f32p]
     L.or_split_attention_f64.argtypes = [_f64p, _f32p, _f32p, _f32p, _sz, _sz, _sz]
     L.or_matvec_f64.argtypes = [_f64p, _f32p, _sz, _f32p, C.c_void_p, _sz, _sz, _sz]
+    _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+    L.or_q8_quantize.restype = C.c_float
+    L.or_q8_quantize.argtypes = [_f32p, _sz, _i8p]
+    L.or_paged_q8_append.argtypes = [_i8p, _i8p, _f32p, _f32p, _u32p, C.c_uint32, _u32p, _u32p, _sz, _f32p, _f32p,
+                                     _sz, _sz, _sz]
+    L.or_paged_q8_attention.argtypes = [_f32p, _sz, _f32p, _sz, _i8p, _i8p, _f32p, _f32p, _u32p, C.c_uint32, _u32p,
+                                        _u32p, _sz, _sz, _sz, _f64p]
     L.or_alloc_new.restype = C.c_void_p
     L.or_alloc_new.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, C.c_void_p]
     L.or_alloc_free.argtypes = [C.c_void_p]
@@ -285,6 +292,63 @@ def paged_attention(pools: PagedPools, layer, table, max_blocks, seqs, poss, q, 
     lib().or_paged_attention(out, c, q.reshape(-1), q.shape[-1] if q.ndim > 1 else c, pools.k[layer],
                              pools.v[layer], np.ascontiguousarray(table, np.uint32).reshape(-1), max_blocks,
                              np.ascontiguousarray(seqs, np.uint32), np.ascontiguousarray(poss, np.uint32), n, n_head, hd, scores)
+    return out
+
+
+# ------------------------------------------------------------ Q8 cache (CPU)
+
+def q8_quantize(x):
+    """kv8.metal:15-48 for one (position, head): (int8 values, f32 scale)."""
+    x = _f32(x).reshape(-1)
+    q = np.zeros(x.size, np.int8)
+    scale = lib().or_q8_quantize(x, x.size, q)
+    return q, np.float32(scale)
+
+
+class PagedPoolsQ8:
+    """Q8 pools in the reference's row layout: values [n_layer][kv_blocks*16][C]
+    int8, scales [n_layer][kv_blocks*16][n_head] f32."""
+
+    def __init__(self, n_layer, kv_blocks, n_head, hd):
+        self.n_layer, self.kv_blocks, self.n_head, self.hd = n_layer, kv_blocks, n_head, hd
+        c = n_head * hd
+        self.kq = np.zeros((n_layer, kv_blocks * KV_BLOCK * c), np.int8)
+        self.vq = np.zeros_like(self.kq)
+        self.ks = np.zeros((n_layer, kv_blocks * KV_BLOCK * n_head), np.float32)
+        self.vs = np.zeros_like(self.ks)
+
+
+def paged_q8_append(pools: PagedPoolsQ8, layer, table, max_blocks, seqs, poss, k, v):
+    k, v = _f32(k), _f32(v)
+    n = len(seqs)
+    lib().or_paged_q8_append(pools.kq[layer], pools.vq[layer], pools.ks[layer], pools.vs[layer],
+                             np.ascontiguousarray(table, np.uint32).reshape(-1), max_blocks,
+                             np.ascontiguousarray(seqs, np.uint32), np.ascontiguousarray(poss, np.uint32), n,
+                             k.reshape(-1), v.reshape(-1), k.shape[-1], pools.n_head, pools.hd)
+
+
+def paged_q8_gather(pools: PagedPoolsQ8, layer, table, max_blocks, seqs, poss):
+    """(k, v) int8 [n][C] and (ks, vs) f32 [n][n_head] of (seq, pos) rows."""
+    c, h = pools.n_head * pools.hd, pools.n_head
+    slots = [kv_slot(table, s, p, max_blocks) for s, p in zip(seqs, poss)]
+    kq = pools.kq[layer].reshape(-1, c)[slots]
+    vq = pools.vq[layer].reshape(-1, c)[slots]
+    ks = pools.ks[layer].reshape(-1, h)[slots]
+    vs = pools.vs[layer].reshape(-1, h)[slots]
+    return (kq, vq), (ks, vs)
+
+
+def paged_q8_attention(pools: PagedPoolsQ8, layer, table, max_blocks, seqs, poss, q):
+    q = _f32(q)
+    n = len(seqs)
+    c = pools.n_head * pools.hd
+    out = np.zeros((n, c), np.float32)
+    scores = np.zeros(int(max(poss)) + 1 if n else 1, np.float64)
+    lib().or_paged_q8_attention(out, c, q.reshape(-1), q.shape[-1] if q.ndim > 1 else c, pools.kq[layer],
+                                pools.vq[layer], pools.ks[layer], pools.vs[layer],
+                                np.ascontiguousarray(table, np.uint32).reshape(-1), max_blocks,
+                                np.ascontiguousarray(seqs, np.uint32), np.ascontiguousarray(poss, np.uint32), n,
+                                pools.n_head, pools.hd, scores)
     return out
 
 

@@ -732,3 +732,83 @@ void or_matvec_f64(double* out, const float* x, size_t x_stride, const float* w,
             out[t * d_out + f] = s + (bias ? (double)bias[f] : 0.0);
         }
 }
+
+/* ------------------------------------------------------------------------- */
+/* Q8 KV cache (crates/metal/src/shaders/kv8.metal)                           */
+/* ------------------------------------------------------------------------- */
+
+/* kv_quant8, kv8.metal:15-48, for one (position, head) of n values:
+ * amax = max |x|, scale = amax / 127 (f32), inv = scale > 0 ? 1 / scale : 0,
+ * q = clamp(rint(x * inv), -127, 127) with rint rounding half to even.
+ * Returns the scale. */
+float or_q8_quantize(const float* x, size_t n, int8_t* q) {
+    float amax = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    volatile float scale = amax / 127.0f; /* volatile: keep both divisions in f32 */
+    volatile float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float y = nearbyintf(x[i] * inv);
+        if (y < -127.0f) y = -127.0f;
+        if (y > 127.0f) y = 127.0f;
+        q[i] = (int8_t)y;
+    }
+    return scale;
+}
+
+/* The paged Q8 cache in the reference's row layout: values [kv_blocks*16][C]
+ * int8 and scales [kv_blocks*16][n_head] f32 per layer (kv8.metal:11-12 with
+ * the position replaced by kv_slot, batch.metal:24-26).  Appends rows of
+ * f32 k/v at `stride`. */
+void or_paged_q8_append(int8_t* kq, int8_t* vq, float* ks, float* vs, const uint32_t* table, uint32_t max_blocks,
+                        const uint32_t* seqs, const uint32_t* poss, size_t n, const float* k, const float* v,
+                        size_t stride, size_t n_head, size_t hd) {
+    size_t c = n_head * hd;
+    for (size_t t = 0; t < n; t++) {
+        size_t slot = or_kv_slot(table, seqs[t], poss[t], max_blocks);
+        for (size_t h = 0; h < n_head; h++) {
+            ks[slot * n_head + h] = or_q8_quantize(k + t * stride + h * hd, hd, kq + slot * c + h * hd);
+            vs[slot * n_head + h] = or_q8_quantize(v + t * stride + h * hd, hd, vq + slot * c + h * hd);
+        }
+    }
+}
+
+/* attn_decode_split_q8 (kv8.metal:50-95) over pages, in double: for row
+ * (seq, pos) and head h, s_j = (sum_d q[d] k_j[d]) * ks_j / sqrt(hd) over
+ * keys j = 0..pos, p = softmax(s), out[d] = sum_j p_j vs_j v_j[d]. */
+void or_paged_q8_attention(float* out, size_t out_stride, const float* q, size_t q_stride, const int8_t* kq,
+                           const int8_t* vq, const float* ks, const float* vs, const uint32_t* table,
+                           uint32_t max_blocks, const uint32_t* seqs, const uint32_t* poss, size_t n, size_t n_head,
+                           size_t hd, double* scores) {
+    size_t c = n_head * hd;
+    double scale = 1.0 / sqrt((double)hd);
+    for (size_t t = 0; t < n; t++)
+        for (size_t h = 0; h < n_head; h++) {
+            size_t n_kv = (size_t)poss[t] + 1;
+            const float* qr = q + t * q_stride + h * hd;
+            double mx = -INFINITY;
+            for (size_t j = 0; j < n_kv; j++) {
+                size_t slot = or_kv_slot(table, seqs[t], (uint32_t)j, max_blocks);
+                double s = 0;
+                for (size_t d = 0; d < hd; d++) s += (double)qr[d] * (double)kq[slot * c + h * hd + d];
+                s *= (double)ks[slot * n_head + h] * scale;
+                scores[j] = s;
+                if (s > mx) mx = s;
+            }
+            double sum = 0;
+            for (size_t j = 0; j < n_kv; j++) {
+                scores[j] = exp(scores[j] - mx);
+                sum += scores[j];
+            }
+            for (size_t d = 0; d < hd; d++) {
+                double acc = 0;
+                for (size_t j = 0; j < n_kv; j++) {
+                    size_t slot = or_kv_slot(table, seqs[t], (uint32_t)j, max_blocks);
+                    acc += scores[j] * (double)vs[slot * n_head + h] * (double)vq[slot * c + h * hd + d];
+                }
+                out[t * out_stride + h * hd + d] = (float)(acc / sum);
+            }
+        }
+}

@@ -1,0 +1,165 @@
+"""The Q8 cache (NI_KV_Q8; kv8.metal:15-95) on the device against the
+oracle: appends bit-exact (int8 values and f32 scales, through
+ni_kv_gather_q8), attention within the north star's 1e-3 of the oracle's
+double-precision Q8 attention over the same stored bytes, fused steps,
+rollback, and the calls a Q8 cache refuses."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import nanoinfer_amd as na
+from nanoinfer_amd import workloads
+from paged_mirror import assert_close, step_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+class MirrorQ8:
+    def __init__(self, opts):
+        self.opts = opts
+        self.kv = na.PagedKv(opts)
+        self.c = opts.n_head * opts.head_dim
+        self.pools = oracle.PagedPoolsQ8(opts.n_layer, opts.kv_blocks, opts.n_head, opts.head_dim)
+
+    def table(self):
+        t = np.zeros((self.opts.max_seqs, self.kv.max_blocks), np.uint32)
+        for s in range(self.opts.max_seqs):
+            bt = self.kv.block_table(s)
+            t[s, :len(bt)] = bt
+        return t
+
+    def append_oracle(self, rows, k, v):
+        rows = np.asarray(rows, np.uint32).reshape(-1, 2)
+        t = self.table()
+        for l in range(self.opts.n_layer):
+            oracle.paged_q8_append(self.pools, l, t, self.kv.max_blocks, rows[:, 0], rows[:, 1], k[l], v[l])
+
+    def fill(self, seq, length, rng, chunk=256):
+        start = self.kv.seq_len(seq)
+        self.kv.reserve(seq, length)
+        for p0 in range(start, length, chunk):
+            p1 = min(length, p0 + chunk)
+            rows = [(seq, p) for p in range(p0, p1)]
+            shape = (self.opts.n_layer, p1 - p0, self.c)
+            k = rng.standard_normal(shape, dtype=np.float32)
+            v = rng.standard_normal(shape, dtype=np.float32)
+            self.kv.append(rows, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+            self.append_oracle(rows, k, v)
+        self.kv.commit(seq, length - start)
+
+    def attention_oracle(self, rows, q):
+        rows = np.asarray(rows, np.uint32).reshape(-1, 2)
+        t = self.table()
+        return np.stack([oracle.paged_q8_attention(self.pools, l, t, self.kv.max_blocks, rows[:, 0], rows[:, 1], q[l])
+                         for l in range(self.opts.n_layer)])
+
+    def check_bytes(self, rows):
+        rows = np.asarray(rows, np.uint32).reshape(-1, 2)
+        t = self.table()
+        (kq, vq), (ks, vs) = self.kv.gather_q8(rows)
+        kq, vq, ks, vs = (x.cpu().numpy() for x in (kq, vq, ks, vs))
+        for l in range(self.opts.n_layer):
+            (wk, wv), (wks, wvs) = oracle.paged_q8_gather(self.pools, l, t, self.kv.max_blocks, rows[:, 0], rows[:, 1])
+            assert np.array_equal(kq[l], wk) and np.array_equal(vq[l], wv), f"layer {l}: int8 values"
+            assert np.array_equal(ks[l].view(np.uint32), wks.view(np.uint32)), f"layer {l}: k scales"
+            assert np.array_equal(vs[l].view(np.uint32), wvs.view(np.uint32)), f"layer {l}: v scales"
+
+
+def opts(shape, **kw):
+    base = dict(**shape, kv_blocks=256, max_seqs=8, n_ctx=2048, max_rows=512, q8=True)
+    base.update(kw)
+    return na.BatchOpts(**base)
+
+
+@pytest.mark.parametrize("shape", [workloads.GPT2, dict(n_layer=2, n_head=4, head_dim=128)], ids=["hd64", "hd128"])
+def test_q8_append_bit_exact(gpu, oracle_lib, shape):
+    rng = np.random.default_rng(90)
+    m = MirrorQ8(opts(shape))
+    s = m.kv.add_seq()
+    L = 77
+    m.kv.reserve(s, L)
+    rows = [(s, p) for p in range(L)]
+    shape3 = (shape["n_layer"], L, m.c)
+    k = (rng.standard_normal(shape3) * rng.choice([1e-4, 1.0, 1e3], size=(1, L, 1))).astype(np.float32)
+    v = rng.standard_normal(shape3).astype(np.float32)
+    d = shape["head_dim"]
+    k[:, 3, :d] = 0.0                  # an all-zero (position, head): scale 0, values 0
+    k[:, 4, :d] = 0.0
+    k[:, 4, 5] = -7.25                 # one spike: it alone sets amax
+    v[:, 5, :] = np.float32(2.5) * np.sign(v[:, 5, :])  # ties of rint at amax/127 steps
+    m.kv.append(rows, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    m.append_oracle(rows, k, v)
+    torch.cuda.synchronize()
+    m.check_bytes(rows)
+
+
+@pytest.mark.parametrize("shape", [workloads.GPT2, dict(n_layer=2, n_head=4, head_dim=128)], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("split", [0, 64, 512])
+def test_q8_decode_contexts(gpu, oracle_lib, shape, split):
+    rng = np.random.default_rng(91)
+    m = MirrorQ8(opts(shape, page_order=rng.permutation(256).tolist()))
+    lens = [1, 15, 16, 17, 300, 1023]
+    seqs = [m.kv.add_seq() for _ in lens]
+    for s, L in zip(seqs, lens):
+        m.fill(s, L, rng)
+    rows = [(s, L - 1) for s, L in zip(seqs, lens)]
+    q = rng.standard_normal((shape["n_layer"], len(rows), m.c)).astype(np.float32)
+    got = m.kv.attention(torch.from_numpy(q).cuda(), rows, split_tokens=split).cpu().numpy()
+    want = m.attention_oracle(rows, q)
+    err = assert_close(got, want, f"q8 split {split}")
+    say(f"q8 {shape} split {split}: max abs err {err:.2e}")
+
+
+def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib):
+    """ni_kv_step on a Q8 cache: decode rows, a prompt chunk queried at its
+    last row, a 5-row verify group (attended row by row) and a mid-prompt
+    chunk (no query); then truncate, free and reuse pages."""
+    rng = np.random.default_rng(92)
+    m = MirrorQ8(opts(workloads.GPT2, n_layer=3))
+    a, b, c, d = (m.kv.add_seq() for _ in range(4))
+    for s, L in zip((a, b, c), (100, 40, 333)):
+        m.fill(s, L, rng)
+    for rnd in range(3):
+        work = [(a, 1, 1), (b, 5, 5), (c, 1, 1), (d, 37, 1 if rnd else 0)]
+        rows, qrows = step_rows(m.kv, work)
+        n = len(rows)
+        q, k, v = (rng.standard_normal((3, n, m.c)).astype(np.float32) for _ in range(3))
+        got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v))).cpu().numpy()
+        # the oracle appends with the tables the step reserved
+        m.append_oracle(rows, k, v)
+        want = m.attention_oracle(rows[qrows], q[:, qrows])
+        assert_close(got[:, qrows], want, f"round {rnd}")
+        m.check_bytes(rows)
+        # verify rollback: keep 2 of b's 5 rows
+        m.kv.truncate(b, m.kv.seq_len(b) - 3)
+    m.kv.free_seq(c)
+    e = m.kv.add_seq()
+    m.fill(e, 50, rng)  # reuses c's pages
+    rows = [(e, 49), (a, m.kv.seq_len(a) - 1)]
+    q = rng.standard_normal((3, 2, m.c)).astype(np.float32)
+    got = m.kv.attention(torch.from_numpy(q).cuda(), rows).cpu().numpy()
+    assert_close(got, m.attention_oracle(rows, q), "after reuse")
+
+
+def test_q8_refusals(gpu):
+    kv = na.PagedKv(na.BatchOpts(n_layer=1, n_head=2, head_dim=64, kv_blocks=8, max_seqs=2, n_ctx=64, q8=True))
+    s = kv.add_seq()
+    kv.reserve(s, 4)
+    with pytest.raises(na.KvError, match="ni_kv_gather_q8"):
+        kv.gather([(s, 0)])
+    w = torch.zeros((384, 64), device="cuda")
+    with pytest.raises(na.KvError, match="Q8 cache"):
+        kv.qkv_append([(s, 0)], torch.zeros((1, 64), device="cuda"), w)
+    f16 = na.PagedKv(na.BatchOpts(n_layer=1, n_head=2, head_dim=64, kv_blocks=8, max_seqs=2, n_ctx=64))
+    t = f16.add_seq()
+    f16.reserve(t, 4)
+    with pytest.raises(na.KvError, match="not a Q8 cache"):
+        f16.gather_q8([(t, 0)])
+    assert kv.kv_block_bytes() * 2 < f16.kv_block_bytes() * 1.1
