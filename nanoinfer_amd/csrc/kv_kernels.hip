@@ -774,90 +774,119 @@ __global__ __launch_bounds__(64 * W) void attn_q8_kernel(const AttnLaunch a, con
 // (matvec_batch<..., BEPI_QKV>, batch.metal:94-165): q to `out`, k/v as f16
 // straight into the rows' page slots, so f32 K/V never travel through HBM.
 //
-// A workgroup computes a 32-row x 16- or 32-feature tile; its 4 waves take
-// every 4th 16-wide slice of d_in and add their partial tiles in LDS in wave
-// order, so the result does not depend on scheduling.  In a slice, lane l
-// loads 4 consecutive x values of row l%16 and 4 of W's feature l%16 at
-// offset 4*(l/16); product c of the slice uses component c of both, so
-// lane group g supplies k = 4g + c to A and B alike.
-// FB feature blocks of 16 per tile (the tile is 32 rows x 16*FB features).
-// 4 waves take every 4th 16-wide slice of d_in.
+// In a 16-wide slice of d_in, lane l holds 4 consecutive x values of row
+// l%16 and 4 of W's feature l%16 at offset 4*(l/16); product c of the slice
+// uses component c of both, so lane group g supplies k = 4g + c to A and B
+// alike.
+//
+// The tile is 32 rows x 16*FB features.  x and W arrive through LDS in
+// chunks of kQkvChunk values of d_in, each row segment loaded contiguously
+// (a wave-wide load covers 1 KB of one or two rows); the next chunk is in
+// registers while the current one is multiplied.  Wave w owns row block
+// w & 1 and half (w >> 1) of every chunk; the two halves are added in a
+// fixed order, so the result does not depend on scheduling.
+constexpr int kQkvChunk = 128;
+constexpr int kQkvPad = kQkvChunk + 4;  // LDS row stride (floats): conflict-free 16-byte reads
+
 template <int FB, int INL>
 __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
     typedef float f4 __attribute__((ext_vector_type(4)));
-    constexpr int NW = 4;
-    __shared__ float red[NW][2][FB][4][64];  // [wave][row block][feature block][element][lane]
+    constexpr int TM = kQkvTileRows, TF = 16 * FB, KC = kQkvChunk, KP = kQkvPad;
+    constexpr int XV = TM * KC / 4 / 256, WV = TF * KC / 4 / 256;  // float4 per thread per chunk
+    __shared__ __attribute__((aligned(16))) float xs[TM][KP];
+    __shared__ __attribute__((aligned(16))) float ws[TF][KP];
+    __shared__ float red[2][FB][4][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const uint32_t m0 = blockIdx.x * kQkvTileRows, n0 = blockIdx.y * (16 * FB);
+    const int rb = wave & 1, kh = wave >> 1;
+    const uint32_t m0 = blockIdx.x * TM, n0 = blockIdx.y * TF;
     const int i = lane & 15, g = lane >> 4;
-    // Rows past n_rows read the last row (their results are not stored).
-    const float* xr[2];
-    const float* wr[FB];
+
+    // Staging: float4 u = threadIdx.x + 256 * j of a chunk is row u / (KC/4),
+    // column 4 * (u % (KC/4)).  Rows past n_rows repeat the last row; values
+    // past d_in (the last, partial chunk) are zeros.
+    float4 xr[XV], wr[WV];
+    auto fetch = [&](uint32_t k0) {
 #pragma unroll
-    for (int b = 0; b < 2; b++) {
-        const uint32_t row = min(m0 + 16 * b + i, a.n_rows - 1);
-        xr[b] = a.x + (int64_t)row * a.x_row_stride + 4 * g;
-    }
+        for (int j = 0; j < XV; j++) {
+            const uint32_t u = threadIdx.x + 256 * j, row = u / (KC / 4), col = 4 * (u % (KC / 4));
+            const uint32_t r = min(m0 + row, a.n_rows - 1);
+            xr[j] = k0 + col < a.d_in ? *reinterpret_cast<const float4*>(a.x + (int64_t)r * a.x_row_stride + k0 + col)
+                                      : float4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
-    for (int b = 0; b < FB; b++) wr[b] = a.w + (uint64_t)(n0 + 16 * b + i) * a.d_in + 4 * g;
-    f4 acc[2][FB];
+        for (int j = 0; j < WV; j++) {
+            const uint32_t u = threadIdx.x + 256 * j, row = u / (KC / 4), col = 4 * (u % (KC / 4));
+            wr[j] = k0 + col < a.d_in ? *reinterpret_cast<const float4*>(a.w + (uint64_t)(n0 + row) * a.d_in + k0 + col)
+                                      : float4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    f4 acc[FB];
 #pragma unroll
-    for (int tb = 0; tb < 2; tb++)
+    for (int fb = 0; fb < FB; fb++) acc[fb] = f4{0.f, 0.f, 0.f, 0.f};
+    fetch(0);
+    for (uint32_t k0 = 0; k0 < a.d_in; k0 += KC) {
+        __syncthreads();  // the previous chunk's products are done with LDS
 #pragma unroll
-        for (int fb = 0; fb < FB; fb++) acc[tb][fb] = f4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t k0 = wave * kQkvK; k0 < a.d_in; k0 += NW * kQkvK) {
-        float4 xv[2], wv[FB];
+        for (int j = 0; j < XV; j++) {
+            const uint32_t u = threadIdx.x + 256 * j;
+            *reinterpret_cast<float4*>(&xs[u / (KC / 4)][4 * (u % (KC / 4))]) = xr[j];
+        }
 #pragma unroll
-        for (int b = 0; b < 2; b++) xv[b] = *reinterpret_cast<const float4*>(xr[b] + k0);
+        for (int j = 0; j < WV; j++) {
+            const uint32_t u = threadIdx.x + 256 * j;
+            *reinterpret_cast<float4*>(&ws[u / (KC / 4)][4 * (u % (KC / 4))]) = wr[j];
+        }
+        __syncthreads();
+        if (k0 + KC < a.d_in) fetch(k0 + KC);
+        // This wave's half of the chunk: slices of 16; lane (i, g) holds k =
+        // 4g .. 4g+3 of the slice for row 16rb + i and for feature 16fb + i.
 #pragma unroll
-        for (int b = 0; b < FB; b++) wv[b] = *reinterpret_cast<const float4*>(wr[b] + k0);
-#pragma unroll
-        for (int tb = 0; tb < 2; tb++)
+        for (int sl = 0; sl < KC / 32; sl++) {
+            const int kk = (kh * (KC / 32) + sl) * 16 + 4 * g;
+            const float4 xv = *reinterpret_cast<const float4*>(&xs[16 * rb + i][kk]);
 #pragma unroll
             for (int fb = 0; fb < FB; fb++) {
-                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].x, wv[fb].x, acc[tb][fb], 0, 0, 0);
-                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].y, wv[fb].y, acc[tb][fb], 0, 0, 0);
-                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].z, wv[fb].z, acc[tb][fb], 0, 0, 0);
-                acc[tb][fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[tb].w, wv[fb].w, acc[tb][fb], 0, 0, 0);
+                const float4 wv = *reinterpret_cast<const float4*>(&ws[16 * fb + i][kk]);
+                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, wv.x, acc[fb], 0, 0, 0);
+                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, wv.y, acc[fb], 0, 0, 0);
+                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, wv.z, acc[fb], 0, 0, 0);
+                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, wv.w, acc[fb], 0, 0, 0);
             }
+        }
     }
-#pragma unroll
-    for (int tb = 0; tb < 2; tb++)
+    if (kh == 1) {
 #pragma unroll
         for (int fb = 0; fb < FB; fb++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) red[wave][tb][fb][e][lane] = acc[tb][fb][e];
+            for (int e = 0; e < 4; e++) red[rb][fb][e][lane] = acc[fb][e];
+    }
     __syncthreads();
-    // Thread t: feature n0 + t%(16FB) of rows t/(16FB), + RSTEP, ...  Output
-    // (row r, feature f) sits at lane f%16 + 16*((r%16)/4), element r%4 of
-    // block (r/16, f/16); the waves' partials are added in wave order.
-    constexpr uint32_t TF = 16 * FB, RSTEP = 64 * NW / TF;
-    const uint32_t fcol = threadIdx.x % TF, r0 = threadIdx.x / TF;
-    const uint32_t f = n0 + fcol;
-    const float b = a.bias ? a.bias[f] : 0.f;
+    if (kh == 1) return;
+    // Output (row 16rb + 4g + e, feature 16fb + i) is element e of lane
+    // i + 16g's block fb (the matrix-core output layout).
     const uint32_t C = a.n_feat / 3, D = a.pool.head_dim;
     const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
 #pragma unroll
-    for (uint32_t r = r0; r < kQkvTileRows; r += RSTEP) {
-        const uint32_t row = m0 + r;
-        if (row >= a.n_rows) break;
-        const int tb = r >> 4, ri = r & 15, fb = fcol >> 4;
-        const int src_lane = (fcol & 15) + 16 * (ri >> 2), el = ri & 3;
-        float y = red[0][tb][fb][el][src_lane];
+    for (int fb = 0; fb < FB; fb++) {
+        const uint32_t f = n0 + 16 * fb + i;
+        const float b = a.bias ? a.bias[f] : 0.f;
 #pragma unroll
-        for (int w = 1; w < NW; w++) y += red[w][tb][fb][el][src_lane];
-        y += b;
-        if (!a.fused || f < C) {
-            a.out[(int64_t)row * a.out_row_stride + f] = y;
-        } else {
-            const AppendEntry en = entries[row];
-            const uint32_t is_v = f >= 2 * C;
-            const uint32_t c = f - C - is_v * C, head = c / D, d = c - head * D;
-            uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)a.layer * a.pool.layer_halves +
-                            (uint64_t)en.page * a.pool.page_halves + (uint64_t)head * a.pool.head_halves +
-                            en.slot * D + d;
-            *dst = (uint16_t)f16_bits(y);
+        for (int e = 0; e < 4; e++) {
+            const uint32_t row = m0 + 16 * rb + 4 * g + e;
+            if (row >= a.n_rows) break;
+            const float y = acc[fb][e] + red[rb][fb][e][lane] + b;
+            if (!a.fused || f < C) {
+                a.out[(int64_t)row * a.out_row_stride + f] = y;
+            } else {
+                const AppendEntry en = entries[row];
+                const uint32_t is_v = f >= 2 * C;
+                const uint32_t c = f - C - is_v * C, head = c / D, d = c - head * D;
+                uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)a.layer * a.pool.layer_halves +
+                                (uint64_t)en.page * a.pool.page_halves + (uint64_t)head * a.pool.head_halves +
+                                en.slot * D + d;
+                *dst = (uint16_t)f16_bits(y);
+            }
         }
     }
 }
@@ -1319,27 +1348,14 @@ hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hip
     });
 }
 
-#ifndef NI_QKV_NARROW_ROWS
-#define NI_QKV_NARROW_ROWS 64
-#endif
-// The kernel is limited by the scattered W rows each load instruction
-// touches (16 rows, 64 B each, 3 KB apart at d_in 768), not by how many
-// slices a wave keeps in flight: 8 or 16 waves per tile with 4 slices
-// loaded ahead measured slower (0.145 vs 0.131 ms for 12 layers of 64 rows).
-
 hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     if (a.n_rows == 0) return hipSuccess;
-    const uint32_t row_tiles = (a.n_rows + kQkvTileRows - 1) / kQkvTileRows;
-    // Few rows: 16-feature tiles, twice the workgroups to stream W with.
-    const bool narrow = a.n_rows <= NI_QKV_NARROW_ROWS;
+    // 16-feature tiles at every row count: the most workgroups to stream W
+    // with (64-feature tiles measured slower from 64 to 512 rows).
+    const dim3 grid((a.n_rows + kQkvTileRows - 1) / kQkvTileRows, a.n_feat / kQkvTileFeat);
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-        if (narrow)
-            hipExtLaunchKernelGGL(qkv_kernel<1, INL>, dim3(row_tiles, a.n_feat / 16), dim3(256), 0, s, t.start,
-                                  t.stop, 0, a, pa);
-        else
-            hipExtLaunchKernelGGL(qkv_kernel<2, INL>, dim3(row_tiles, a.n_feat / 32), dim3(256), 0, s, t.start,
-                                  t.stop, 0, a, pa);
+        hipExtLaunchKernelGGL(qkv_kernel<kQkvTileFeat / 16, INL>, grid, dim3(256), 0, s, t.start, t.stop, 0, a, pa);
         return hipGetLastError();
     });
 }

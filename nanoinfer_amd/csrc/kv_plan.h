@@ -117,7 +117,7 @@ struct QkvLaunch {
     uint32_t layer;
     uint32_t fused;
 };
-constexpr uint32_t kQkvTileRows = 32, kQkvTileFeat = 32, kQkvK = 16;  // d_in must be a multiple of kQkvK
+constexpr uint32_t kQkvTileRows = 32, kQkvTileFeat = 16, kQkvK = 16;  // d_in must be a multiple of kQkvK
 
 // Q8 gather: int8 K/V values [n_lay][n][C] and f32 scales [n_lay][n][n_head].
 struct GatherQ8Launch {
