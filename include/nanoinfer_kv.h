@@ -64,8 +64,7 @@ enum ni_status {
  * each (position, head) of K and V is stored as head_dim int8 values and one
  * f32 scale = amax / 127 (68 bytes per 64 values instead of 128).  Appends
  * quantise (kv_quant8, :15-48; inputs must be finite), attention dequantises
- * (attn_decode_split_q8, :50-95); query rows are attended one by one (no
- * shared K/V reads for groups); ni_kv_gather and ni_kv_qkv_append are
+ * (attn_decode_split_q8, :50-95); ni_kv_gather and ni_kv_qkv_append are
  * refused (ni_kv_gather_q8 returns the stored bytes). */
 #define NI_KV_Q8 2u
 

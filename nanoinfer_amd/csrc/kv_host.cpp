@@ -203,9 +203,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 bool is_q8(const ni_kv_opts& o) { return (o.flags & NI_KV_Q8) != 0; }
 
-// Rows of one sequence that share one pass over the keys: the matrix-core
-// tile for f16 pools; Q8 pools attend rows one by one.
-uint32_t max_group_rows(const ni_kv* kv) { return is_q8(kv->o) ? 1u : kMaxGroupRows; }
+// Rows of one sequence that share one pass over the keys (the matrix-core
+// tile, f16 and Q8 pools alike).
+uint32_t max_group_rows(const ni_kv*) { return kMaxGroupRows; }
 
 // Halves of one K (or V) block of a (page, head).
 uint64_t kv_block_halves(const ni_kv_opts& o) {

@@ -925,12 +925,16 @@ constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
 #ifndef NI_MFMA_MIN_WAVES
 #define NI_MFMA_MIN_WAVES 4
 #endif
-template <int D, int W, int PB, bool FUSED, int INL>
+// Q8: the pool holds int8 values with a scale per (position, head); K
+// values enter the products as f16 (int8 converts exactly), the key scale
+// multiplies the scores and the value scale multiplies p before its split.
+template <int D, int W, int PB, bool FUSED, int INL, bool Q8>
 __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_mfma_kernel(const AttnLaunch a,
                                                                                             const PlanArg<INL> pa) {
     constexpr int QC = D / 32;      // 32-dim chunks of the QK product
     constexpr int VC = D / 16;      // 16-dim chunks of the PV product
-    constexpr int LPK = D / 8;      // lanes per key row in a coalesced V load
+    constexpr int VE = Q8 ? 16 : 8; // V values per 16-byte lane load
+    constexpr int LPK = D / VE;     // lanes per key row in a coalesced V load
     constexpr int KPL = 64 / LPK;   // key rows per V load
     constexpr int LPP = kPage / KPL;
     constexpr int VROW = D + 8;     // LDS halves per V row (pad: conflict-free column reads)
@@ -947,9 +951,13 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         const uint32_t n_attn = a.n_items * lh;
         if (blockIdx.x >= n_attn) {
             const uint32_t base = (blockIdx.x - n_attn) * (64u * W);
-            append_chunk(a.pool, a.k, a.v, a.kv_row_stride, a.kv_layer_stride,
-                         reinterpret_cast<const AppendEntry*>(plan + a.off_orphans), a.n_orphans, a.layer0,
-                         a.n_lay, base + threadIdx.x);
+            const AppendEntry* orphans = reinterpret_cast<const AppendEntry*>(plan + a.off_orphans);
+            if constexpr (Q8)
+                append_chunk_q8(a.pool, a.k, a.v, a.kv_row_stride, a.kv_layer_stride, orphans, a.n_orphans, a.layer0,
+                                a.n_lay, base + threadIdx.x);
+            else
+                append_chunk(a.pool, a.k, a.v, a.kv_row_stride, a.kv_layer_stride, orphans, a.n_orphans, a.layer0,
+                             a.n_lay, base + threadIdx.x);
             return;
         }
     }
@@ -972,7 +980,10 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
 
     if constexpr (FUSED) {
         if (it.napp) {
-            item_append<D>(a, plan, it, lay, head, layer_off, page_stride, 64 * W);
+            if constexpr (Q8)
+                item_append_q8<D>(a, plan, it, lay, head, layer_off, page_stride, 64 * W);
+            else
+                item_append<D>(a, plan, it, lay, head, layer_off, page_stride, 64 * W);
             __syncthreads();
         }
     }
@@ -980,21 +991,38 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     // Page registers: K as the A operand (key col, dims c*32 + 8*rg ..), V
     // as coalesced rows (key i*KPL + lane/LPK, dims (lane%LPK)*8 ..).  Pages
     // past pg_end are not loaded (their keys are masked).
+    // Q8: K as 8 int8 per (key, chunk), the scales of keys 4*rg .. 4*rg+3
+    // (the rows of S^T and P^T this lane holds).
     struct Regs {
-        u32x4 k[PB][QC];
+        u32x4 k[PB][QC];  // Q8: .x, .y hold 8 int8
         u32x4 v[PB][LPP];
+        float4 ks[Q8 ? PB : 1], vs[Q8 ? PB : 1];
     };
     auto load = [&](uint32_t pg, Regs& r) {
 #pragma unroll
         for (int b = 0; b < PB; b++) {
             if (pg + b >= pg_end) continue;
             const uint64_t phys = tab[pg + b];
-            const uint16_t* kp = kbase + phys * page_stride + col * D + 8 * rg;
+            if constexpr (Q8) {
+                const uint8_t* kb = reinterpret_cast<const uint8_t*>(kbase + phys * page_stride);
+                const uint8_t* vb = reinterpret_cast<const uint8_t*>(vbase + phys * page_stride);
 #pragma unroll
-            for (int c = 0; c < QC; c++) r.k[b][c] = load16(reinterpret_cast<const u32x4*>(kp + c * 32));
-            const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
+                for (int c = 0; c < QC; c++) {
+                    const uint2 w = *reinterpret_cast<const uint2*>(kb + col * D + c * 32 + 8 * rg);
+                    r.k[b][c] = u32x4{w.x, w.y, 0u, 0u};
+                }
 #pragma unroll
-            for (int i = 0; i < LPP; i++) r.v[b][i] = load16(vp + i * 64);
+                for (int i = 0; i < LPP; i++) r.v[b][i] = load16(reinterpret_cast<const u32x4*>(vb) + lane + i * 64);
+                r.ks[b] = *reinterpret_cast<const float4*>(kb + kPage * D + 16 * rg);
+                r.vs[b] = *reinterpret_cast<const float4*>(vb + kPage * D + 16 * rg);
+            } else {
+                const uint16_t* kp = kbase + phys * page_stride + col * D + 8 * rg;
+#pragma unroll
+                for (int c = 0; c < QC; c++) r.k[b][c] = load16(reinterpret_cast<const u32x4*>(kp + c * 32));
+                const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
+#pragma unroll
+                for (int i = 0; i < LPP; i++) r.v[b][i] = load16(vp + i * 64);
+            }
         }
     };
     Regs cur;
@@ -1044,7 +1072,21 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
             for (int i = 0; i < LPP; i++) {
                 const uint32_t key = i * KPL + lane / LPK;
                 const u32x4 val = (pg + b) * kPage + key < it.kv_end ? cur.v[b][i] : u32x4{0, 0, 0, 0};
-                *reinterpret_cast<u32x4*>(my_vt + (b * kPage + key) * VROW + (lane % LPK) * 8) = val;
+                _Float16* dst = my_vt + (b * kPage + key) * VROW + (lane % LPK) * VE;
+                if constexpr (Q8) {
+                    half8_t h0, h1;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        h0[j] = static_cast<_Float16>(i8f(val[0], j));
+                        h0[4 + j] = static_cast<_Float16>(i8f(val[1], j));
+                        h1[j] = static_cast<_Float16>(i8f(val[2], j));
+                        h1[4 + j] = static_cast<_Float16>(i8f(val[3], j));
+                    }
+                    reinterpret_cast<half8_t*>(dst)[0] = h0;
+                    reinterpret_cast<half8_t*>(dst)[1] = h1;
+                } else {
+                    *reinterpret_cast<u32x4*>(dst) = val;
+                }
             }
         }
         // S^T = K Q^T per page; scores of keys 4*rg+j of each page.
@@ -1055,7 +1097,16 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
             float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < QC; c++) {
-                const half8_t kh = __builtin_bit_cast(half8_t, cur.k[b][c]);
+                half8_t kh;
+                if constexpr (Q8) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        kh[j] = static_cast<_Float16>(i8f(cur.k[b][c][0], j));
+                        kh[4 + j] = static_cast<_Float16>(i8f(cur.k[b][c][1], j));
+                    }
+                } else {
+                    kh = __builtin_bit_cast(half8_t, cur.k[b][c]);
+                }
                 st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
                 sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
             }
@@ -1063,7 +1114,9 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
             for (int j = 0; j < 4; j++) {
                 const uint32_t kp = (pg + b) * kPage + 4 * rg + j;
                 const bool ok = qok && kp < it.kv_end && kp <= qpos;
-                s[b][j] = ok ? st[j] + sl[j] * kLoUnscale : -INFINITY;
+                float sv = st[j] + sl[j] * kLoUnscale;
+                if constexpr (Q8) sv *= cur.ks[b][j];
+                s[b][j] = ok ? sv : -INFINITY;
                 mx = fmaxf(mx, s[b][j]);
             }
         }
@@ -1081,7 +1134,10 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 const float p = fast_exp2(s[b][j] - mn);
                 ps += p;
                 _Float16 h, l;
-                split_f16(p * kPScale, h, l);
+                if constexpr (Q8)
+                    split_f16(p * cur.vs[b][j] * kPScale, h, l);
+                else
+                    split_f16(p * kPScale, h, l);
                 ph[b][j] = h;
                 pl[b][j] = l;
             }
@@ -1273,15 +1329,15 @@ hipError_t merge_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipS
     });
 }
 
-template <int D>
+template <int D, bool Q8>
 hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         if (a.napp_total || a.n_orphan_blocks)
-            return go(attn_mfma_kernel<D, kWaves, kMfmaPages, true, INL>, blocks, 64 * kWaves, s, t, a, pa);
-        return go(attn_mfma_kernel<D, kWaves, kMfmaPages, false, INL>, blocks, 64 * kWaves, s, t, a, pa);
+            return go(attn_mfma_kernel<D, kWaves, kMfmaPages, true, INL, Q8>, blocks, 64 * kWaves, s, t, a, pa);
+        return go(attn_mfma_kernel<D, kWaves, kMfmaPages, false, INL, Q8>, blocks, 64 * kWaves, s, t, a, pa);
     });
 }
 
@@ -1302,7 +1358,9 @@ hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStre
 template <int D>
 hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge,
                             const LaunchTiming& t) {
-    if (a.pool.q8) {  // single query rows only (the host plans no groups on a Q8 pool)
+    if (a.pool.q8) {  // single rows on the vector kernel, groups on the matrix cores
+        if (a.nq_tile == kMfmaTile)
+            return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s, t) : mfma_launch_t<D, true>(a, ip, ib, s, t);
         if (a.nq_tile != 1) return hipErrorInvalidValue;
         return merge ? merge_launch_t<D, 1>(a, ip, ib, s, t) : q8_launch_t<D>(a, ip, ib, s, t);
     }
@@ -1311,7 +1369,7 @@ hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hi
 #if NI_ATTN_MFMA
     // Groups of several rows always take the 16-row matrix tile.
     if (a.nq_tile == kMfmaTile)
-        return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s, t) : mfma_launch_t<D>(a, ip, ib, s, t);
+        return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s, t) : mfma_launch_t<D, false>(a, ip, ib, s, t);
     switch (a.nq_tile) {
         NI_NQ_CASE(1)
         default: return hipErrorInvalidValue;

@@ -117,10 +117,28 @@ def test_q8_decode_contexts(gpu, oracle_lib, shape, split):
     say(f"q8 {shape} split {split}: max abs err {err:.2e}")
 
 
+@pytest.mark.parametrize("nq", [2, 5, 16, 20])
+def test_q8_causal_groups(gpu, oracle_lib, nq):
+    """Consecutive rows of one sequence share their K/V reads on the matrix
+    cores (int8 converted to f16 exactly, scales applied to scores and p);
+    groups over 16 rows split in two."""
+    rng = np.random.default_rng(93 + nq)
+    m = MirrorQ8(opts(workloads.GPT2, n_layer=2))
+    for split in (0, 64):
+        for L in sorted({nq, nq + 1, 17 + nq, 130, 700}):
+            s = m.kv.add_seq()
+            m.fill(s, L, rng)
+            rows = [(s, p) for p in range(L - nq, L)]
+            q = rng.standard_normal((2, nq, m.c)).astype(np.float32)
+            got = m.kv.attention(torch.from_numpy(q).cuda(), rows, split_tokens=split).cpu().numpy()
+            assert_close(got, m.attention_oracle(rows, q), f"q8 nq {nq} L {L} split {split}")
+            m.kv.free_seq(s)
+
+
 def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib):
     """ni_kv_step on a Q8 cache: decode rows, a prompt chunk queried at its
-    last row, a 5-row verify group (attended row by row) and a mid-prompt
-    chunk (no query); then truncate, free and reuse pages."""
+    last row, a 5-row verify group and a mid-prompt chunk (no query), all in
+    one fused launch; then truncate, free and reuse pages."""
     rng = np.random.default_rng(92)
     m = MirrorQ8(opts(workloads.GPT2, n_layer=3))
     a, b, c, d = (m.kv.add_seq() for _ in range(4))
