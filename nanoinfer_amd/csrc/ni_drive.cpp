@@ -4,7 +4,7 @@
 // one JSON line.
 //
 //   ni_drive [serve|spec|qkv] [--per-layer] [--steps K] [--warmup W] [--split T]
-//            [--all-prompt-rows] [--seed S] [--rows N]
+//            [--all-prompt-rows] [--seed S] [--rows N] [--q8]
 //
 // qkv: the QKV projection of N rows per layer with K/V appended in its
 // epilogue; --per-layer runs the unfused path (f32 projection + append).
@@ -20,6 +20,7 @@ static uint32_t pages(uint32_t n) { return (n + NI_KV_BLOCK - 1) / NI_KV_BLOCK; 
 int main(int argc, char** argv) {
     ni_drive_opts o{};
     std::string workload = "serve";
+    bool q8 = false;  // the Q8 cache (NI_KV_Q8)
     o.launch = NI_DRIVE_STEP;
     o.steps = 2000;
     o.warmup = 300;
@@ -36,6 +37,7 @@ int main(int argc, char** argv) {
         };
         if (!strcmp(a, "serve") || !strcmp(a, "spec") || !strcmp(a, "qkv")) workload = a;
         else if (!strcmp(a, "--rows")) o.qkv_rows = (uint32_t)atoi(val(a));
+        else if (!strcmp(a, "--q8")) q8 = true;
         else if (!strcmp(a, "--per-layer")) o.launch = NI_DRIVE_PER_LAYER;
         else if (!strcmp(a, "--all-prompt-rows")) o.serve.query_all_prompt_rows = 1;
         else if (!strcmp(a, "--steps")) o.steps = (uint32_t)atoi(val(a));
@@ -44,7 +46,7 @@ int main(int argc, char** argv) {
         else if (!strcmp(a, "--seed")) o.data_seed = o.serve.seed = strtoull(val(a), nullptr, 10);
         else {
             fprintf(stderr, "usage: ni_drive [serve|spec|qkv] [--per-layer] [--steps K] [--warmup W] [--split T] "
-                            "[--all-prompt-rows] [--seed S] [--rows N]\n");
+                            "[--all-prompt-rows] [--seed S] [--rows N] [--q8]\n");
             return 2;
         }
     }
@@ -78,6 +80,7 @@ int main(int argc, char** argv) {
         o.kv.max_seqs = o.spec_seqs;
         o.kv.max_rows = 512;
     }
+    if (q8) o.kv.flags |= NI_KV_Q8;
     ni_drive_result r{};
     if (int rc = ni_drive_run(&o, &r)) {
         fprintf(stderr, "ni_drive: %s (status %d)\n", ni_drive_last_error(), rc);
@@ -91,9 +94,9 @@ int main(int argc, char** argv) {
            "\"value\": %.2f, \"unit\": \"GB/s\", \"pct_of_peak\": %.2f, \"ms_per_step\": %.5f, "
            "\"gpu_ms_per_step\": %.5f, \"host_us_per_step\": %.1f, \"abi_calls_per_step\": %.1f, "
            "\"seq_tokens_per_s\": %.1f, \"algorithmic_bytes_per_step\": %.0f, \"mean_live\": %.2f, "
-           "\"mean_context\": %.1f}\n",
+           "\"mean_context\": %.1f, \"kv\": \"%s\"}\n",
            workload.c_str(), o.launch == NI_DRIVE_STEP ? "step" : "per-layer", r.steps, o.warmup, gbs,
            100.0 * gbs / 8000.0, r.seconds / r.steps * 1e3, r.gpu_seconds / r.steps * 1e3, r.host_us_per_step,
-           (double)r.launches / r.steps, r.seq_tokens / r.seconds, r.bytes / r.steps, r.mean_live, r.mean_context);
+           (double)r.launches / r.steps, r.seq_tokens / r.seconds, r.bytes / r.steps, r.mean_live, r.mean_context, q8 ? "q8" : "f16");
     return 0;
 }
