@@ -46,15 +46,26 @@ def log(*a):
 
 
 PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "attn_split_fused_config3.md")
+# Workloads whose committed profile holds a PMC traffic section.
+TRAFFIC_PROFILES = {
+    "config3": PROFILE_SUMMARY,
+    "config2": os.path.join(ROOT, "profiles", "attn_split_config2.md"),
+    "config4": os.path.join(ROOT, "profiles", "attn_split_merge_config4.md"),
+    "config5": os.path.join(ROOT, "profiles", "attn_mfma_config5.md"),
+}
 
 
-def measured_traffic():
-    """HBM bytes per launch of the attention kernel from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (scaled by the copy calibration
-    it records), with the algorithmic bytes of the same profiled steps."""
+def measured_traffic(workload="config3"):
+    """HBM bytes per launch of the attention kernel (with its merge, where
+    the workload splits) from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (scaled by the copy calibration it records), with the
+    algorithmic bytes of the same profiled steps."""
     vals = {}
+    path = TRAFFIC_PROFILES.get(workload)
+    if path is None:
+        return None
     try:
-        for line in open(PROFILE_SUMMARY):
+        for line in open(path):
             if "=" in line and line.split("=")[0].strip() in ("traffic_bytes_per_launch",
                                                               "algorithmic_bytes_per_launch_same_steps"):
                 k, v = line.split("=")
@@ -324,6 +335,13 @@ def run_secondary(args):
         res["roofline"] = _roofline(rp, "attn_q8_kernel (+ attn_merge_kernel when split)" if args.workload.endswith("q8")
                                     else "attn_split_kernel / attn_mfma_kernel (+ attn_merge_kernel when split)",
                                     with_merge=True)
+        tr = measured_traffic(args.workload)
+        if tr:
+            res["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
+            res["roofline"]["traffic_vs_algorithmic"] = round(
+                tr["traffic_bytes_per_launch"] / tr["algorithmic_bytes_per_launch_same_steps"], 3)
+            res["roofline"]["traffic_source"] = os.path.relpath(TRAFFIC_PROFILES[args.workload], ROOT) + \
+                " (rocprofv3 --pmc, scaled; attention + merge per step)"
     if args.workload.endswith("q8"):
         res["kv_dtype"] = "int8 + f32 scale per (position, head)"
     return res
