@@ -902,6 +902,23 @@ __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanA
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Four signed int8 values (bytes 0..3 of w) as f16, exactly and bit for bit
+// as static_cast<_Float16>: the f16 bit pattern 0x6400 | (b ^ 0x80) is 1024 +
+// (b + 128), and subtracting 1152 leaves b (operands and result exactly
+// representable, so the subtraction does not round).  Two values per byte
+// permute (a byte to the low byte of each 16-bit half, zeros above), XOR and
+// packed f16 subtract, against a bit extract and two conversions per value.
+__device__ __forceinline__ half4_t i8x4_f16(uint32_t w) {
+    const uint32_t lo = __builtin_amdgcn_perm(w, w, 0x0c010c00u) ^ 0x64806480u;  // bytes 0, 1
+    const uint32_t hi = __builtin_amdgcn_perm(w, w, 0x0c030c02u) ^ 0x64806480u;  // bytes 2, 3
+    const half2_t k1152 = {static_cast<_Float16>(1152.f), static_cast<_Float16>(1152.f)};
+    const half2_t a = __builtin_bit_cast(half2_t, lo) - k1152;
+    const half2_t b = __builtin_bit_cast(half2_t, hi) - k1152;
+    return half4_t{a[0], a[1], b[0], b[1]};
+}
+
 // f32 -> f16 hi plus the residual scaled by 2^11 (kept in the normal range
 // of f16, where the residual itself would often be subnormal): x ~= hi +
 // lo * 2^-11 to ~2^-22 relative.  Products of hi and of lo are accumulated
@@ -1080,16 +1097,10 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 const u32x4 val = (pg + b) * kPage + key < it.kv_end ? cur.v[b][i] : u32x4{0, 0, 0, 0};
                 _Float16* dst = my_vt + (b * kPage + key) * VROW + (lane % LPK) * VE;
                 if constexpr (Q8) {
-                    half8_t h0, h1;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        h0[j] = static_cast<_Float16>(i8f(val[0], j));
-                        h0[4 + j] = static_cast<_Float16>(i8f(val[1], j));
-                        h1[j] = static_cast<_Float16>(i8f(val[2], j));
-                        h1[4 + j] = static_cast<_Float16>(i8f(val[3], j));
-                    }
-                    reinterpret_cast<half8_t*>(dst)[0] = h0;
-                    reinterpret_cast<half8_t*>(dst)[1] = h1;
+                    reinterpret_cast<half4_t*>(dst)[0] = i8x4_f16(val[0]);
+                    reinterpret_cast<half4_t*>(dst)[1] = i8x4_f16(val[1]);
+                    reinterpret_cast<half4_t*>(dst)[2] = i8x4_f16(val[2]);
+                    reinterpret_cast<half4_t*>(dst)[3] = i8x4_f16(val[3]);
                 } else {
                     *reinterpret_cast<u32x4*>(dst) = val;
                 }
@@ -1105,11 +1116,8 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
             for (int c = 0; c < QC; c++) {
                 half8_t kh;
                 if constexpr (Q8) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        kh[j] = static_cast<_Float16>(i8f(cur.k[b][c][0], j));
-                        kh[4 + j] = static_cast<_Float16>(i8f(cur.k[b][c][1], j));
-                    }
+                    const half4_t k0 = i8x4_f16(cur.k[b][c][0]), k1 = i8x4_f16(cur.k[b][c][1]);
+                    kh = half8_t{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
                 } else {
                     kh = __builtin_bit_cast(half8_t, cur.k[b][c]);
                 }
