@@ -1160,11 +1160,18 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // Rescale only when some query's running max moved: otherwise every
+        // alpha is exactly 1 and the multiplies change nothing.
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+            for (int c = 0; c < VC; c++) {
+                o[c] *= alpha;
+                ol[c] *= alpha;
+            }
+        }
         // O^T += V^T P^T, 16 dims per product.
 #pragma unroll
         for (int c = 0; c < VC; c++) {
-            o[c] *= alpha;
-            ol[c] *= alpha;
 #pragma unroll
             for (int b = 0; b < PB; b++) {
                 half4_t vt4;
