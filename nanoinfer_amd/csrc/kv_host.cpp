@@ -68,6 +68,7 @@ struct Plan {
     uint32_t nq_tile = 1;
     uint32_t napp_total = 0;  // fused: rows the attention items append
     bool fused = false;
+    bool wide = false;        // kWideWaves waves per attention workgroup
     void clear() {
         app.clear();
         orphans.clear();
@@ -78,6 +79,7 @@ struct Plan {
         nq_tile = 1;
         napp_total = 0;
         fused = false;
+        wide = false;
     }
 };
 
@@ -266,14 +268,25 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     // the tail is short -- only items longer than kLongItem keys are split
     // then.  Below that, the largest of 1024/512/256/128 tokens that yields
     // >= 2048 workgroups.
+    // Between kWideMinUnits and kFillWorkgroups units of single-row items
+    // (head_dim 64: a launch of one layer of 43..170 sequences), workgroups
+    // of kWideWaves waves share each item's pages instead of splitting it:
+    // no partials, no merge launch.
     uint32_t part = split_tokens;
     if (part == 0) {
         constexpr uint64_t kFillWorkgroups = 2048;
+        constexpr uint64_t kWideMinUnits = 512;
         constexpr uint32_t kLongItem = 4096;
         static const uint32_t kChoices[] = {1024, 512, 256, 128};
         const uint64_t per_unit = (uint64_t)n_lay * kv->o.n_head;
-        if ((uint64_t)groups.size() * per_unit >= kFillWorkgroups) {
+        const uint64_t units = (uint64_t)groups.size() * per_unit;
+        bool single = true;
+        for (const Group& g : groups) single &= g.nq == 1;
+        if (units >= kFillWorkgroups) {
             part = kLongItem;
+        } else if (single && units >= kWideMinUnits && kv->o.head_dim == 64) {
+            part = kLongItem;
+            P.wide = true;
         } else {
             part = kChoices[3];
             for (uint32_t c : kChoices) {
@@ -549,6 +562,7 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
         a.n_lay = n_lay;
         a.nq_tile = P.nq_tile;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
+        a.wide = P.wide ? 1u : 0u;
         a.n_orphan_blocks = P.fused ? orphan_blocks(a) : 0;
         {
             ProfileScope ps(kv, NI_K_ATTN);

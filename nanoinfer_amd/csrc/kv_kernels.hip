@@ -1332,6 +1332,18 @@ hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
     constexpr int PB = NQ > 1 ? 1 : (D == 128 ? NI_ATTN_PAGES_D128 : kPagesPerIter);
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
+    if constexpr (D == 64 && NQ == 1) {
+        if (a.wide) {
+            constexpr int WW = kWideWaves;
+            return with_plan(a, ip, ib, [&](auto pa) {
+                constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+                if (a.napp_total || a.n_orphan_blocks)
+                    return go(attn_split_kernel<D, NQ, WW, PB, true, INL>, blocks, 64 * WW, s, t, a, pa);
+                return go(attn_split_kernel<D, NQ, WW, PB, false, INL>, blocks, 64 * WW, s, t, a, pa);
+            });
+        }
+    }
+    if (a.wide) return hipErrorInvalidValue;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         if (a.napp_total || a.n_orphan_blocks)
@@ -1366,6 +1378,19 @@ template <int D>
 hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
+    if constexpr (D == 64) {
+        if (a.wide) {
+            constexpr int WW = kWideWaves;
+            return with_plan(a, ip, ib, [&](auto pa) {
+                constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+                constexpr int PB = NI_Q8_PAGES;
+                if (a.napp_total || a.n_orphan_blocks)
+                    return go(attn_q8_kernel<D, WW, PB, true, INL>, blocks, 64 * WW, s, t, a, pa);
+                return go(attn_q8_kernel<D, WW, PB, false, INL>, blocks, 64 * WW, s, t, a, pa);
+            });
+        }
+    }
+    if (a.wide) return hipErrorInvalidValue;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         constexpr int PB = NI_Q8_PAGES;
@@ -1464,7 +1489,8 @@ hipError_t launch_attention(const AttnLaunch& a, const void* ip, uint32_t ib, hi
 
 uint32_t orphan_blocks(const AttnLaunch& a) {
     const uint64_t threads = (uint64_t)a.n_lay * a.n_orphans * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
-    return (uint32_t)((threads + 64 * kWaves - 1) / (64 * kWaves));
+    const uint64_t per_block = 64ull * (a.wide ? kWideWaves : kWaves);
+    return (uint32_t)((threads + per_block - 1) / per_block);
 }
 
 hipError_t launch_merge(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {

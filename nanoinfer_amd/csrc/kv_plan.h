@@ -21,6 +21,15 @@ constexpr uint32_t kNoSlot = 0xffffffffu; // AttnItem::part_slot: the item is it
 #define NI_ATTN_MFMA 1
 #endif
 constexpr uint32_t kMfmaTile = 16;
+// Waves per workgroup of a "wide" launch of single-row items: when a launch has
+// too few (item, layer, head) units to fill the GPU, each item's pages are
+// spread over this many waves of one workgroup (merged through LDS) instead of
+// being split into partitions merged by a second kernel.  8 measured best (per
+// layer, config 3: 2900 -> 3464 GB/s f16, 1697 -> 2167 Q8; 16 waves: 3078, 1594).
+#ifndef NI_WIDE_WAVES
+#define NI_WIDE_WAVES 8
+#endif
+constexpr uint32_t kWideWaves = NI_WIDE_WAVES;
 constexpr uint32_t kMaxGroupRows = NI_ATTN_MFMA ? kMfmaTile : 8;  // most query rows sharing one K/V stream
 
 // Where one appended row goes: pool page `page`, position `slot` (0..15) in it.
@@ -164,6 +173,7 @@ struct AttnLaunch {
     uint32_t n_lay;
     uint32_t nq_tile;         // query tile: 1..8 (vector kernel) or kMfmaTile (matrix cores)
     float qscale;             // log2(e) / sqrt(head_dim)
+    uint32_t wide;            // 1: kWideWaves waves per workgroup (single-row items, head_dim 64)
 };
 
 // A plan travels to the device either inside the kernel arguments (up to

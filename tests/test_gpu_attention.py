@@ -10,7 +10,7 @@ import torch
 import oracle
 import nanoinfer_amd as na
 from nanoinfer_amd import workloads
-from paged_mirror import Mirror, assert_close
+from paged_mirror import Mirror, assert_close, mirror_step, step_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -206,3 +206,41 @@ def test_config4_full_size(gpu, oracle_lib):
     got, want = m.attention(rows, q, split_tokens=512)
     err = assert_close(got, want, "config 4")
     say(f"config 4: max abs err {err:.2e}")
+
+
+def test_wide_workgroups(gpu, oracle_lib):
+    """Launches of single rows with 512..2047 (item, layer, head) units run
+    wide workgroups (kWideWaves waves) sharing each item's pages (no
+    partitions, no merge launch): per-layer decode of 48 sequences (576 units), all layers of 30
+    sequences (720) and a fused step of 30 decode rows plus a mid-prompt
+    chunk (orphan rows), against the oracle."""
+    rng = np.random.default_rng(31)
+    shape = dict(n_layer=2, n_head=12, head_dim=64)
+    m = Mirror(opts(shape, kv_blocks=1400, max_seqs=48, n_ctx=1024))
+    seqs = [m.kv.add_seq() for _ in range(48)]
+    lens = np.concatenate([[1, 2, 16, 17, 33, 400], rng.integers(3, 401, 42)])
+    for s, L in zip(seqs, lens):
+        m.fill(s, int(L), rng)
+    m.kv.profile([1, 2])
+    rows = [(s, int(L) - 1) for s, L in zip(seqs, lens)]
+    for layer in (0, 1):
+        q = rng.standard_normal((len(rows), m.c)).astype(np.float32)
+        got, want = m.attention(rows, q, layer=layer)
+        assert_close(got, want, f"per-layer {layer}")
+    q = rng.standard_normal((2, 30, m.c)).astype(np.float32)
+    got, want = m.attention(rows[:30], q)
+    assert_close(got, want, "all layers, 30 sequences")
+    # fused step: decode rows of 30 sequences, 40 rows of a prompt without a query
+    work = [(s, 1, 1) for s in seqs[:30]] + [(seqs[40], 40, 0)]
+    srows, _ = step_rows(m.kv, work)
+    n = len(srows)
+    q, k, v = (rng.standard_normal((2, n, m.c)).astype(np.float32) for _ in range(3))
+    got, want, qr = mirror_step(m, work, q, k, v)
+    assert_close(got[:, qr], want[:, qr], "fused step")
+    (kg, vg), (kw, vw) = m.gather(srows)
+    assert np.array_equal(kg, kw) and np.array_equal(vg, vw)
+    _, n_attn = m.kv.profile_read(1)
+    _, n_merge = m.kv.profile_read(2)
+    m.kv.profile([])
+    assert n_attn == 4 and n_merge == 0, (n_attn, n_merge)
+    say("wide workgroups: per-layer, all-layer and fused launches within bounds, no merge launches")
