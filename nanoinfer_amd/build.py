@@ -43,6 +43,9 @@ def command(out: str = LIB) -> list[str]:
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         # Q8 scales: amax / 127 and its inverse must be IEEE divisions.
         "-fhip-fp32-correctly-rounded-divide-sqrt",
+        # Matrix-core accumulators in VGPRs: the online softmax rescales them
+        # with VALU multiplies, which in AGPRs cost a read and a write each.
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-Wall", "-Wno-unused-function",
         f"-I{INCLUDE}", f"-I{CSRC}",
         *SOURCES, "-o", out,

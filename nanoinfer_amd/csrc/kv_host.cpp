@@ -63,8 +63,11 @@ struct Plan {
     std::vector<AppendEntry> orphans;  // fused: rows of sequences without queries
     std::vector<AttnItem> items;
     std::vector<MergeItem> merges;
+    std::vector<AttnItem> pitems;    // prefill groups (attn_prefill_kernel), their merges
+    std::vector<MergeItem> pmerges;  //   and partial slots (a region after the others')
     std::vector<uint32_t> table;
     uint32_t n_slots = 0;
+    uint32_t n_pslots = 0;
     uint32_t nq_tile = 1;
     uint32_t napp_total = 0;  // fused: rows the attention items append
     bool fused = false;
@@ -74,8 +77,11 @@ struct Plan {
         orphans.clear();
         items.clear();
         merges.clear();
+        pitems.clear();
+        pmerges.clear();
         table.clear();
         n_slots = 0;
+        n_pslots = 0;
         nq_tile = 1;
         napp_total = 0;
         fused = false;
@@ -250,7 +256,9 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     };
     std::vector<Group> groups;
     groups.reserve(qr.size());
-    const uint32_t max_group = max_group_rows(kv);
+    // Runs longer than one matrix tile form prefill groups (f16 pools).
+    const bool prefill = NI_ATTN_MFMA && NI_ATTN_PREFILL && !is_q8(kv->o);
+    const uint32_t max_group = prefill ? kPrefillRows : max_group_rows(kv);
     for (const QRow& r : qr) {
         if (!groups.empty()) {
             Group& g = groups.back();
@@ -315,6 +323,8 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     }
     uint32_t max_nq = 1;
     // An item [b, e) of a fused step appends this call's new rows in [b, e).
+    // (Prefill groups only occur in unfused calls: a fused step has at most
+    // max_group_rows queries per sequence.)
     auto item = [&](const Group& g, uint32_t tab, uint32_t b, uint32_t e, uint32_t slot) {
         AttnItem it{};
         it.tab = tab;
@@ -332,10 +342,11 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
                 P.napp_total += it.napp;
             }
         }
-        P.items.push_back(it);
+        (g.nq > kMfmaTile ? P.pitems : P.items).push_back(it);
     };
     for (const Group& g : groups) {
-        max_nq = std::max(max_nq, g.nq);
+        const bool pre = g.nq > kMfmaTile;
+        if (!pre) max_nq = std::max(max_nq, g.nq);
         const uint32_t L = g.pos0 + g.nq;
         const uint32_t n_parts = (L + part - 1) / part;
         const uint32_t tab = (uint32_t)kv->seq_tab[g.seq];
@@ -343,10 +354,11 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
             item(g, tab, 0, L, kNoSlot);
             continue;
         }
-        const uint32_t slot0 = P.n_slots;
+        uint32_t& n_slots = pre ? P.n_pslots : P.n_slots;
+        const uint32_t slot0 = n_slots;
         for (uint32_t p = 0; p < n_parts; p++) item(g, tab, p * part, std::min((p + 1) * part, L), slot0 + p);
-        P.merges.push_back({g.row0, g.nq, slot0, n_parts});
-        P.n_slots += n_parts;
+        (pre ? P.pmerges : P.merges).push_back({g.row0, g.nq, slot0, n_parts});
+        n_slots += n_parts;
     }
     for (const Group& g : groups) {
         kv->seq_need[g.seq] = 0;
@@ -354,9 +366,11 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     }
     // Longest first, so the long items start early and the short ones fill
     // the tail.
-    std::stable_sort(P.items.begin(), P.items.end(), [](const AttnItem& x, const AttnItem& y) {
+    auto longest_first = [](const AttnItem& x, const AttnItem& y) {
         return (x.kv_end - x.kv_begin) > (y.kv_end - y.kv_begin);
-    });
+    };
+    std::stable_sort(P.items.begin(), P.items.end(), longest_first);
+    std::stable_sort(P.pitems.begin(), P.pitems.end(), longest_first);
     // Single queries stream on the vector kernel; groups go to matrix cores.
     P.nq_tile = (NI_ATTN_MFMA && max_nq > 1) ? kMfmaTile : max_nq;
     return NI_OK;
@@ -433,7 +447,7 @@ int ensure_partials(ni_kv* kv, size_t bytes) {
 }
 
 struct Offsets {
-    size_t app, orphans, items, merges, table, total;
+    size_t app, orphans, items, merges, pitems, pmerges, table, total;
 };
 
 Offsets layout(const Plan& P) {
@@ -442,7 +456,9 @@ Offsets layout(const Plan& P) {
     o.orphans = align_up(o.app + P.app.size() * sizeof(AppendEntry), kAlign);
     o.items = align_up(o.orphans + P.orphans.size() * sizeof(AppendEntry), kAlign);
     o.merges = align_up(o.items + P.items.size() * sizeof(AttnItem), kAlign);
-    o.table = align_up(o.merges + P.merges.size() * sizeof(MergeItem), kAlign);
+    o.pitems = align_up(o.merges + P.merges.size() * sizeof(MergeItem), kAlign);
+    o.pmerges = align_up(o.pitems + P.pitems.size() * sizeof(AttnItem), kAlign);
+    o.table = align_up(o.pmerges + P.pmerges.size() * sizeof(MergeItem), kAlign);
     o.total = align_up(o.table + P.table.size() * sizeof(uint32_t), kAlign);
     return o;
 }
@@ -467,6 +483,9 @@ int place_plan(ni_kv* kv, hipStream_t s, Offsets* off, PlanRef* ref) {
         memcpy(blob.data() + off->orphans, P.orphans.data(), P.orphans.size() * sizeof(AppendEntry));
     if (!P.items.empty()) memcpy(blob.data() + off->items, P.items.data(), P.items.size() * sizeof(AttnItem));
     if (!P.merges.empty()) memcpy(blob.data() + off->merges, P.merges.data(), P.merges.size() * sizeof(MergeItem));
+    if (!P.pitems.empty()) memcpy(blob.data() + off->pitems, P.pitems.data(), P.pitems.size() * sizeof(AttnItem));
+    if (!P.pmerges.empty())
+        memcpy(blob.data() + off->pmerges, P.pmerges.data(), P.pmerges.size() * sizeof(MergeItem));
     if (!P.table.empty()) memcpy(blob.data() + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
     *ref = PlanRef{};
     if (off->total <= kInlinePlanBytes) {
@@ -509,9 +528,11 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
              int64_t out_row_stride, int64_t out_layer_stride, hipStream_t s) {
     Plan& P = kv->plan;
     const uint32_t D = kv->o.head_dim, H = kv->o.n_head;
-    if (!P.items.empty() && P.n_slots > 0) {
-        const size_t need = (size_t)P.n_slots * n_lay * H * P.nq_tile * (D + 2) * sizeof(float);
-        int rc = ensure_partials(kv, need);
+    // Partials: the single-row/group launch's slots, then the prefill launch's.
+    const size_t main_floats = (size_t)P.n_slots * n_lay * H * P.nq_tile * (D + 2);
+    const size_t pre_floats = (size_t)P.n_pslots * n_lay * H * kPrefillRows * (D + 2);
+    if (main_floats + pre_floats > 0) {
+        int rc = ensure_partials(kv, (main_floats + pre_floats) * sizeof(float));
         if (rc) return rc;
     }
     Offsets off;
@@ -535,7 +556,7 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
         if (e != hipSuccess) return kv->hip_fail(e, "append kernel");
     }
     if (!P.items.empty() || !P.orphans.empty()) {
-        AttnLaunch a;
+        AttnLaunch a{};
         a.pool = kv->geom();
         a.k = k;
         a.v = v;
@@ -573,6 +594,39 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
             ProfileScope ps(kv, NI_K_MERGE);
             hipError_t e = launch_merge(a, ref.inl, ref.inl_bytes, s, ps.t);
             if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
+        }
+    }
+    if (!P.pitems.empty()) {
+        // Prefill groups: their own launch (after the append above), items,
+        // merges and partials region; never fused.
+        AttnLaunch a{};
+        a.pool = kv->geom();
+        a.q = q;
+        a.q_row_stride = q_row_stride;
+        a.q_layer_stride = q_layer_stride;
+        a.out = out;
+        a.out_row_stride = out_row_stride;
+        a.out_layer_stride = out_layer_stride;
+        a.plan = ref.dev;
+        a.off_items = (uint32_t)off.pitems;
+        a.off_table = (uint32_t)off.table;
+        a.off_merges = (uint32_t)off.pmerges;
+        a.partials = kv->partials ? kv->partials + main_floats : nullptr;
+        a.n_items = (uint32_t)P.pitems.size();
+        a.n_merges = (uint32_t)P.pmerges.size();
+        a.layer0 = layer0;
+        a.n_lay = n_lay;
+        a.nq_tile = kPrefillRows;
+        a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
+        {
+            ProfileScope ps(kv, NI_K_ATTN);
+            hipError_t e = launch_attention(a, ref.inl, ref.inl_bytes, s, ps.t);
+            if (e != hipSuccess) return kv->hip_fail(e, "prefill attention kernel");
+        }
+        if (!P.pmerges.empty()) {
+            ProfileScope ps(kv, NI_K_MERGE);
+            hipError_t e = launch_merge(a, ref.inl, ref.inl_bytes, s, ps.t);
+            if (e != hipSuccess) return kv->hip_fail(e, "prefill merge kernel");
         }
     }
     return release_plan(kv, ref, s);

@@ -1226,6 +1226,220 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     }
 }
 
+// ------------------------------------------------- attention, prefill groups
+//
+// Groups of kMfmaTile+1 .. kPrefillRows consecutive query rows of one
+// sequence (a prompt chunk with every row queried).  Wave w owns rows
+// 16w .. 16w+15 of the group and runs attn_mfma_kernel's per-page arithmetic
+// for them (S^T = K Q^T with q split into f16 hi + scaled lo, the online
+// softmax on S^T's columns, O^T += V^T P^T with p split likewise), but the
+// workgroup's 256 threads load each tile of PT pages of K and V once into LDS
+// (double buffered, one barrier per tile) and all four waves read it there:
+// each K/V byte leaves memory once per 64 queries instead of once per 16.
+// Keys past the item's end are zeroed in LDS (stale halves, possibly NaN bit
+// patterns, never reach a product); a wave skips pages past its own last
+// query.  No cross-wave merge: each wave writes its own rows (or their
+// partials when the group is split into partitions).
+#ifndef NI_PREFILL_PAGES
+#define NI_PREFILL_PAGES 2
+#endif
+constexpr int kPrefillPages = NI_PREFILL_PAGES;  // pages per LDS tile
+
+template <int D, int PT, int INL>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+    constexpr int QC = D / 32;              // 32-dim chunks of the QK product
+    constexpr int VC = D / 16;              // 16-dim chunks of the PV product
+    constexpr int ROW = D + 8;              // LDS halves per key row (pad: conflict-free column reads)
+    constexpr int TK = PT * (int)kPage;     // keys per tile
+    constexpr int CH = D / 8;               // 16-byte chunks per key row
+    constexpr int CPT = TK * CH / 256;      // chunks of K (and of V) per thread per tile
+    static_assert(TK * CH % 256 == 0, "a tile must split evenly over the workgroup");
+    __shared__ __attribute__((aligned(16))) _Float16 kt[2][TK * ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][TK * ROW];
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t H = a.pool.n_head;
+    const uint32_t lh = a.n_lay * H;
+    const uint8_t* plan = plan_base(pa, a.plan);
+    const uint32_t item_i = blockIdx.x / lh;
+    const uint32_t rem = blockIdx.x - item_i * lh;
+    const uint32_t lay = rem / H;
+    const uint32_t head = rem - lay * H;
+    const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
+    const int col = lane & 15;  // query slot of S^T / O^T columns
+    const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
+
+    const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
+    const uint16_t* kbase = a.pool.k + layer_off;
+    const uint16_t* vbase = a.pool.v + layer_off;
+    const uint64_t page_stride = a.pool.page_halves;
+    const uint32_t* __restrict__ tab = reinterpret_cast<const uint32_t*>(plan + a.off_table) + it.tab;
+    const uint32_t pg_begin = it.kv_begin / kPage;
+    const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
+
+    // This wave's queries: rows r0 .. r0+nqw-1 of the group.
+    const uint32_t r0 = wave * 16;
+    const uint32_t nqw = it.nq > r0 ? min(16u, it.nq - r0) : 0u;
+    const bool qok = col < (int)nqw;
+    const uint32_t qpos = it.pos0 + r0 + col;
+    const uint32_t kend_w = min(it.kv_end, it.pos0 + r0 + nqw);  // keys this wave needs end here
+
+    // Tile staging: chunk u = threadIdx.x + 256 j of a tile is key u / CH of
+    // the tile (page u / CH / 16 of it, slot (u / CH) % 16), halves
+    // (u % CH) * 8 .. +7.
+    u32x4 kr[CPT], vr[CPT];
+    auto fetch = [&](uint32_t pg) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const uint32_t u = threadIdx.x + 256 * j, key = u / CH, c8 = (u % CH) * 8;
+            const uint32_t p = pg + key / kPage;
+            if (p < pg_end) {
+                const uint64_t off = (uint64_t)tab[p] * page_stride + (key % kPage) * D + c8;
+                kr[j] = load16(reinterpret_cast<const u32x4*>(kbase + off));
+                vr[j] = load16(reinterpret_cast<const u32x4*>(vbase + off));
+            } else {
+                kr[j] = vr[j] = u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    auto stage = [&](int buf, uint32_t pg) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const uint32_t u = threadIdx.x + 256 * j, key = u / CH, c8 = (u % CH) * 8;
+            const bool in = pg * kPage + key < it.kv_end;
+            *reinterpret_cast<u32x4*>(&kt[buf][key * ROW + c8]) = in ? kr[j] : u32x4{0, 0, 0, 0};
+            *reinterpret_cast<u32x4*>(&vt[buf][key * ROW + c8]) = in ? vr[j] : u32x4{0, 0, 0, 0};
+        }
+    };
+    fetch(pg_begin);
+
+    // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo.
+    half8_t qh[QC], ql[QC];
+    {
+        const float* qb = a.q + (int64_t)lay * a.q_layer_stride +
+                          (int64_t)(it.row0 + r0 + (qok ? col : 0)) * a.q_row_stride + head * D + 8 * rg;
+#pragma unroll
+        for (int c = 0; c < QC; c++) {
+            float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (qok) {
+                const float4 x0 = reinterpret_cast<const float4*>(qb + c * 32)[0];
+                const float4 x1 = reinterpret_cast<const float4*>(qb + c * 32)[1];
+                x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
+                x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                _Float16 h, l;
+                split_f16(x[e] * a.qscale, h, l);
+                qh[c][e] = h;
+                ql[c][e] = l;
+            }
+        }
+    }
+    float m = kMinScore, lsum = 0.f;
+    float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
+#pragma unroll
+    for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    stage(0, pg_begin);
+    __syncthreads();
+    const uint32_t n_tiles = (pg_end - pg_begin + PT - 1) / PT;
+    for (uint32_t ti = 0; ti < n_tiles; ti++) {
+        const uint32_t pg = pg_begin + ti * PT;
+        const int buf = ti & 1;
+        const bool more = ti + 1 < n_tiles;
+        if (more) fetch(pg + PT);
+#pragma unroll
+        for (int b = 0; b < PT; b++) {
+            if ((pg + b) * kPage >= kend_w) break;  // wave-uniform: past this wave's last query
+            const _Float16* kp = &kt[buf][b * kPage * ROW];
+            const _Float16* vp = &vt[buf][b * kPage * ROW];
+            // S^T = K Q^T: scores of keys 4*rg+j of the page for query col.
+            float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < QC; c++) {
+                const half8_t kh = *reinterpret_cast<const half8_t*>(kp + col * ROW + c * 32 + 8 * rg);
+                st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
+            }
+            float sc[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t key = (pg + b) * kPage + 4 * rg + j;
+                const bool ok = qok && key < it.kv_end && key <= qpos;
+                sc[j] = ok ? st[j] + sl[j] * kLoUnscale : -INFINITY;
+                mx = fmaxf(mx, sc[j]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mn = fmaxf(m, mx);
+            const float alpha = fast_exp2(m - mn);
+            m = mn;
+            half4_t ph, pl;
+            float ps = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float p = fast_exp2(sc[j] - mn);
+                ps += p;
+                _Float16 h, l;
+                split_f16(p * kPScale, h, l);
+                ph[j] = h;
+                pl[j] = l;
+            }
+            lsum = lsum * alpha + ps;
+            // Rescale only when some query's running max moved (alpha == 1 otherwise).
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int c = 0; c < VC; c++) {
+                    o[c] *= alpha;
+                    ol[c] *= alpha;
+                }
+            }
+            // O^T += V^T P^T, 16 dims per product.
+#pragma unroll
+            for (int c = 0; c < VC; c++) {
+                half4_t v4;
+#pragma unroll
+                for (int j = 0; j < 4; j++) v4[j] = vp[(4 * rg + j) * ROW + c * 16 + col];
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph, o[c], 0, 0, 0);
+                ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl, ol[c], 0, 0, 0);
+            }
+        }
+        if (more) stage(buf ^ 1, pg + PT);
+        __syncthreads();  // the next tile is staged; nobody reads this one any more
+    }
+    // Lanes q, q+16, q+32, q+48 hold partial sums of query q's softmax.
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (!qok) return;
+    const uint32_t row = it.row0 + r0 + col;
+    if (it.part_slot == kNoSlot) {
+        float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)row * a.out_row_stride + head * D;
+        const float scale = kPUnscale / lsum;
+#pragma unroll
+        for (int c = 0; c < VC; c++) {
+            float4 y;
+            y.x = (o[c][0] + ol[c][0] * kLoUnscale) * scale;
+            y.y = (o[c][1] + ol[c][1] * kLoUnscale) * scale;
+            y.z = (o[c][2] + ol[c][2] * kLoUnscale) * scale;
+            y.w = (o[c][3] + ol[c][3] * kLoUnscale) * scale;
+            *reinterpret_cast<float4*>(dst + c * 16 + 4 * rg) = y;
+        }
+    } else {
+        float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * H + head) * kPrefillRows + r0 + col) * (D + 2);
+        if (rg == 0) {
+            p[0] = m;
+            p[1] = lsum;
+        }
+#pragma unroll
+        for (int c = 0; c < VC; c++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * kPUnscale;
+    }
+}
+
 // One workgroup per (merge item, layer, head).  Thread t owns output unit
 // u = (row, dim) of the group and partitions j, j+G, j+2G, ... where G =
 // kMergeThreads / (rows * D) groups of threads split the partitions; each
@@ -1375,6 +1589,18 @@ hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
 }
 
 template <int D>
+hipError_t prefill_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
+    const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head;
+    if (blocks == 0) return hipSuccess;
+    return with_plan(a, ip, ib, [&](auto pa) {
+        constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+        // head_dim 128 stages one page per tile (two spill registers).
+        constexpr int PT = D == 128 ? 1 : kPrefillPages;
+        return go(attn_prefill_kernel<D, PT, INL>, blocks, 256, s, t, a, pa);
+    });
+}
+
+template <int D>
 hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
@@ -1403,6 +1629,10 @@ hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStre
 template <int D>
 hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge,
                             const LaunchTiming& t) {
+    if (a.nq_tile == kPrefillRows) {  // prefill groups (f16 pools only)
+        if (a.pool.q8) return hipErrorInvalidValue;
+        return merge ? merge_launch_t<D, kPrefillRows>(a, ip, ib, s, t) : prefill_launch_t<D>(a, ip, ib, s, t);
+    }
     if (a.pool.q8) {  // single rows on the vector kernel, groups on the matrix cores
         if (a.nq_tile == kMfmaTile)
             return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s, t) : mfma_launch_t<D, true>(a, ip, ib, s, t);

@@ -21,6 +21,13 @@ constexpr uint32_t kNoSlot = 0xffffffffu; // AttnItem::part_slot: the item is it
 #define NI_ATTN_MFMA 1
 #endif
 constexpr uint32_t kMfmaTile = 16;
+// Prefill: groups of kMfmaTile+1 .. kPrefillRows consecutive query rows of one
+// sequence run on attn_prefill_kernel (f16 pools), one 16-row tile per wave,
+// every wave reading the same K/V tiles from LDS.
+#ifndef NI_ATTN_PREFILL
+#define NI_ATTN_PREFILL 1
+#endif
+constexpr uint32_t kPrefillRows = 64;
 // Waves per workgroup of a "wide" launch of single-row items: when a launch has
 // too few (item, layer, head) units to fill the GPU, each item's pages are
 // spread over this many waves of one workgroup (merged through LDS) instead of
@@ -166,12 +173,12 @@ struct AttnLaunch {
     uint32_t off_items;       // AttnItem[n_items], sorted longest first
     uint32_t off_table;       // uint32_t page ids the items index
     uint32_t off_merges;      // MergeItem[n_merges]
-    float* partials;          // [slot][n_lay][n_head][nq_tile][head_dim + 2]
+    float* partials;          // [slot][n_lay][n_head][nq_tile][head_dim + 2] (this launch's region)
     uint32_t n_items;
     uint32_t n_merges;
     uint32_t layer0;
     uint32_t n_lay;
-    uint32_t nq_tile;         // query tile: 1..8 (vector kernel) or kMfmaTile (matrix cores)
+    uint32_t nq_tile;         // query tile: 1..8 (vector kernel), kMfmaTile (matrix cores) or kPrefillRows
     float qscale;             // log2(e) / sqrt(head_dim)
     uint32_t wide;            // 1: kWideWaves waves per workgroup (single-row items, head_dim 64)
 };

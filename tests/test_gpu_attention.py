@@ -42,11 +42,13 @@ def test_decode_contexts(gpu, oracle_lib, shape, split):
 
 
 @pytest.mark.parametrize("shape", [workloads.GPT2, dict(n_layer=2, n_head=4, head_dim=128)], ids=["hd64", "hd128"])
-@pytest.mark.parametrize("nq", [2, 5, 8, 13, 16, 20])
+@pytest.mark.parametrize("nq", [2, 5, 8, 13, 16, 17, 20, 33, 64, 65, 100, 200])
 def test_causal_groups(gpu, oracle_lib, shape, nq):
     """nq consecutive rows of one sequence (g + drafts, prefill chunks) attend
     causally and share their K/V reads; rows straddle page and partition
-    edges; groups over 16 rows split in two."""
+    edges.  Up to 16 rows run as one matrix-core group, 17..64 as one
+    prefill group (attn_prefill_kernel), longer runs as several prefill
+    groups."""
     rng = np.random.default_rng(21 + nq)
     m = Mirror(opts(shape))
     for split in (0, 64, 128):
@@ -65,17 +67,19 @@ def test_causal_groups(gpu, oracle_lib, shape, nq):
 @pytest.mark.parametrize("shape", [dict(n_layer=1, n_head=12, head_dim=64), dict(n_layer=1, n_head=4, head_dim=128)],
                          ids=["hd64", "hd128"])
 @pytest.mark.parametrize("sharp", [1.0, 8.0])
-def test_group_precision(gpu, oracle_lib, shape, sharp):
+@pytest.mark.parametrize("nq", [16, 64])
+def test_group_precision(gpu, oracle_lib, shape, sharp, nq):
     """Query groups keep f32-level accuracy on the matrix cores (q and p are
     split into f16 hi + scaled lo parts), also with sharply peaked scores
-    where most weights are tiny: max error well under the 1e-3 bound."""
+    where most weights are tiny: max error well under the 1e-3 bound.  16
+    rows run on attn_mfma_kernel, 64 on attn_prefill_kernel."""
     rng = np.random.default_rng(41)
     m = Mirror(opts(shape))
     s = m.kv.add_seq()
     L = 900
     m.fill(s, L, rng)
-    rows = [(s, p) for p in range(L - 16, L)]
-    q = (rng.standard_normal((1, 16, m.c)) * sharp).astype(np.float32)
+    rows = [(s, p) for p in range(L - nq, L)]
+    q = (rng.standard_normal((1, nq, m.c)) * sharp).astype(np.float32)
     got, want = m.attention(rows, q, split_tokens=0)
     err = float(np.abs(got - want).max())
     # The same queries one row at a time run on the vector kernel (f32
@@ -83,16 +87,16 @@ def test_group_precision(gpu, oracle_lib, shape, sharp):
     # order only, like the vector kernel does.
     qd = torch.from_numpy(q).cuda()
     single = np.concatenate([m.kv.attention(qd[:, i:i + 1].contiguous(), [rows[i]], split_tokens=0).cpu().numpy()
-                             for i in range(16)], axis=1)
+                             for i in range(nq)], axis=1)
     err1 = float(np.abs(single - want).max())
-    say(f"{shape} sharp {sharp}: group max abs err {err:.2e}, one row at a time {err1:.2e}")
+    say(f"{shape} sharp {sharp} nq {nq}: group max abs err {err:.2e}, one row at a time {err1:.2e}")
     assert_close(got, want, "group")
     assert err <= 4 * err1 + 2e-6
 
 
 def test_mixed_rows_and_long_groups(gpu, oracle_lib):
-    """Decode rows, a 5-row group and a 20-row group (split into groups of
-    at most 8) in one call, rows interleaved."""
+    """Decode rows, a 5-row group (matrix-core group kernel) and a 20-row
+    group (prefill kernel, a second launch) in one call, rows interleaved."""
     rng = np.random.default_rng(22)
     m = Mirror(opts(workloads.GPT2))
     a, b, c = m.kv.add_seq(), m.kv.add_seq(), m.kv.add_seq()
