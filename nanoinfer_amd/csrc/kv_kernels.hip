@@ -1249,13 +1249,14 @@ template <int D, int PT, int INL>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
     constexpr int QC = D / 32;              // 32-dim chunks of the QK product
     constexpr int VC = D / 16;              // 16-dim chunks of the PV product
-    constexpr int ROW = D + 8;              // LDS halves per key row (pad: conflict-free column reads)
+    constexpr int ROW = D + 8;              // K tile: LDS halves per key row (pad)
     constexpr int TK = PT * (int)kPage;     // keys per tile
+    constexpr int TKP = TK + 4;             // V tile, transposed: LDS halves per dim row (pad)
     constexpr int CH = D / 8;               // 16-byte chunks per key row
     constexpr int CPT = TK * CH / 256;      // chunks of K (and of V) per thread per tile
     static_assert(TK * CH % 256 == 0, "a tile must split evenly over the workgroup");
     __shared__ __attribute__((aligned(16))) _Float16 kt[2][TK * ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[2][TK * ROW];
+    __shared__ __attribute__((aligned(16))) _Float16 vt[2][D * TKP];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1284,10 +1285,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
     const bool qok = col < (int)nqw;
     const uint32_t qpos = it.pos0 + r0 + col;
     const uint32_t kend_w = min(it.kv_end, it.pos0 + r0 + nqw);  // keys this wave needs end here
+    // Keys below this are visible to every query of the wave (no masking).
+    const uint32_t kfull_w = min(it.kv_end, it.pos0 + r0 + 1);
 
     // Tile staging: chunk u = threadIdx.x + 256 j of a tile is key u / CH of
     // the tile (page u / CH / 16 of it, slot (u / CH) % 16), halves
-    // (u % CH) * 8 .. +7.
+    // (u % CH) * 8 .. +7.  K goes in as rows, V transposed ([dim][key]) so
+    // that a lane's 4 keys of one dim are one 8-byte read.
     u32x4 kr[CPT], vr[CPT];
     auto fetch = [&](uint32_t pg) {
 #pragma unroll
@@ -1309,7 +1313,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
             const uint32_t u = threadIdx.x + 256 * j, key = u / CH, c8 = (u % CH) * 8;
             const bool in = pg * kPage + key < it.kv_end;
             *reinterpret_cast<u32x4*>(&kt[buf][key * ROW + c8]) = in ? kr[j] : u32x4{0, 0, 0, 0};
-            *reinterpret_cast<u32x4*>(&vt[buf][key * ROW + c8]) = in ? vr[j] : u32x4{0, 0, 0, 0};
+            const half8_t vh = __builtin_bit_cast(half8_t, in ? vr[j] : u32x4{0, 0, 0, 0});
+#pragma unroll
+            for (int e = 0; e < 8; e++) vt[buf][(c8 + e) * TKP + key] = vh[e];
         }
     };
     fetch(pg_begin);
@@ -1350,43 +1356,56 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
         const int buf = ti & 1;
         const bool more = ti + 1 < n_tiles;
         if (more) fetch(pg + PT);
-#pragma unroll
-        for (int b = 0; b < PT; b++) {
-            if ((pg + b) * kPage >= kend_w) break;  // wave-uniform: past this wave's last query
-            const _Float16* kp = &kt[buf][b * kPage * ROW];
-            const _Float16* vp = &vt[buf][b * kPage * ROW];
-            // S^T = K Q^T: scores of keys 4*rg+j of the page for query col.
-            float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < QC; c++) {
-                const half8_t kh = *reinterpret_cast<const half8_t*>(kp + col * ROW + c * 32 + 8 * rg);
-                st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
-                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
-            }
-            float sc[4];
+        if (pg * kPage < kend_w) {  // wave-uniform: the tile holds keys this wave needs
+            // Pages b < nb of the tile are needed; one softmax update per tile.
+            const uint32_t nb = min((uint32_t)PT, (kend_w - pg * kPage + kPage - 1) / kPage);
+            const bool full = (pg + PT) * kPage <= kfull_w;  // every key visible to every query
+            float sc[PT][4];
             float mx = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t key = (pg + b) * kPage + 4 * rg + j;
-                const bool ok = qok && key < it.kv_end && key <= qpos;
-                sc[j] = ok ? st[j] + sl[j] * kLoUnscale : -INFINITY;
-                mx = fmaxf(mx, sc[j]);
+            for (int b = 0; b < PT; b++) {
+                // S^T = K Q^T: scores of keys 4*rg+j of page b for query col.
+                float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+                if (b < (int)nb) {
+                    const _Float16* kp = &kt[buf][b * kPage * ROW];
+#pragma unroll
+                    for (int c = 0; c < QC; c++) {
+                        const half8_t kh = *reinterpret_cast<const half8_t*>(kp + col * ROW + c * 32 + 8 * rg);
+                        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
+                        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float sv = st[j] + sl[j] * kLoUnscale;
+                    if (full) {
+                        sc[b][j] = sv;
+                    } else {
+                        const uint32_t key = (pg + b) * kPage + 4 * rg + j;
+                        const bool ok = qok && b < (int)nb && key < it.kv_end && key <= qpos;
+                        sc[b][j] = ok ? sv : -INFINITY;
+                    }
+                    mx = fmaxf(mx, sc[b][j]);
+                }
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float mn = fmaxf(m, mx);
             const float alpha = fast_exp2(m - mn);
             m = mn;
-            half4_t ph, pl;
+            half4_t ph[PT], pl[PT];
             float ps = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float p = fast_exp2(sc[j] - mn);
-                ps += p;
-                _Float16 h, l;
-                split_f16(p * kPScale, h, l);
-                ph[j] = h;
-                pl[j] = l;
+            for (int b = 0; b < PT; b++) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float p = fast_exp2(sc[b][j] - mn);
+                    ps += p;
+                    _Float16 h, l;
+                    split_f16(p * kPScale, h, l);
+                    ph[b][j] = h;
+                    pl[b][j] = l;
+                }
             }
             lsum = lsum * alpha + ps;
             // Rescale only when some query's running max moved (alpha == 1 otherwise).
@@ -1397,14 +1416,18 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
                     ol[c] *= alpha;
                 }
             }
-            // O^T += V^T P^T, 16 dims per product.
+            // O^T += V^T P^T, 16 dims per product: a lane's V^T operand is
+            // keys 4*rg .. 4*rg+3 of dim c*16 + col, one read.
 #pragma unroll
-            for (int c = 0; c < VC; c++) {
-                half4_t v4;
+            for (int b = 0; b < PT; b++) {
+                if (b >= (int)nb) break;
 #pragma unroll
-                for (int j = 0; j < 4; j++) v4[j] = vp[(4 * rg + j) * ROW + c * 16 + col];
-                o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph, o[c], 0, 0, 0);
-                ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl, ol[c], 0, 0, 0);
+                for (int c = 0; c < VC; c++) {
+                    const half4_t v4 =
+                        *reinterpret_cast<const half4_t*>(&vt[buf][(c * 16 + col) * TKP + b * kPage + 4 * rg]);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph[b], o[c], 0, 0, 0);
+                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl[b], ol[c], 0, 0, 0);
+                }
             }
         }
         if (more) stage(buf ^ 1, pg + PT);
