@@ -1244,6 +1244,14 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
 #define NI_PREFILL_PAGES 2
 #endif
 constexpr int kPrefillPages = NI_PREFILL_PAGES;  // pages per LDS tile
+// The prefill kernel keeps its exponent reference m until some query's max
+// exceeds it by more than kRefSlack (log2 units): weights are then up to
+// 2^kRefSlack, so p enters PV scaled by 2^(15 - kRefSlack) (at most 2^15 in
+// f16) -- the same ~2^-29 range below the largest weight as kPScale gives
+// attn_mfma_kernel -- and the accumulators are rescaled only when the
+// reference moves.
+constexpr float kRefSlack = 8.f;
+constexpr float kPScalePre = 128.f, kPUnscalePre = 1.f / 128.f;
 
 template <int D, int PT, int INL>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
@@ -1390,32 +1398,34 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mn = fmaxf(m, mx);
-            const float alpha = fast_exp2(m - mn);
-            m = mn;
-            half4_t ph[PT], pl[PT];
-            float ps = 0.f;
-#pragma unroll
-            for (int b = 0; b < PT; b++) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float p = fast_exp2(sc[b][j] - mn);
-                    ps += p;
-                    _Float16 h, l;
-                    split_f16(p * kPScale, h, l);
-                    ph[b][j] = h;
-                    pl[b][j] = l;
-                }
-            }
-            lsum = lsum * alpha + ps;
-            // Rescale only when some query's running max moved (alpha == 1 otherwise).
-            if (__any(alpha != 1.f)) {
+            // Move every query's reference to its running max (and rescale)
+            // only when some query's max got more than kRefSlack above it.
+            if (__any(mx > m + kRefSlack)) {
+                const float mn = fmaxf(m, mx);
+                const float alpha = fast_exp2(m - mn);
+                m = mn;
+                lsum *= alpha;
 #pragma unroll
                 for (int c = 0; c < VC; c++) {
                     o[c] *= alpha;
                     ol[c] *= alpha;
                 }
             }
+            half4_t ph[PT], pl[PT];
+            float ps = 0.f;
+#pragma unroll
+            for (int b = 0; b < PT; b++) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float p = fast_exp2(sc[b][j] - m);
+                    ps += p;
+                    _Float16 h, l;
+                    split_f16(p * kPScalePre, h, l);
+                    ph[b][j] = h;
+                    pl[b][j] = l;
+                }
+            }
+            lsum += ps;
             // O^T += V^T P^T, 16 dims per product: a lane's V^T operand is
             // keys 4*rg .. 4*rg+3 of dim c*16 + col, one read.
 #pragma unroll
@@ -1440,7 +1450,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
     const uint32_t row = it.row0 + r0 + col;
     if (it.part_slot == kNoSlot) {
         float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)row * a.out_row_stride + head * D;
-        const float scale = kPUnscale / lsum;
+        const float scale = kPUnscalePre / lsum;
 #pragma unroll
         for (int c = 0; c < VC; c++) {
             float4 y;
@@ -1459,7 +1469,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
 #pragma unroll
         for (int c = 0; c < VC; c++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * kPUnscale;
+            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * kPUnscalePre;
     }
 }
 
