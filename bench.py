@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the paged f16 decode-attention + append hot path on one MI355X.
 
-Default workload: BASELINE.json config 3, the one the target is quoted on --
+Default workload: benchmark configuration 3, the one the target is quoted on --
 a continuous-batching trace with 64 sequence slots, Poisson arrivals (seeded,
 1 request per step so the slots stay full), prompts U[32,512], outputs
 U[16,256], GPT-2 attention shape (12 layers x 12 heads x 64), f16 KV in
@@ -83,7 +83,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="config3",
-                    help="config3 (default), config2, config4, config5, or qkv[ROWS] (the QKV projection with "
+                    help="config3 (default), config2, config4, config5, configNq8 (the same on the Q8 cache), "
+                         "prefill (16 x 512-row prompts, every row queried), or qkv[ROWS] (the QKV projection with "
                          "the append in its epilogue, ROWS rows per layer, default 64)")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = automatic)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (0 = skip)")
@@ -387,11 +388,53 @@ def run_qkv(args):
     return res
 
 
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 matrix throughput, AMD's published figure
+
+
+def run_prefill(args):
+    """Prefill: 16 sequences each append a 512-row prompt from empty and
+    attend every row causally (groups of up to 64 rows on the prefill
+    kernel, after a separate append launch), rolled back each step.  The
+    roofline prices the attention launch alone: its algorithmic bytes (q
+    read, out written, each sequence's K/V read once) against HBM, with its
+    useful flops (4 per query, visible key and element of C) against the f16
+    matrix peak beside them."""
+    from nanoinfer_amd import drivers, workloads
+
+    B, P = drivers.PREFILL_SEQS, drivers.PREFILL_ROWS
+    c, L = 768, workloads.GPT2["n_layer"]
+    r = _drive("prefill", args)
+    res = _line(args, r, f"prefill: {B} sequences x {P}-row prompt from empty, every row queried (causal), GPT-2 "
+                         f"12x12x64, 16-token pages, rolled back each step",
+                {"seqs": B, "rows": P, "algorithmic_bytes_per_step": int(r["bytes"] / r["steps"]),
+                 "host_loop": "C++ driver (ni_drive_run)"},
+                "synthetic (seeded N(0,1) q/k/v resident in HBM)")
+    res["metric"] = "paged prefill attention + append, algorithmic GB/s, 1 MI355X"
+    res["attention_tflops_whole_step"] = round(r["flops"] / r["seconds"] / 1e12, 2)
+    if not args.no_profile:
+        rp = _drive("prefill", args, profile_mask=(1 << 0) | (1 << 1) | (1 << 2))
+        steps = rp["steps"]
+        attn_ms = rp["kernel_ms"][1] + rp["kernel_ms"][2]
+        append_bytes = B * P * c * 12 * L
+        attn_bytes = rp["bytes"] / steps - append_bytes
+        t = attn_ms / 1e3 / steps
+        gbs = attn_bytes / t / 1e9
+        tfl = rp["flops"] / steps / t / 1e12
+        res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_GBS, 4), "traffic": None, "kernel": "attn_prefill_kernel<64,2>",
+                           "avg_launch_us": round(t * 1e6, 3), "launches": rp["kernel_launches"][1],
+                           "algorithmic_bytes_per_launch": int(attn_bytes),
+                           "flops_per_launch": int(rp["flops"] / steps), "achieved_tflops": round(tfl, 2),
+                           "frac_of_f16_matrix_peak": round(tfl / PEAK_F16_TFLOPS, 4),
+                           "append_us": round(rp["kernel_ms"][0] / steps * 1e3, 3)}
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (see DESIGN.md for how the "
-                                   "path would shard)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the path would shard by "
+                                   "sequence, one page pool per GPU, with no exchange)"}))
         sys.exit(2)
     import torch
 
@@ -406,6 +449,8 @@ def main():
         res = run_config3(args)
     elif args.workload.startswith("qkv"):
         res = run_qkv(args)
+    elif args.workload == "prefill":
+        res = run_prefill(args)
     elif args.workload in SECONDARY:
         res = run_secondary(args)
     else:

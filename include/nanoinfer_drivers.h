@@ -95,9 +95,10 @@ int ni_spec_set_window(ni_spec* s, uint32_t window);
 enum ni_drive_workload {
     NI_DRIVE_SERVE = 0, /* ni_serve over the trace (config 3) */
     NI_DRIVE_SPEC = 1,  /* ni_spec verify rounds (config 5) */
-    /* Fixed contexts (configs 2 and 4): sequence i holds fixed_ctx[i] - 1
-     * positions; every iteration appends one row to each and attends it,
-     * then truncates back, so every iteration does the same work. */
+    /* Fixed contexts (configs 2 and 4, and prefill): sequence i holds
+     * fixed_ctx[i] - R positions (R = fixed_rows, default 1); every
+     * iteration appends R rows to each and attends all of them, then
+     * truncates back, so every iteration does the same work. */
     NI_DRIVE_FIXED = 2,
     /* The QKV projection of qkv_rows rows (d_in = C, random W and bias per
      * layer) with K/V appended, every layer per iteration: launch
@@ -130,6 +131,7 @@ typedef struct ni_drive_opts {
     float kv_std;           /* k/v data ~ N(0, kv_std^2); 0 = 1 (q is always N(0,1)) */
     uint32_t profile_mask;  /* ni_kv_profile mask over the timed iterations; 0 = none */
     uint32_t qkv_rows;      /* NI_DRIVE_QKV: rows per projection */
+    uint32_t fixed_rows;    /* NI_DRIVE_FIXED: rows appended and queried per sequence and iteration (0 = 1) */
 } ni_drive_opts;
 
 typedef struct ni_drive_result {
@@ -142,7 +144,8 @@ typedef struct ni_drive_result {
     uint64_t launches;      /* data-path ABI calls in the timed region */
     double mean_live;       /* mean queried sequences per iteration */
     double mean_context;    /* mean context of queried sequences */
-    double flops;           /* NI_DRIVE_QKV: matrix flops of the timed iterations */
+    double flops;           /* NI_DRIVE_QKV: matrix flops; NI_DRIVE_FIXED: attention flops (causal, 4 per
+                             * query, key and element of C: q.k and p.v), of the timed iterations */
     double kernel_ms[NI_K_COUNT]; /* per ni_kernel_id over the timed iterations, when profiled */
     uint64_t kernel_launches[NI_K_COUNT];
 } ni_drive_result;

@@ -537,27 +537,32 @@ int run_spec(Runner& r, ni_drive_result* res) {
 
 int run_fixed(Runner& r, ni_drive_result* res) {
     if (!r.o.fixed_ctx || r.o.fixed_n == 0) return drive_fail(NI_ERR_BAD_ARG, "fixed workload without contexts");
+    const uint32_t R = r.o.fixed_rows ? r.o.fixed_rows : 1;
     std::vector<uint32_t> seqs;
     std::vector<ni_work> work;
+    double flops = 0;
     for (uint32_t i = 0; i < r.o.fixed_n; i++) {
         const uint32_t ctx = r.o.fixed_ctx[i];
-        if (ctx == 0) return drive_fail(NI_ERR_BAD_ARG, "fixed context 0");
+        if (ctx < R) return drive_fail(NI_ERR_BAD_ARG, "fixed context %u < %u rows", ctx, R);
         uint32_t s = 0;
         if (int rc = ni_kv_add_seq(r.kv, &s)) return r.kv_fail(rc, "add_seq");
-        if (ctx > 1)
-            if (int rc = r.fill(s, ctx - 1)) return rc;
+        if (ctx > R)
+            if (int rc = r.fill(s, ctx - R)) return rc;
         seqs.push_back(s);
-        work.push_back({s, 1, 1});
+        work.push_back({s, R, R});
+        // Row j (position ctx - R + j) sees ctx - R + j + 1 keys.
+        flops += 4.0 * r.C * r.L * ((double)R * (ctx - R) + (double)R * (R + 1) / 2);
     }
     const double bytes = step_bytes(work.data(), (uint32_t)work.size(), r.o.fixed_ctx, r.L, r.C, r.kvb);
     int rc = timed_run(r, res, [&](bool timed) -> int {
         if (int e = r.launch(work.data(), (uint32_t)work.size())) return e;
         // Roll back, so the next iteration appends the same positions.
         for (uint32_t i = 0; i < r.o.fixed_n; i++)
-            if (int e = ni_kv_truncate(r.kv, seqs[i], r.o.fixed_ctx[i] - 1)) return r.kv_fail(e, "truncate");
+            if (int e = ni_kv_truncate(r.kv, seqs[i], r.o.fixed_ctx[i] - R)) return r.kv_fail(e, "truncate");
         if (timed) {
             res->bytes += bytes;
-            res->seq_tokens += r.o.fixed_n;
+            res->flops += flops;
+            res->seq_tokens += (double)r.o.fixed_n * R;
         }
         return NI_OK;
     });

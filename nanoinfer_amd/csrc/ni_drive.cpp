@@ -3,14 +3,18 @@
 // loop (`spec`) on the device, launched per step or per layer, printed as
 // one JSON line.
 //
-//   ni_drive [serve|spec|qkv] [--per-layer] [--steps K] [--warmup W] [--split T]
+//   ni_drive [serve|spec|qkv|prefill] [--per-layer] [--steps K] [--warmup W] [--split T]
 //            [--all-prompt-rows] [--seed S] [--rows N] [--q8]
+//
+// prefill: 16 sequences append and attend N-row prompts (default 512) from
+// empty, every row queried, rolled back each iteration.
 //
 // qkv: the QKV projection of N rows per layer with K/V appended in its
 // epilogue; --per-layer runs the unfused path (f32 projection + append).
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <string>
 
 #include "nanoinfer_drivers.h"
@@ -35,7 +39,7 @@ int main(int argc, char** argv) {
             }
             return argv[++i];
         };
-        if (!strcmp(a, "serve") || !strcmp(a, "spec") || !strcmp(a, "qkv")) workload = a;
+        if (!strcmp(a, "serve") || !strcmp(a, "spec") || !strcmp(a, "qkv") || !strcmp(a, "prefill")) workload = a;
         else if (!strcmp(a, "--rows")) o.qkv_rows = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--q8")) q8 = true;
         else if (!strcmp(a, "--per-layer")) o.launch = NI_DRIVE_PER_LAYER;
@@ -45,7 +49,7 @@ int main(int argc, char** argv) {
         else if (!strcmp(a, "--split")) o.split_tokens = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--seed")) o.data_seed = o.serve.seed = strtoull(val(a), nullptr, 10);
         else {
-            fprintf(stderr, "usage: ni_drive [serve|spec|qkv] [--per-layer] [--steps K] [--warmup W] [--split T] "
+            fprintf(stderr, "usage: ni_drive [serve|spec|qkv|prefill] [--per-layer] [--steps K] [--warmup W] [--split T] "
                             "[--all-prompt-rows] [--seed S] [--rows N] [--q8]\n");
             return 2;
         }
@@ -60,6 +64,19 @@ int main(int argc, char** argv) {
         o.kv.max_seqs = o.serve.max_batch;
         o.kv.max_ctx = 1024;
         o.kv.max_rows = o.serve.max_rows;
+    } else if (workload == "prefill") {
+        static uint32_t ctx[16];
+        const uint32_t P = o.qkv_rows ? o.qkv_rows : 512;
+        for (uint32_t& c : ctx) c = P;
+        o.qkv_rows = 0;
+        o.workload = NI_DRIVE_FIXED;
+        o.fixed_ctx = ctx;
+        o.fixed_n = 16;
+        o.fixed_rows = P;
+        o.kv.kv_pages = 16 * pages(P) + 8;
+        o.kv.max_seqs = 16;
+        o.kv.max_ctx = std::max<uint32_t>(1024, P);
+        o.kv.max_rows = 16 * P;
     } else if (workload == "qkv") {
         o.workload = NI_DRIVE_QKV;
         if (o.qkv_rows == 0) o.qkv_rows = 64;
@@ -90,6 +107,9 @@ int main(int argc, char** argv) {
     if (workload == "qkv")
         fprintf(stderr, "ni_drive: qkv %u rows: %.2f TFLOP/s, %.3f ms per iteration (12 layers)\n", o.qkv_rows,
                 r.flops / r.seconds / 1e12, r.seconds / r.steps * 1e3);
+    if (workload == "prefill")
+        fprintf(stderr, "ni_drive: prefill 16 x %u rows: %.2f attention TFLOP/s over the whole step, %.3f ms per step\n",
+                o.fixed_rows, r.flops / r.seconds / 1e12, r.seconds / r.steps * 1e3);
     printf("{\"driver\": \"ni_drive\", \"workload\": \"%s\", \"launch\": \"%s\", \"steps\": %u, \"warmup\": %u, "
            "\"value\": %.2f, \"unit\": \"GB/s\", \"pct_of_peak\": %.2f, \"ms_per_step\": %.5f, "
            "\"gpu_ms_per_step\": %.5f, \"host_us_per_step\": %.1f, \"abi_calls_per_step\": %.1f, "

@@ -38,7 +38,8 @@ class ni_drive_opts(C.Structure):
                 ("spec_seqs", _u32), ("spec_ctx_min", _u32), ("spec_ctx_max", _u32), ("spec_k", _u32),
                 ("spec_seed", C.c_uint64), ("spec_window", _u32), ("warmup", _u32), ("steps", _u32),
                 ("split_tokens", _u32), ("data_seed", C.c_uint64), ("fixed_ctx", C.POINTER(_u32)),
-                ("fixed_n", _u32), ("kv_std", C.c_float), ("profile_mask", _u32), ("qkv_rows", _u32)]
+                ("fixed_n", _u32), ("kv_std", C.c_float), ("profile_mask", _u32), ("qkv_rows", _u32),
+                ("fixed_rows", _u32)]
 
 
 class ni_drive_result(C.Structure):
@@ -185,9 +186,12 @@ def _kv(o, shape, kv_pages, max_seqs, max_ctx, max_rows, order=None):
         o.kv.page_order = arr.ctypes.data_as(C.POINTER(_u32))
 
 
+PREFILL_SEQS, PREFILL_ROWS = 16, 512
+
+
 def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, split: int = 0, seed: int = 7,
            profile_mask: int = 0, query_all_prompt_rows: bool = False) -> ni_drive_opts:
-    """ni_drive_opts of config 2, 3, 4 or 5."""
+    """ni_drive_opts of benchmark configuration 2, 3, 4 or 5, the QKV projection (qkvN) or the prefill workload."""
     from . import workloads
 
     o = ni_drive_opts()
@@ -223,6 +227,15 @@ def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, spli
         o.kv_std = 0.5
         o.split_tokens = split or 512
         _kv(o, workloads.LONG, B * L // 16, B, L, 4096, workloads.XorShift.seeded(4).permutation(B * L // 16))
+    elif name == "prefill":
+        # Prefill (every row of a prompt queried): 16 sequences each
+        # append and query a 512-row prompt from empty, rolled back each step.
+        B, P = PREFILL_SEQS, PREFILL_ROWS
+        o.workload = NI_DRIVE_FIXED
+        arr = np.full(B, P, np.uint32)
+        o._keep.append(arr)
+        o.fixed_ctx, o.fixed_n, o.fixed_rows = arr.ctypes.data_as(C.POINTER(_u32)), B, P
+        _kv(o, workloads.GPT2, B * workloads.pages(P) + 8, B, 1024, B * P)
     elif name.startswith("qkv"):
         # qkv<rows>: the projection of <rows> rows per layer, GPT-2 shape
         o.workload = NI_DRIVE_QKV

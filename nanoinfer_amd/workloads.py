@@ -228,7 +228,7 @@ def normal(seed: int, shape, std: float = 1.0) -> np.ndarray:
     return (np.random.default_rng(seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 
 
-# Shapes of the configurations (BASELINE.json "configs").
+# Shapes of the benchmark configurations.
 GPT2 = dict(n_layer=12, n_head=12, head_dim=64)
 LONG = dict(n_layer=1, n_head=32, head_dim=128)
 

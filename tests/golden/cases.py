@@ -215,7 +215,7 @@ CONFIG1 = dict(seed=1, prefill=64, decode=64)
 
 
 def config1(make) -> dict:
-    """one sequence, prefill 64 positions (all queried,
+    """Benchmark configuration 1: one sequence, prefill 64 positions (all queried,
     causal), then 64 decode steps of one row each; qkv f32 N(0,1) from seed 1
     drawn as [layer][rows][3C] per step (the reference's fused QKV rows)."""
     shape = workloads.GPT2
@@ -235,7 +235,7 @@ def config1(make) -> dict:
 
 
 def config2(make) -> dict:
-    """16 sequences, context U[64,1024] after the step
+    """Benchmark configuration 2: 16 sequences, context U[64,1024] after the step
     (XorShift seed 2), pages from a seeded permutation of a 1024-page pool;
     fill ctx-1 positions per sequence, then one step appending one row per
     sequence and querying it.  k/v/q f32 N(0,1), seed 2."""

@@ -54,6 +54,23 @@ def test_drive_launch_modes_agree(gpu, workload):
     assert a["launches"] == 60 and b["launches"] >= 12 * 60
 
 
+def test_drive_prefill_accounting(gpu):
+    """The prefill preset (fixed contexts with every appended row queried):
+    both launch paths run, and bytes, flops and tokens per step follow the
+    closed forms of the workload."""
+    B, P, c, L = drivers.PREFILL_SEQS, drivers.PREFILL_ROWS, 768, 12
+    want_bytes = L * B * (P * c * 12 + P * c * 8 + 2 * P * c * 2 + (P + 15) // 16 * 4)
+    want_flops = 4.0 * c * L * B * P * (P + 1) / 2
+    for launch in (drivers.NI_DRIVE_STEP, drivers.NI_DRIVE_PER_LAYER):
+        say(f"ni_drive_run prefill launch {launch}")
+        r = drivers.drive(drivers.preset("prefill", 4, 1, launch=launch))
+        say(f"  {r['seconds'] / r['steps'] * 1e6:.1f} us/step")
+        assert r["steps"] == 4
+        assert r["bytes"] == 4 * want_bytes
+        assert r["flops"] == pytest.approx(4 * want_flops, rel=1e-12)
+        assert r["seq_tokens"] == 4 * B * P
+
+
 def test_per_layer_launches_match_step(gpu):
     """A config-3 trace through both ABI paths on twin handles."""
     opts = na.BatchOpts(**workloads.GPT2, kv_blocks=3080, max_seqs=64, n_ctx=1024, max_rows=512)
