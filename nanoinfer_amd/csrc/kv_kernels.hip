@@ -1080,6 +1080,12 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
 #pragma unroll
     for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    // Q8: p enters PV as p * vs / vref (at most kPScale after scaling, so its
+    // f16 hi never overflows) and the accumulators hold the sum in units of
+    // vref: vref starts at 1 (scales up to 1, values up to 127 in magnitude,
+    // leave it there, and the products match p * vs * kPScale bit for bit)
+    // and follows the largest scale seen beyond that.
+    float vref = 1.f, vsc = kPScale;  // vsc = kPScale / vref
     _Float16* my_vt = vt[wave];
     const uint32_t qpos = it.pos0 + col;  // this lane's query position
     const bool qok = col < (int)it.nq;
@@ -1138,7 +1144,35 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float mn = fmaxf(m, mx);
         const float alpha = fast_exp2(m - mn);
+        float oalpha = alpha;  // the accumulators' factor
         m = mn;
+        if constexpr (Q8) {
+            // Past the reference vref, move it to the tile's largest value
+            // scale (a scale belongs to its key, so the same for every lane
+            // once reduced over the lane rows) and shrink the accumulators
+            // with it. Scales past kv_end are stale: only the item's last
+            // tile masks them.
+            float vm = 0.f;
+            if ((pg + PB) * kPage <= it.kv_end) {
+#pragma unroll
+                for (int b = 0; b < PB; b++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) vm = fmaxf(vm, cur.vs[b][j]);
+            } else {
+#pragma unroll
+                for (int b = 0; b < PB; b++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if ((pg + b) * kPage + 4 * rg + j < it.kv_end) vm = fmaxf(vm, cur.vs[b][j]);
+            }
+            if (__any(vm > vref)) {
+                vm = fmaxf(vm, __shfl_xor(vm, 16));
+                vm = fmaxf(vm, __shfl_xor(vm, 32));
+                oalpha *= vref / vm;
+                vref = vm;
+                vsc = kPScale / vm;
+            }
+        }
         half4_t ph[PB], pl[PB];
         float ps = 0.f;
 #pragma unroll
@@ -1149,7 +1183,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 ps += p;
                 _Float16 h, l;
                 if constexpr (Q8)
-                    split_f16(p * cur.vs[b][j] * kPScale, h, l);
+                    split_f16(p * cur.vs[b][j] * vsc, h, l);
                 else
                     split_f16(p * kPScale, h, l);
                 ph[b][j] = h;
@@ -1160,13 +1194,14 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // Rescale only when some query's running max moved: otherwise every
-        // alpha is exactly 1 and the multiplies change nothing.
-        if (__any(alpha != 1.f)) {
+        // Rescale only when some query's running max (or, Q8, the value
+        // scale reference) moved: otherwise every alpha is exactly 1 and the
+        // multiplies change nothing.
+        if (__any(oalpha != 1.f)) {
 #pragma unroll
             for (int c = 0; c < VC; c++) {
-                o[c] *= alpha;
-                ol[c] *= alpha;
+                o[c] *= oalpha;
+                ol[c] *= oalpha;
             }
         }
         // O^T += V^T P^T, 16 dims per product.
@@ -1198,7 +1233,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         for (int c = 0; c < VC; c++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                red[wave][col][2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * kPUnscale;
+                red[wave][col][2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * (kPUnscale * vref);
     }
     __syncthreads();
     for (uint32_t t = threadIdx.x; t < it.nq * D; t += 64 * W) {

@@ -41,7 +41,7 @@ class MirrorQ8:
         for l in range(self.opts.n_layer):
             oracle.paged_q8_append(self.pools, l, t, self.kv.max_blocks, rows[:, 0], rows[:, 1], k[l], v[l])
 
-    def fill(self, seq, length, rng, chunk=256):
+    def fill(self, seq, length, rng, chunk=256, vstd=1.0):
         start = self.kv.seq_len(seq)
         self.kv.reserve(seq, length)
         for p0 in range(start, length, chunk):
@@ -49,7 +49,7 @@ class MirrorQ8:
             rows = [(seq, p) for p in range(p0, p1)]
             shape = (self.opts.n_layer, p1 - p0, self.c)
             k = rng.standard_normal(shape, dtype=np.float32)
-            v = rng.standard_normal(shape, dtype=np.float32)
+            v = (rng.standard_normal(shape, dtype=np.float32) * np.float32(vstd)).astype(np.float32)
             self.kv.append(rows, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
             self.append_oracle(rows, k, v)
         self.kv.commit(seq, length - start)
@@ -133,6 +133,24 @@ def test_q8_causal_groups(gpu, oracle_lib, nq):
             got = m.kv.attention(torch.from_numpy(q).cuda(), rows, split_tokens=split).cpu().numpy()
             assert_close(got, m.attention_oracle(rows, q), f"q8 nq {nq} L {L} split {split}")
             m.kv.free_seq(s)
+
+
+@pytest.mark.parametrize("nq", [1, 5, 16])
+def test_q8_large_values(gpu, oracle_lib, nq):
+    """Value scales far above 1 (|v| in the thousands) after a prefix of
+    ordinary values: on the matrix cores p * scale would overflow f16 without
+    the value-scale reference, which here must also move in mid-stream."""
+    rng = np.random.default_rng(95 + nq)
+    m = MirrorQ8(opts(workloads.GPT2, n_layer=2))
+    s = m.kv.add_seq()
+    m.fill(s, 300, rng)
+    m.fill(s, 600, rng, vstd=3000.0)
+    rows = [(s, p) for p in range(600 - nq, 600)]
+    q = rng.standard_normal((2, nq, m.c)).astype(np.float32)
+    for split in (0, 128):
+        got = m.kv.attention(torch.from_numpy(q).cuda(), rows, split_tokens=split).cpu().numpy()
+        err = assert_close(got, m.attention_oracle(rows, q), f"q8 large values nq {nq} split {split}")
+        say(f"q8 large values nq {nq} split {split}: max abs err {err:.3e}")
 
 
 def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib):
