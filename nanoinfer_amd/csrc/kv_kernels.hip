@@ -903,6 +903,7 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Four signed int8 values (bytes 0..3 of w) as f16, exactly and bit for bit
 // as static_cast<_Float16>: the f16 bit pattern 0x6400 | (b ^ 0x80) is 1024 +
@@ -922,13 +923,48 @@ __device__ __forceinline__ half4_t i8x4_f16(uint32_t w) {
 // f32 -> f16 hi plus the residual scaled by 2^11 (kept in the normal range
 // of f16, where the residual itself would often be subnormal): x ~= hi +
 // lo * 2^-11 to ~2^-22 relative.  Products of hi and of lo are accumulated
-// separately on the matrix cores and combined in f32.
+// separately on the matrix cores and combined in f32.  gfx950's f16 matrix
+// products take subnormal operands exactly (both operands, 16x16x16 and
+// 16x16x32, down to 2^-24), so a subnormal hi needs no special case.
 constexpr float kLoScale = 2048.f, kLoUnscale = 1.f / 2048.f;
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
-    // A hi below the normal range would be flushed by the matrix cores; the
-    // whole value then goes to lo.
-    hi = static_cast<_Float16>(fabsf(x) < 6.103515625e-05f ? 0.f : x);
+    // x as one f32 register: otherwise the compiler may fold the caller's
+    // product into the conversions (a mixed-precision FMA rounding the exact
+    // product to f16 once) for one use of hi and not the other, and the two
+    // disagree by an f16 ulp in double-rounding cases (q off by 2^-10).
+    asm("" : "+v"(x));
+    hi = static_cast<_Float16>(x);
     lo = static_cast<_Float16>((x - static_cast<float>(hi)) * kLoScale);
+}
+// The same split for two softmax weights already scaled up (x in [0,
+// 2^15]), packed: hi = f16(x), lo = f16(x - hi) unscaled, ~2^-22 relative
+// where lo is normal and within 2^-25 absolute where it is subnormal.  One
+// packed convert and one mixed-precision FMA per weight (x * 1 - hi, hi
+// read as the f16 half of the packed register) instead of convert, convert
+// back, subtract and convert; the same bits (checked on gfx950 against the
+// plain formula over 2^21 pairs from 2^-40 to 2^16, zeros included).
+__device__ __forceinline__ void split_w16x2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    const half2_t h = {static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
+    hi = __builtin_bit_cast(uint32_t, h);
+    asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(lo) : "v"(x0), "v"(hi));
+    asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(lo) : "v"(x1), "v"(hi));
+}
+// Max and sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lanes holding
+// one query column of an MFMA 16x16 output): v_permlane16_swap and
+// v_permlane32_swap of a value with itself leave the two halves of each
+// lane pair in the two results, so combining them is the pair's max or sum
+// in both lanes.  No LDS round trip; the same bits as __shfl_xor.
+__device__ __forceinline__ float rows4_max(float v) {
+    u32x2_t s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+    u32x2_t s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 // p in [0, 1] enters PV scaled by 2^14 so that p down to ~4e-9 is a normal f16.
 constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
@@ -1268,38 +1304,71 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
 // 16w .. 16w+15 of the group and runs attn_mfma_kernel's per-page arithmetic
 // for them (S^T = K Q^T with q split into f16 hi + scaled lo, the online
 // softmax on S^T's columns, O^T += V^T P^T with p split likewise), but the
-// workgroup's 256 threads load each tile of PT pages of K and V once into LDS
-// (double buffered, one barrier per tile) and all four waves read it there:
-// each K/V byte leaves memory once per 64 queries instead of once per 16.
-// Keys past the item's end are zeroed in LDS (stale halves, possibly NaN bit
-// patterns, never reach a product); a wave skips pages past its own last
-// query.  No cross-wave merge: each wave writes its own rows (or their
-// partials when the group is split into partitions).
+// workgroup's 256 threads copy each tile of PT pages of K and V once into LDS
+// and all four waves read it there: each K/V byte leaves memory once per 64
+// queries instead of once per 16.  Tiles travel by DMA
+// (global_load_lds_dwordx4: lane l's 16 bytes land at the wave's LDS base +
+// 16 l, whatever address the lane loads) through a ring of kPrefillStages
+// tiles: two tiles in flight while one is computed, one barrier per tile, no
+// registers held for them.  Rows past the item's end load the item's first
+// key instead (finite data; their weights are 0), and a wave skips pages
+// past its own last query.  No cross-wave merge: each wave writes its own
+// rows (or their partials when the group is split into partitions).
 #ifndef NI_PREFILL_PAGES
 #define NI_PREFILL_PAGES 2
 #endif
 constexpr int kPrefillPages = NI_PREFILL_PAGES;  // pages per LDS tile
+#ifndef NI_PREFILL_STAGES
+#define NI_PREFILL_STAGES 3
+#endif
+#ifndef NI_PREFILL_MIN_WAVES
+#define NI_PREFILL_MIN_WAVES 1
+#endif
+constexpr int kPrefillStages = NI_PREFILL_STAGES;  // LDS tiles in the ring (3 or 4)
+static_assert(kPrefillStages == 3 || kPrefillStages == 4, "ring of 3 or 4 tiles");
+
+// Position, in 16-byte chunks, of chunk q of row `key` in an LDS tile of
+// CH-chunk rows: row major, the chunk index XORed with a permutation of the
+// row's 256-byte window index, so that the 16 lanes reading one chunk of 16
+// consecutive rows (the K operand) and the 32 lanes reading 4 dims of 8 rows
+// for the transposed V operand each hit distinct banks.
+template <int CH>
+__device__ __forceinline__ uint32_t tile_chunk(uint32_t key, uint32_t q) {
+    const uint32_t i = (key * CH / 16) % CH;
+    const uint32_t sw = ((i & (CH / 2 - 1)) << 1) | (i / (CH / 2));
+    return key * CH + (q ^ sw);
+}
+typedef __fp16 v4fp16_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+#define NI_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// 16 bytes per lane from g to LDS at the wave-uniform dst + 16 * lane
+// (global_load_lds_dwordx4, M0 = dst's LDS address).  Written as assembly
+// so that the compiler does not add a wait for every DMA in flight before
+// each LDS read it cannot prove disjoint from them: the caller waits
+// (vmcnt) and synchronises itself.  The "memory" clobber and dst as an
+// operand tell the compiler that LDS may change here.
+__device__ __forceinline__ void lds_dma16(const void* g, void* dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)NI_LDS(dst));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(m0) : "memory", "m0");
+}
 // The prefill kernel keeps its exponent reference m until some query's max
 // exceeds it by more than kRefSlack (log2 units): weights are then up to
 // 2^kRefSlack, so p enters PV scaled by 2^(15 - kRefSlack) (at most 2^15 in
-// f16) -- the same ~2^-29 range below the largest weight as kPScale gives
-// attn_mfma_kernel -- and the accumulators are rescaled only when the
-// reference moves.
+// f16; weights down to 2^-31 of the reference stay nonzero as f16
+// subnormals, which the matrix cores take exactly), and the accumulators
+// are rescaled only when the reference moves.
 constexpr float kRefSlack = 8.f;
-constexpr float kPScalePre = 128.f, kPUnscalePre = 1.f / 128.f;
+constexpr float kLog2PScalePre = 7.f, kPUnscalePre = 1.f / 128.f;
 
 template <int D, int PT, int INL>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+__global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_prefill_kernel(const AttnLaunch a,
+                                                                                             const PlanArg<INL> pa) {
     constexpr int QC = D / 32;              // 32-dim chunks of the QK product
     constexpr int VC = D / 16;              // 16-dim chunks of the PV product
-    constexpr int ROW = D + 8;              // K tile: LDS halves per key row (pad)
     constexpr int TK = PT * (int)kPage;     // keys per tile
-    constexpr int TKP = TK + 4;             // V tile, transposed: LDS halves per dim row (pad)
     constexpr int CH = D / 8;               // 16-byte chunks per key row
-    constexpr int CPT = TK * CH / 256;      // chunks of K (and of V) per thread per tile
-    static_assert(TK * CH % 256 == 0, "a tile must split evenly over the workgroup");
-    __shared__ __attribute__((aligned(16))) _Float16 kt[2][TK * ROW];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[2][D * TKP];
+    constexpr int TH = TK * D;              // halves per K (or V) tile
+    static_assert(TK * CH == 256, "one chunk of K and one of V per thread per tile");
+    __shared__ __attribute__((aligned(16))) _Float16 ring[kPrefillStages][2][TH];  // [stage][K, V]
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1318,7 +1387,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
     const uint16_t* kbase = a.pool.k + layer_off;
     const uint16_t* vbase = a.pool.v + layer_off;
     const uint64_t page_stride = a.pool.page_halves;
-    const uint32_t* __restrict__ tab = reinterpret_cast<const uint32_t*>(plan + a.off_table) + it.tab;
+    // Page ids through the constant address space: wave-uniform scalar loads,
+    // which a wait for the DMA tiles (in order with every vector load) does
+    // not depend on.
+    const __attribute__((address_space(4))) uint32_t* tab =
+        (const __attribute__((address_space(4))) uint32_t*)(plan + a.off_table) + it.tab;
     const uint32_t pg_begin = it.kv_begin / kPage;
     const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
 
@@ -1331,37 +1404,38 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
     // Keys below this are visible to every query of the wave (no masking).
     const uint32_t kfull_w = min(it.kv_end, it.pos0 + r0 + 1);
 
-    // Tile staging: chunk u = threadIdx.x + 256 j of a tile is key u / CH of
-    // the tile (page u / CH / 16 of it, slot (u / CH) % 16), halves
-    // (u % CH) * 8 .. +7.  K goes in as rows, V transposed ([dim][key]) so
-    // that a lane's 4 keys of one dim are one 8-byte read.
-    u32x4 kr[CPT], vr[CPT];
-    auto fetch = [&](uint32_t pg) {
+    // Tile DMA: thread t copies LDS chunk t of each tile (K and V): row
+    // t / CH, logical chunk (t % CH) ^ sw -- tile_chunk's inverse.  Every
+    // wave issues exactly two DMA loads per tile, so "tile i landed" is
+    // "at most the next tile's two loads outstanding".
+    const uint32_t dkey = threadIdx.x / CH;
+    const uint32_t dq = threadIdx.x % CH ^ (tile_chunk<CH>(dkey, 0) - dkey * CH);
+    const uint32_t dpage = dkey / kPage;                      // page of the tile
+    const uint32_t doff = (dkey % kPage) * D + dq * 8;        // halves into the page
+    _Float16* const kdst0 = &ring[0][0][0] + wave * 512;  // this wave's 1 KB of a tile
+    auto issue = [&](int st, uint32_t pg) {
+        // Page bases are wave-uniform (scalar); a row past the end reads
+        // page pg's first row, a key of this item.
+        const uint16_t* kp = kbase + (uint64_t)tab[pg] * page_stride;
+        const uint16_t* vp = vbase + (uint64_t)tab[pg] * page_stride;
+        const bool in = pg * kPage + dkey < it.kv_end;
 #pragma unroll
-        for (int j = 0; j < CPT; j++) {
-            const uint32_t u = threadIdx.x + 256 * j, key = u / CH, c8 = (u % CH) * 8;
-            const uint32_t p = pg + key / kPage;
-            if (p < pg_end) {
-                const uint64_t off = (uint64_t)tab[p] * page_stride + (key % kPage) * D + c8;
-                kr[j] = load16(reinterpret_cast<const u32x4*>(kbase + off));
-                vr[j] = load16(reinterpret_cast<const u32x4*>(vbase + off));
-            } else {
-                kr[j] = vr[j] = u32x4{0, 0, 0, 0};
+        for (int b = 1; b < PT; b++) {
+            const uint64_t base = (uint64_t)tab[min(pg + b, pg_end - 1)] * page_stride;
+            if (in && dpage == (uint32_t)b) {
+                kp = kbase + base;
+                vp = vbase + base;
             }
         }
+        const uint32_t off = in ? doff : dq * 8;
+        _Float16* const kdst = kdst0 + st * (2 * TH);
+        lds_dma16(kp + off, kdst);
+        lds_dma16(vp + off, kdst + TH);
     };
-    auto stage = [&](int buf, uint32_t pg) {
+    const uint32_t n_tiles = (pg_end - pg_begin + PT - 1) / PT;
 #pragma unroll
-        for (int j = 0; j < CPT; j++) {
-            const uint32_t u = threadIdx.x + 256 * j, key = u / CH, c8 = (u % CH) * 8;
-            const bool in = pg * kPage + key < it.kv_end;
-            *reinterpret_cast<u32x4*>(&kt[buf][key * ROW + c8]) = in ? kr[j] : u32x4{0, 0, 0, 0};
-            const half8_t vh = __builtin_bit_cast(half8_t, in ? vr[j] : u32x4{0, 0, 0, 0});
-#pragma unroll
-            for (int e = 0; e < 8; e++) vt[buf][(c8 + e) * TKP + key] = vh[e];
-        }
-    };
-    fetch(pg_begin);
+    for (int t = 0; t < kPrefillStages - 1; t++)
+        if ((uint32_t)t < n_tiles) issue(t, pg_begin + t * PT);
 
     // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo.
     half8_t qh[QC], ql[QC];
@@ -1386,59 +1460,76 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
             }
         }
     }
-    float m = kMinScore, lsum = 0.f;
+    // Weights are exp2(s - mref) with mref = m - kLog2PScalePre: p already
+    // scaled by 2^7, and lsum and the accumulators in the same units.
+    float m = kMinScore, mref = kMinScore - kLog2PScalePre, lsum = 0.f;
     float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
 #pragma unroll
     for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    stage(0, pg_begin);
-    __syncthreads();
-    const uint32_t n_tiles = (pg_end - pg_begin + PT - 1) / PT;
+    int st = 0;  // ring stage of tile ti
     for (uint32_t ti = 0; ti < n_tiles; ti++) {
         const uint32_t pg = pg_begin + ti * PT;
-        const int buf = ti & 1;
-        const bool more = ti + 1 < n_tiles;
-        if (more) fetch(pg + PT);
+        // This wave's part of tile ti has landed (vmcnt is in order: only
+        // the two loads of each later tile already issued may still be
+        // outstanding); after the barrier every wave's part has, and every
+        // wave is done with tile ti-1, whose stage the next tile takes.
+        const uint32_t ahead = min(n_tiles - 1 - ti, (uint32_t)(kPrefillStages - 2));
+        if (ahead >= 2)
+            __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+        else if (ahead == 1)
+            __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+        else
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        __syncthreads();
+        if (ti + kPrefillStages - 1 < n_tiles)
+            issue(st == 0 ? kPrefillStages - 1 : st - 1, pg + (kPrefillStages - 1) * PT);
+        const _Float16* const kt = &ring[st][0][0];
+        const _Float16* const vt = &ring[st][1][0];
         if (pg * kPage < kend_w) {  // wave-uniform: the tile holds keys this wave needs
             // Pages b < nb of the tile are needed; one softmax update per tile.
             const uint32_t nb = min((uint32_t)PT, (kend_w - pg * kPage + kPage - 1) / kPage);
             const bool full = (pg + PT) * kPage <= kfull_w;  // every key visible to every query
             float sc[PT][4];
-            float mx = -INFINITY;
 #pragma unroll
             for (int b = 0; b < PT; b++) {
-                // S^T = K Q^T: scores of keys 4*rg+j of page b for query col.
+                // S^T = K Q^T: scores of keys 4*rg+j of page b for query col
+                // (also of a page past nb: its rows are finite, its scores
+                // masked below).
                 float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
-                if (b < (int)nb) {
-                    const _Float16* kp = &kt[buf][b * kPage * ROW];
 #pragma unroll
-                    for (int c = 0; c < QC; c++) {
-                        const half8_t kh = *reinterpret_cast<const half8_t*>(kp + col * ROW + c * 32 + 8 * rg);
-                        st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
-                        sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
-                    }
+                for (int c = 0; c < QC; c++) {
+                    const half8_t kh =
+                        *reinterpret_cast<const half8_t*>(kt + tile_chunk<CH>(b * kPage + col, 4 * c + rg) * 8);
+                    st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
+                    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
                 }
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float sv = st[j] + sl[j] * kLoUnscale;
-                    if (full) {
-                        sc[b][j] = sv;
-                    } else {
+                for (int j = 0; j < 4; j++) sc[b][j] = st[j] + sl[j] * kLoUnscale;
+            }
+            if (!full) {
+#pragma unroll
+                for (int b = 0; b < PT; b++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
                         const uint32_t key = (pg + b) * kPage + 4 * rg + j;
                         const bool ok = qok && b < (int)nb && key < it.kv_end && key <= qpos;
-                        sc[b][j] = ok ? sv : -INFINITY;
+                        sc[b][j] = ok ? sc[b][j] : -INFINITY;
                     }
-                    mx = fmaxf(mx, sc[b][j]);
-                }
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            float mx = sc[0][0];
+#pragma unroll
+            for (int b = 0; b < PT; b++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) mx = fmaxf(mx, sc[b][j]);
+            mx = rows4_max(mx);
             // Move every query's reference to its running max (and rescale)
             // only when some query's max got more than kRefSlack above it.
             if (__any(mx > m + kRefSlack)) {
                 const float mn = fmaxf(m, mx);
                 const float alpha = fast_exp2(m - mn);
                 m = mn;
+                mref = mn - kLog2PScalePre;
                 lsum *= alpha;
 #pragma unroll
                 for (int c = 0; c < VC; c++) {
@@ -1447,64 +1538,93 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a, c
                 }
             }
             half4_t ph[PT], pl[PT];
-            float ps = 0.f;
+            float ps[PT];
 #pragma unroll
             for (int b = 0; b < PT; b++) {
+                float p[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float p = fast_exp2(sc[b][j] - m);
-                    ps += p;
-                    _Float16 h, l;
-                    split_f16(p * kPScalePre, h, l);
-                    ph[b][j] = h;
-                    pl[b][j] = l;
-                }
+                for (int j = 0; j < 4; j++) p[j] = fast_exp2(sc[b][j] - mref);
+                ps[b] = (p[0] + p[1]) + (p[2] + p[3]);
+                uint32_t h0, l0, h1, l1;
+                split_w16x2(p[0], p[1], h0, l0);
+                split_w16x2(p[2], p[3], h1, l1);
+                ph[b] = __builtin_bit_cast(half4_t, u32x2_t{h0, h1});
+                pl[b] = __builtin_bit_cast(half4_t, u32x2_t{l0, l1});
             }
-            lsum += ps;
-            // O^T += V^T P^T, 16 dims per product: a lane's V^T operand is
-            // keys 4*rg .. 4*rg+3 of dim c*16 + col, one read.
 #pragma unroll
-            for (int b = 0; b < PT; b++) {
-                if (b >= (int)nb) break;
+            for (int b = 0; b < PT; b++) lsum += ps[b];
+            // O^T += V^T P^T, 16 dims per product.  A lane's V^T operand,
+            // keys 4*rg .. 4*rg+3 of dim c*16 + col of a page, comes from
+            // the row-major tile by a transposing read
+            // (ds_read_b64_tr_b16: within 16 lanes, lane 4t+a reads dims
+            // c*16 + 4a .. +3 of key 4*rg + t and lane 4a'+b' receives
+            // element b' of lanes a', 4+a', 8+a', 12+a', i.e. dim c*16 +
+            // 4a'+b' of keys 4*rg .. 4*rg+3).  Pages go in pairs through the
+            // 32-key product (nearly twice the work per issue of the 16-key
+            // one): k-slot 8*rg + 4*i + j of the pair is key 4*rg + j of its
+            // page i, in both operands.
+            const int vt_t = (lane >> 2) & 3, vt_a = lane & 3;
+            auto vread = [&](int b, int c) {
+                const _Float16* vp =
+                    vt + tile_chunk<CH>(b * kPage + 4 * rg + vt_t, 2 * c + (vt_a >> 1)) * 8 + (vt_a & 1) * 4;
+                const v4fp16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (__attribute__((address_space(3))) v4fp16_t*)(vp));
+                return __builtin_bit_cast(half4_t, r);
+            };
+            if constexpr (PT % 2 == 0) {
 #pragma unroll
-                for (int c = 0; c < VC; c++) {
-                    const half4_t v4 =
-                        *reinterpret_cast<const half4_t*>(&vt[buf][(c * 16 + col) * TKP + b * kPage + 4 * rg]);
-                    o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph[b], o[c], 0, 0, 0);
-                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl[b], ol[c], 0, 0, 0);
+                for (int b = 0; b < PT; b += 2) {
+                    if (b >= (int)nb) break;  // a page past nb has p = 0 and finite V
+                    const half8_t p8h = __builtin_shufflevector(ph[b], ph[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+                    const half8_t p8l = __builtin_shufflevector(pl[b], pl[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                    for (int c = 0; c < VC; c++) {
+                        const half8_t v8 = __builtin_shufflevector(vread(b, c), vread(b + 1, c), 0, 1, 2, 3, 4, 5, 6, 7);
+                        o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8h, o[c], 0, 0, 0);
+                        ol[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, ol[c], 0, 0, 0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int b = 0; b < PT; b++) {
+                    if (b >= (int)nb) break;
+#pragma unroll
+                    for (int c = 0; c < VC; c++) {
+                        const half4_t v4 = vread(b, c);
+                        o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph[b], o[c], 0, 0, 0);
+                        ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl[b], ol[c], 0, 0, 0);
+                    }
                 }
             }
         }
-        if (more) stage(buf ^ 1, pg + PT);
-        __syncthreads();  // the next tile is staged; nobody reads this one any more
+        st = st == kPrefillStages - 1 ? 0 : st + 1;
     }
     // Lanes q, q+16, q+32, q+48 hold partial sums of query q's softmax.
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
+    lsum = rows4_sum(lsum);
     if (!qok) return;
     const uint32_t row = it.row0 + r0 + col;
     if (it.part_slot == kNoSlot) {
         float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)row * a.out_row_stride + head * D;
-        const float scale = kPUnscalePre / lsum;
+        const float scale = 1.f / lsum;  // lsum and o both carry the 2^7
 #pragma unroll
         for (int c = 0; c < VC; c++) {
             float4 y;
-            y.x = (o[c][0] + ol[c][0] * kLoUnscale) * scale;
-            y.y = (o[c][1] + ol[c][1] * kLoUnscale) * scale;
-            y.z = (o[c][2] + ol[c][2] * kLoUnscale) * scale;
-            y.w = (o[c][3] + ol[c][3] * kLoUnscale) * scale;
+            y.x = (o[c][0] + ol[c][0]) * scale;
+            y.y = (o[c][1] + ol[c][1]) * scale;
+            y.z = (o[c][2] + ol[c][2]) * scale;
+            y.w = (o[c][3] + ol[c][3]) * scale;
             *reinterpret_cast<float4*>(dst + c * 16 + 4 * rg) = y;
         }
     } else {
         float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * H + head) * kPrefillRows + r0 + col) * (D + 2);
         if (rg == 0) {
             p[0] = m;
-            p[1] = lsum;
+            p[1] = lsum * kPUnscalePre;
         }
 #pragma unroll
         for (int c = 0; c < VC; c++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * kPUnscalePre;
+            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j]) * kPUnscalePre;
     }
 }
 
