@@ -966,14 +966,29 @@ __device__ __forceinline__ float rows4_sum(float v) {
     s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
-// p in [0, 1] enters PV scaled by 2^14 so that p down to ~4e-9 is a normal f16.
-constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f;
+// Position, in 16-byte chunks, of chunk q of row `key` in an LDS tile of
+// CH-chunk rows: row major, the chunk index XORed with a permutation of the
+// row's 256-byte window index, so that the 16 lanes reading one chunk of 16
+// consecutive rows (the K operand) and the 32 lanes reading 4 dims of 8 rows
+// for the transposed V operand each hit distinct banks.
+template <int CH>
+__device__ __forceinline__ uint32_t tile_chunk(uint32_t key, uint32_t q) {
+    const uint32_t i = (key * CH / 16) % CH;
+    const uint32_t sw = ((i & (CH / 2 - 1)) << 1) | (i / (CH / 2));
+    return key * CH + (q ^ sw);
+}
+typedef __fp16 v4fp16_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+#define NI_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+// p in [0, 1] enters PV scaled by 2^14 (through the exponent reference:
+// exp2(s - (m - 14))), so that p down to ~4e-9 is a normal f16.
+constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f, kLog2PScale = 14.f;
 
 // Groups of 2..16 queries of one sequence (speculative verify, prefill
 // chunks) on matrix cores: one wave per page walks S^T = K Q^T (16 keys x 16
 // query slots, v_mfma_f32_16x16x32_f16, q split into f16 hi + lo), the
 // online softmax on S^T's columns, and O^T += V^T P^T (v_mfma_f32_16x16x16_f16,
-// p split hi + lo), V transposed through a padded LDS tile.  Lane l owns
+// p split hi + lo), V rows through a per-wave LDS tile read back transposed
+// (ds_read_b64_tr_b16).  Lane l owns
 // query column l % 16 of S^T and O^T, rows 4*(l/16) .. +3 (MFMA output
 // layout), so the softmax state of a query lives in lanes q, q+16, q+32, q+48.
 // Waves take the item's pages round-robin and merge through LDS at the end,
@@ -996,10 +1011,12 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     constexpr int LPK = D / VE;     // lanes per key row in a coalesced V load
     constexpr int KPL = 64 / LPK;   // key rows per V load
     constexpr int LPP = kPage / KPL;
-    constexpr int VROW = D + 8;     // LDS halves per V row (pad: conflict-free column reads)
+    constexpr int CH = D / 8;       // 16-byte chunks per V row
     constexpr int NQ = 16;
     __shared__ float red[W][NQ][D + 2];
-    __shared__ __attribute__((aligned(16))) _Float16 vt[W][PB * kPage * VROW];
+    // Per-wave V tile, row major with tile_chunk's chunk swizzle: rows go in
+    // with 16-byte writes, V^T comes out through transposing reads.
+    __shared__ __attribute__((aligned(16))) _Float16 vt[W][PB * kPage * D];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1121,7 +1138,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     // vref: vref starts at 1 (scales up to 1, values up to 127 in magnitude,
     // leave it there, and the products match p * vs * kPScale bit for bit)
     // and follows the largest scale seen beyond that.
-    float vref = 1.f, vsc = kPScale;  // vsc = kPScale / vref
+    float vref = 1.f, vinv = 1.f;  // vinv = 1 / vref
     _Float16* my_vt = vt[wave];
     const uint32_t qpos = it.pos0 + col;  // this lane's query position
     const bool qok = col < (int)it.nq;
@@ -1135,16 +1152,18 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         for (int b = 0; b < PB; b++) {
 #pragma unroll
             for (int i = 0; i < LPP; i++) {
-                const uint32_t key = i * KPL + lane / LPK;
-                const u32x4 val = (pg + b) * kPage + key < it.kv_end ? cur.v[b][i] : u32x4{0, 0, 0, 0};
-                _Float16* dst = my_vt + (b * kPage + key) * VROW + (lane % LPK) * VE;
-                if constexpr (Q8) {
-                    reinterpret_cast<half4_t*>(dst)[0] = i8x4_f16(val[0]);
-                    reinterpret_cast<half4_t*>(dst)[1] = i8x4_f16(val[1]);
-                    reinterpret_cast<half4_t*>(dst)[2] = i8x4_f16(val[2]);
-                    reinterpret_cast<half4_t*>(dst)[3] = i8x4_f16(val[3]);
+                const uint32_t key = b * kPage + i * KPL + lane / LPK;
+                const u32x4 val = pg * kPage + key < it.kv_end ? cur.v[b][i] : u32x4{0, 0, 0, 0};
+                if constexpr (Q8) {  // 16 values: chunks 2q, 2q+1 of the row
+                    const uint32_t q = 2 * (lane % LPK);
+                    const half4_t v0 = i8x4_f16(val[0]), v1 = i8x4_f16(val[1]);
+                    const half4_t v2 = i8x4_f16(val[2]), v3 = i8x4_f16(val[3]);
+                    *reinterpret_cast<half8_t*>(my_vt + tile_chunk<CH>(key, q) * 8) =
+                        __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+                    *reinterpret_cast<half8_t*>(my_vt + tile_chunk<CH>(key, q + 1) * 8) =
+                        __builtin_shufflevector(v2, v3, 0, 1, 2, 3, 4, 5, 6, 7);
                 } else {
-                    *reinterpret_cast<u32x4*>(dst) = val;
+                    *reinterpret_cast<u32x4*>(my_vt + tile_chunk<CH>(key, lane % LPK) * 8) = val;
                 }
             }
         }
@@ -1176,8 +1195,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 mx = fmaxf(mx, s[b][j]);
             }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = rows4_max(mx);
         const float mn = fmaxf(m, mx);
         const float alpha = fast_exp2(m - mn);
         float oalpha = alpha;  // the accumulators' factor
@@ -1202,29 +1220,32 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                         if ((pg + b) * kPage + 4 * rg + j < it.kv_end) vm = fmaxf(vm, cur.vs[b][j]);
             }
             if (__any(vm > vref)) {
-                vm = fmaxf(vm, __shfl_xor(vm, 16));
-                vm = fmaxf(vm, __shfl_xor(vm, 32));
+                vm = rows4_max(vm);
                 oalpha *= vref / vm;
                 vref = vm;
-                vsc = kPScale / vm;
+                vinv = 1.f / vm;
             }
         }
+        // Weights scaled by kPScale through the exponent reference, so lsum
+        // is in those units too; Q8 weighs p by vs / vref before the split.
+        const float mref = mn - kLog2PScale;
         half4_t ph[PB], pl[PB];
         float ps = 0.f;
 #pragma unroll
         for (int b = 0; b < PB; b++) {
+            float p[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float p = fast_exp2(s[b][j] - mn);
-                ps += p;
-                _Float16 h, l;
-                if constexpr (Q8)
-                    split_f16(p * cur.vs[b][j] * vsc, h, l);
-                else
-                    split_f16(p * kPScale, h, l);
-                ph[b][j] = h;
-                pl[b][j] = l;
+            for (int j = 0; j < 4; j++) p[j] = fast_exp2(s[b][j] - mref);
+            ps += (p[0] + p[1]) + (p[2] + p[3]);
+            if constexpr (Q8) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) p[j] *= cur.vs[b][j] * vinv;
             }
+            uint32_t h0, l0, h1, l1;
+            split_w16x2(p[0], p[1], h0, l0);
+            split_w16x2(p[2], p[3], h1, l1);
+            ph[b] = __builtin_bit_cast(half4_t, u32x2_t{h0, h1});
+            pl[b] = __builtin_bit_cast(half4_t, u32x2_t{l0, l1});
         }
         lsum = lsum * alpha + ps;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1240,14 +1261,18 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 ol[c] *= oalpha;
             }
         }
-        // O^T += V^T P^T, 16 dims per product.
+        // O^T += V^T P^T, 16 dims per product; V^T (dim c*16 + col of keys
+        // 4*rg .. 4*rg+3) by a transposing read of the row-major tile, as in
+        // attn_prefill_kernel.
 #pragma unroll
         for (int c = 0; c < VC; c++) {
 #pragma unroll
             for (int b = 0; b < PB; b++) {
-                half4_t vt4;
-#pragma unroll
-                for (int j = 0; j < 4; j++) vt4[j] = my_vt[(b * kPage + 4 * rg + j) * VROW + c * 16 + col];
+                const int t = (lane >> 2) & 3, av = lane & 3;
+                const _Float16* vp =
+                    my_vt + tile_chunk<CH>(b * kPage + 4 * rg + t, 2 * c + (av >> 1)) * 8 + (av & 1) * 4;
+                const half4_t vt4 = __builtin_bit_cast(
+                    half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4fp16_t*)(vp)));
                 o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, ph[b], o[c], 0, 0, 0);
                 ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl[b], ol[c], 0, 0, 0);
             }
@@ -1258,18 +1283,17 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         if (pg + STRIDE < pg_end) cur = nxt;
     }
     // Lanes q, q+16, q+32, q+48 hold partial sums of query q's softmax.
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
+    lsum = rows4_sum(lsum);
     if (qok) {
         if (rg == 0) {
             red[wave][col][0] = m;
-            red[wave][col][1] = lsum;
+            red[wave][col][1] = lsum * kPUnscale;
         }
 #pragma unroll
         for (int c = 0; c < VC; c++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                red[wave][col][2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j] * kLoUnscale) * (kPUnscale * vref);
+                red[wave][col][2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j]) * (kPUnscale * vref);
     }
     __syncthreads();
     for (uint32_t t = threadIdx.x; t < it.nq * D; t += 64 * W) {
@@ -1327,19 +1351,6 @@ constexpr int kPrefillPages = NI_PREFILL_PAGES;  // pages per LDS tile
 constexpr int kPrefillStages = NI_PREFILL_STAGES;  // LDS tiles in the ring (3 or 4)
 static_assert(kPrefillStages == 3 || kPrefillStages == 4, "ring of 3 or 4 tiles");
 
-// Position, in 16-byte chunks, of chunk q of row `key` in an LDS tile of
-// CH-chunk rows: row major, the chunk index XORed with a permutation of the
-// row's 256-byte window index, so that the 16 lanes reading one chunk of 16
-// consecutive rows (the K operand) and the 32 lanes reading 4 dims of 8 rows
-// for the transposed V operand each hit distinct banks.
-template <int CH>
-__device__ __forceinline__ uint32_t tile_chunk(uint32_t key, uint32_t q) {
-    const uint32_t i = (key * CH / 16) % CH;
-    const uint32_t sw = ((i & (CH / 2 - 1)) << 1) | (i / (CH / 2));
-    return key * CH + (q ^ sw);
-}
-typedef __fp16 v4fp16_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
-#define NI_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 // 16 bytes per lane from g to LDS at the wave-uniform dst + 16 * lane
 // (global_load_lds_dwordx4, M0 = dst's LDS address).  Written as assembly
 // so that the compiler does not add a wait for every DMA in flight before
