@@ -1378,7 +1378,8 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     constexpr int TK = PT * (int)kPage;     // keys per tile
     constexpr int CH = D / 8;               // 16-byte chunks per key row
     constexpr int TH = TK * D;              // halves per K (or V) tile
-    static_assert(TK * CH == 256, "one chunk of K and one of V per thread per tile");
+    constexpr int CPT = TK * CH / 256;      // chunks of K (and of V) per thread per tile
+    static_assert(TK * CH % 256 == 0, "a tile must split evenly over the workgroup");
     __shared__ __attribute__((aligned(16))) _Float16 ring[kPrefillStages][2][TH];  // [stage][K, V]
 
     const int lane = threadIdx.x & 63;
@@ -1415,33 +1416,30 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     // Keys below this are visible to every query of the wave (no masking).
     const uint32_t kfull_w = min(it.kv_end, it.pos0 + r0 + 1);
 
-    // Tile DMA: thread t copies LDS chunk t of each tile (K and V): row
-    // t / CH, logical chunk (t % CH) ^ sw -- tile_chunk's inverse.  Every
-    // wave issues exactly two DMA loads per tile, so "tile i landed" is
-    // "at most the next tile's two loads outstanding".
-    const uint32_t dkey = threadIdx.x / CH;
-    const uint32_t dq = threadIdx.x % CH ^ (tile_chunk<CH>(dkey, 0) - dkey * CH);
-    const uint32_t dpage = dkey / kPage;                      // page of the tile
-    const uint32_t doff = (dkey % kPage) * D + dq * 8;        // halves into the page
-    _Float16* const kdst0 = &ring[0][0][0] + wave * 512;  // this wave's 1 KB of a tile
+    // Tile DMA: thread t copies LDS chunks u = t + 256 c (c < CPT) of each
+    // tile (K and V): row u / CH, logical chunk (u % CH) ^ sw -- tile_chunk's
+    // inverse.  Every wave issues exactly 2 CPT DMA loads per tile, so "tile
+    // i landed" is "at most the later tiles' 2 CPT loads each outstanding".
     auto issue = [&](int st, uint32_t pg) {
         // Page bases are wave-uniform (scalar); a row past the end reads
         // page pg's first row, a key of this item.
-        const uint16_t* kp = kbase + (uint64_t)tab[pg] * page_stride;
-        const uint16_t* vp = vbase + (uint64_t)tab[pg] * page_stride;
-        const bool in = pg * kPage + dkey < it.kv_end;
+        uint64_t base[PT];
 #pragma unroll
-        for (int b = 1; b < PT; b++) {
-            const uint64_t base = (uint64_t)tab[min(pg + b, pg_end - 1)] * page_stride;
-            if (in && dpage == (uint32_t)b) {
-                kp = kbase + base;
-                vp = vbase + base;
-            }
+        for (int b = 0; b < PT; b++) base[b] = (uint64_t)tab[min(pg + b, pg_end - 1)] * page_stride;
+#pragma unroll
+        for (int c = 0; c < CPT; c++) {
+            const uint32_t u = threadIdx.x + 256 * c, dkey = u / CH;
+            const uint32_t dq = u % CH ^ (tile_chunk<CH>(dkey, 0) - dkey * CH);
+            const bool in = pg * kPage + dkey < it.kv_end;
+            uint64_t pb = base[0];
+#pragma unroll
+            for (int b = 1; b < PT; b++)
+                if (in && dkey / kPage == (uint32_t)b) pb = base[b];
+            const uint32_t off = (in ? (dkey % kPage) * D : 0u) + dq * 8;
+            _Float16* const dst = &ring[st][0][0] + (256 * c + 64 * wave) * 8;  // this wave's 1 KB
+            lds_dma16(kbase + pb + off, dst);
+            lds_dma16(vbase + pb + off, dst + TH);
         }
-        const uint32_t off = in ? doff : dq * 8;
-        _Float16* const kdst = kdst0 + st * (2 * TH);
-        lds_dma16(kp + off, kdst);
-        lds_dma16(vp + off, kdst + TH);
     };
     const uint32_t n_tiles = (pg_end - pg_begin + PT - 1) / PT;
 #pragma unroll
@@ -1487,9 +1485,9 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
         // wave is done with tile ti-1, whose stage the next tile takes.
         const uint32_t ahead = min(n_tiles - 1 - ti, (uint32_t)(kPrefillStages - 2));
         if (ahead >= 2)
-            __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4)
+            __builtin_amdgcn_s_waitcnt(0x0f70 | 4 * CPT);  // vmcnt(4 CPT)
         else if (ahead == 1)
-            __builtin_amdgcn_s_waitcnt(0x0f72);  // vmcnt(2)
+            __builtin_amdgcn_s_waitcnt(0x0f70 | 2 * CPT);  // vmcnt(2 CPT)
         else
             __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
         __syncthreads();
