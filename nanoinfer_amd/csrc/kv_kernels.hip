@@ -1263,18 +1263,35 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
         }
         // O^T += V^T P^T, 16 dims per product; V^T (dim c*16 + col of keys
         // 4*rg .. 4*rg+3) by a transposing read of the row-major tile, as in
-        // attn_prefill_kernel.
+        // attn_prefill_kernel, and pages in pairs through the 32-key product
+        // when PB is even.
+        auto vread = [&](int b, int c) {
+            const int t = (lane >> 2) & 3, av = lane & 3;
+            const _Float16* vp = my_vt + tile_chunk<CH>(b * kPage + 4 * rg + t, 2 * c + (av >> 1)) * 8 + (av & 1) * 4;
+            return __builtin_bit_cast(
+                half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4fp16_t*)(vp)));
+        };
+        if constexpr (PB % 2 == 0) {
 #pragma unroll
-        for (int c = 0; c < VC; c++) {
+            for (int b = 0; b < PB; b += 2) {
+                const half8_t p8h = __builtin_shufflevector(ph[b], ph[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+                const half8_t p8l = __builtin_shufflevector(pl[b], pl[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-            for (int b = 0; b < PB; b++) {
-                const int t = (lane >> 2) & 3, av = lane & 3;
-                const _Float16* vp =
-                    my_vt + tile_chunk<CH>(b * kPage + 4 * rg + t, 2 * c + (av >> 1)) * 8 + (av & 1) * 4;
-                const half4_t vt4 = __builtin_bit_cast(
-                    half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4fp16_t*)(vp)));
-                o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, ph[b], o[c], 0, 0, 0);
-                ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl[b], ol[c], 0, 0, 0);
+                for (int c = 0; c < VC; c++) {
+                    const half8_t v8 = __builtin_shufflevector(vread(b, c), vread(b + 1, c), 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8h, o[c], 0, 0, 0);
+                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, ol[c], 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < VC; c++) {
+#pragma unroll
+                for (int b = 0; b < PB; b++) {
+                    const half4_t vt4 = vread(b, c);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, ph[b], o[c], 0, 0, 0);
+                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl[b], ol[c], 0, 0, 0);
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
