@@ -1066,7 +1066,9 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
 
     // Page registers: K as the A operand (key col, dims c*32 + 8*rg ..), V
     // as coalesced rows (key i*KPL + lane/LPK, dims (lane%LPK)*8 ..).  Pages
-    // past pg_end are not loaded (their keys are masked).
+    // past pg_end (possible only with PB > 1) are not loaded: their keys are
+    // masked, and their registers are zeroed so that, Q8, p = 0 meets a
+    // scale of 0, not whatever the registers held.
     // Q8: K as 8 int8 per (key, chunk), the scales of keys 4*rg .. 4*rg+3
     // (the rows of S^T and P^T this lane holds).
     struct Regs {
@@ -1077,7 +1079,14 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     auto load = [&](uint32_t pg, Regs& r) {
 #pragma unroll
         for (int b = 0; b < PB; b++) {
-            if (pg + b >= pg_end) continue;
+            if (pg + b >= pg_end) {
+#pragma unroll
+                for (int c = 0; c < QC; c++) r.k[b][c] = u32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int i = 0; i < LPP; i++) r.v[b][i] = u32x4{0, 0, 0, 0};
+                if constexpr (Q8) r.ks[b] = r.vs[b] = float4{0.f, 0.f, 0.f, 0.f};
+                continue;
+            }
             const uint64_t phys = tab[pg + b];
             if constexpr (Q8) {
                 const uint8_t* kb = reinterpret_cast<const uint8_t*>(kbase + phys * page_stride);
