@@ -1,0 +1,85 @@
+"""Configs 3 and 5 at the sizes the benchmark measures, every step against the
+oracle.
+
+Config 3 is the continuous-batching trace of metal_serve.rs:255-363 with 64
+slots and the reference's 3080-page pool (metal_serve.rs:485); config 5 is the
+speculative-verify loop of metal_spec.rs:118-169 over 32 sequences with
+contexts U[128, 1024].  test_gpu_lifecycle.py runs both scaled down for many
+more steps; here the sizes are the real ones (GPT-2 12 x 12 x 64, 16-token
+pages), so every launch shape the benchmark uses -- all layers in one fused
+launch, 768+ workgroups, prompt chunks appended by the launch's extra blocks,
+5-row groups on the matrix cores -- is checked row by row.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import nanoinfer_amd as na
+from nanoinfer_amd import workloads
+from paged_mirror import Mirror, assert_close, mirror_step
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True, file=sys.stderr)
+
+
+def test_config3_full_size_trace(gpu, oracle_lib):
+    """Config 3 from an empty cache through the ramp-up: Poisson arrivals at
+    1 per step, prompts U[32,512], outputs U[16,256], prefill budget 256 rows
+    per step, 64 slots, 3080 pages; every decode row and the last row of
+    each prompt queried (the benchmark's setting), the append fused into the
+    attention launch.  60 steps against the oracle, then every live
+    sequence's K/V gathered bit for bit."""
+    rng = np.random.default_rng(41)
+    m = Mirror(na.BatchOpts(**workloads.GPT2, kv_blocks=3080, max_seqs=64, n_ctx=1024, max_rows=512))
+    trace = workloads.ContinuousBatching(m.kv)  # config 3's parameters are the defaults
+    worst, queried = 0.0, 0
+    for step in range(60):
+        st = trace.plan()
+        n = int(st.work[:, 1].sum())
+        q, k, v = (rng.standard_normal((12, n, m.c)).astype(np.float32) for _ in range(3))
+        got, want, qrows = mirror_step(m, st.work, q, k, v)
+        worst = max(worst, assert_close(got[:, qrows], want[:, qrows], f"config 3 step {step}"))
+        queried += len(qrows)
+        trace.commit()
+        if step % 15 == 14:
+            live = sum(m.kv.is_live(s) for s in range(64))
+            say(f"config 3 step {step}: {live} live, {n} rows this step, max abs err {worst:.2e}")
+    live = [s for s in range(64) if m.kv.is_live(s)]
+    assert len(live) >= 40 and queried > 1000
+    used = sum(-(-m.kv.seq_len(s) // 16) for s in live)
+    assert 3080 - m.kv.free_block_count() == used
+    rows = [(s, p) for s in live for p in range(m.kv.seq_len(s))]
+    (kg, vg), (kw, vw) = m.gather(rows)
+    assert np.array_equal(kg, kw) and np.array_equal(vg, vw)
+    say(f"config 3: {len(live)} live, {len(rows)} rows gathered bit for bit, {queried} rows queried, "
+        f"max abs err {worst:.2e}")
+
+
+def test_config5_full_size_trace(gpu, oracle_lib):
+    """Config 5: 32 sequences with contexts U[128, 1024] (the benchmark's
+    seed), each step appending g + 4 drafts and querying them as one causal
+    5-row group, accepting U[0,4] and truncating the rest.  5 steps against
+    the oracle."""
+    rng = np.random.default_rng(42)
+    ctx, _ = workloads.config5_contexts()
+    m = Mirror(na.BatchOpts(**workloads.GPT2, kv_blocks=2400, max_seqs=32, n_ctx=1104, max_rows=512))
+    seqs = [m.kv.add_seq() for _ in ctx]
+    for s, L in zip(seqs, ctx):
+        m.fill(s, L, rng, chunk=512)
+    spec = workloads.SpecVerify(m.kv, seqs, k=4, seed=9)
+    worst = 0.0
+    for step in range(5):
+        st = spec.plan()
+        n = int(st.work[:, 1].sum())
+        assert n == 5 * len(seqs)
+        q, k, v = (rng.standard_normal((12, n, m.c)).astype(np.float32) for _ in range(3))
+        got, want, qrows = mirror_step(m, st.work, q, k, v)
+        worst = max(worst, assert_close(got[:, qrows], want[:, qrows], f"config 5 step {step}"))
+        spec.commit()
+        say(f"config 5 step {step}: max abs err {worst:.2e}")
+    for s in seqs:
+        assert len(m.kv.block_table(s)) == -(-m.kv.seq_len(s) // 16)
