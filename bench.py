@@ -84,7 +84,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="config3",
                     help="config3 (default), config2, config4, config5, configNq8 (the same on the Q8 cache), "
-                         "prefill (16 x 512-row prompts, every row queried), or qkv[ROWS] (the QKV projection with "
+                         "prefill (16 x 512-row prompts, every row queried), prefillq8 (the same on the Q8 cache), or qkv[ROWS] (the QKV projection with "
                          "the append in its epilogue, ROWS rows per layer, default 64)")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = automatic)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (0 = skip)")
@@ -402,26 +402,31 @@ def run_prefill(args):
     from nanoinfer_amd import drivers, workloads
 
     B, P = drivers.PREFILL_SEQS, drivers.PREFILL_ROWS
-    c, L = 768, workloads.GPT2["n_layer"]
-    r = _drive("prefill", args)
+    c, L, H = 768, workloads.GPT2["n_layer"], workloads.GPT2["n_head"]
+    q8 = args.workload.endswith("q8")
+    kvb = c + 4 * H if q8 else 2 * c  # stored bytes of one position's K (or V) in one layer
+    r = _drive(args.workload, args)
     res = _line(args, r, f"prefill: {B} sequences x {P}-row prompt from empty, every row queried (causal), GPT-2 "
-                         f"12x12x64, 16-token pages, rolled back each step",
+                         f"12x12x64, 16-token pages, rolled back each step{'; Q8 KV cache' if q8 else ''}",
                 {"seqs": B, "rows": P, "algorithmic_bytes_per_step": int(r["bytes"] / r["steps"]),
                  "host_loop": "C++ driver (ni_drive_run)"},
                 "synthetic (seeded N(0,1) q/k/v resident in HBM)")
     res["metric"] = "paged prefill attention + append, algorithmic GB/s, 1 MI355X"
+    if q8:
+        res["kv_dtype"] = "q8"
     res["attention_tflops_whole_step"] = round(r["flops"] / r["seconds"] / 1e12, 2)
     if not args.no_profile:
-        rp = _drive("prefill", args, profile_mask=(1 << 0) | (1 << 1) | (1 << 2))
+        rp = _drive(args.workload, args, profile_mask=(1 << 0) | (1 << 1) | (1 << 2))
         steps = rp["steps"]
         attn_ms = rp["kernel_ms"][1] + rp["kernel_ms"][2]
-        append_bytes = B * P * c * 12 * L
+        append_bytes = B * P * L * (8 * c + 2 * kvb)
         attn_bytes = rp["bytes"] / steps - append_bytes
         t = attn_ms / 1e3 / steps
         gbs = attn_bytes / t / 1e9
         tfl = rp["flops"] / steps / t / 1e12
         res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_GBS, "unit": "GB/s",
-                           "frac": round(gbs / PEAK_GBS, 4), "traffic": None, "kernel": "attn_prefill_kernel<64,2>",
+                           "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
+                           "kernel": "attn_prefill_kernel<64,2,q8>" if q8 else "attn_prefill_kernel<64,2>",
                            "avg_launch_us": round(t * 1e6, 3), "launches": rp["kernel_launches"][1],
                            "algorithmic_bytes_per_launch": int(attn_bytes),
                            "flops_per_launch": int(rp["flops"] / steps), "achieved_tflops": round(tfl, 2),
@@ -449,7 +454,7 @@ def main():
         res = run_config3(args)
     elif args.workload.startswith("qkv"):
         res = run_qkv(args)
-    elif args.workload == "prefill":
+    elif args.workload in ("prefill", "prefillq8"):
         res = run_prefill(args)
     elif args.workload in SECONDARY:
         res = run_secondary(args)

@@ -257,7 +257,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     std::vector<Group> groups;
     groups.reserve(qr.size());
     // Runs longer than one matrix tile form prefill groups (f16 pools).
-    const bool prefill = NI_ATTN_MFMA && NI_ATTN_PREFILL && !is_q8(kv->o);
+    const bool prefill = NI_ATTN_MFMA && NI_ATTN_PREFILL && (!is_q8(kv->o) || kv->o.head_dim == 64);
     const uint32_t max_group = prefill ? kPrefillRows : max_group_rows(kv);
     for (const QRow& r : qr) {
         if (!groups.empty()) {

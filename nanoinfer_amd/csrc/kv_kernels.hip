@@ -1396,7 +1396,29 @@ __device__ __forceinline__ void lds_dma16(const void* g, void* dst) {
 constexpr float kRefSlack = 8.f;
 constexpr float kLog2PScalePre = 7.f, kPUnscalePre = 1.f / 128.f;
 
-template <int D, int PT, int INL>
+// Q8 tiles (head_dim 64): int8 rows of 64 bytes, 16-byte chunk q of row key
+// at key * 4 + (q ^ sw), sw = ((key >> 2) & 3) ^ (((key >> 4) & 1) << 1):
+// the 16 lanes reading one chunk of 16 rows (the K operand) and the 32 lanes
+// of a transposing read of 8 rows of two pages (the V operand) both hit
+// distinct banks.
+__device__ __forceinline__ uint32_t tile_chunk_q8(uint32_t key, uint32_t q) {
+    return key * 4 + (q ^ (((key >> 2) & 3) ^ (((key >> 4) & 1) << 1)));
+}
+typedef int v2i32_t __attribute__((ext_vector_type(2)));
+
+// Wait until at most `ahead` tiles of N DMA loads each are outstanding (vmcnt
+// counts this wave's loads in order).
+template <int N>
+__device__ __forceinline__ void wait_tiles(uint32_t ahead) {
+    if (ahead >= 2)
+        __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * N));
+    else if (ahead == 1)
+        __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+    else
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+}
+
+template <int D, int PT, int INL, bool Q8>
 __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_prefill_kernel(const AttnLaunch a,
                                                                                              const PlanArg<INL> pa) {
     constexpr int QC = D / 32;              // 32-dim chunks of the QK product
@@ -1406,7 +1428,12 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     constexpr int TH = TK * D;              // halves per K (or V) tile
     constexpr int CPT = TK * CH / 256;      // chunks of K (and of V) per thread per tile
     static_assert(TK * CH % 256 == 0, "a tile must split evenly over the workgroup");
-    __shared__ __attribute__((aligned(16))) _Float16 ring[kPrefillStages][2][TH];  // [stage][K, V]
+    // A stage: f16, [K | V] tiles of TH halves; Q8, [K int8 | V int8 | K
+    // scales | V scales], TK * D bytes each, then TK floats each.
+    constexpr int QS = 2 * TK * D;          // Q8: byte offset of the K scales in a stage
+    constexpr int SB = Q8 ? QS + 8 * TK : 4 * TH;
+    static_assert(!Q8 || (D == 64 && PT == 2), "Q8 tiles: head_dim 64, two pages");
+    __shared__ __attribute__((aligned(16))) uint8_t ring[kPrefillStages][SB];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1425,6 +1452,8 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     const uint16_t* kbase = a.pool.k + layer_off;
     const uint16_t* vbase = a.pool.v + layer_off;
     const uint64_t page_stride = a.pool.page_halves;
+    const uint8_t* kb8 = reinterpret_cast<const uint8_t*>(kbase);  // Q8 pools, in bytes
+    const uint8_t* vb8 = reinterpret_cast<const uint8_t*>(vbase);
     // Page ids through the constant address space: wave-uniform scalar loads,
     // which a wait for the DMA tiles (in order with every vector load) does
     // not depend on.
@@ -1442,11 +1471,42 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     // Keys below this are visible to every query of the wave (no masking).
     const uint32_t kfull_w = min(it.kv_end, it.pos0 + r0 + 1);
 
-    // Tile DMA: thread t copies LDS chunks u = t + 256 c (c < CPT) of each
-    // tile (K and V): row u / CH, logical chunk (u % CH) ^ sw -- tile_chunk's
-    // inverse.  Every wave issues exactly 2 CPT DMA loads per tile, so "tile
-    // i landed" is "at most the later tiles' 2 CPT loads each outstanding".
+    // Tile DMA, f16: thread t copies LDS chunks u = t + 256 c (c < CPT) of
+    // each tile (K and V): row u / CH, logical chunk (u % CH) ^ sw --
+    // tile_chunk's inverse.  Every wave issues exactly 2 CPT DMA loads per
+    // tile, so "tile i landed" is "at most the later tiles' 2 CPT loads each
+    // outstanding".  Q8: thread t copies int8 chunk t % 128 of K (waves 0, 1)
+    // or V (waves 2, 3), and lanes 0..15 of wave 0 the 16 chunks of scales
+    // (4 keys each, K then V): one DMA load per tile, wave 0 two.
+    auto issue8 = [&](int st, uint32_t pg) {
+        uint64_t base[PT];  // bytes
+#pragma unroll
+        for (int b = 0; b < PT; b++) base[b] = (uint64_t)tab[min(pg + b, pg_end - 1)] * page_stride * 2;
+        const uint32_t u = threadIdx.x & 127, dkey = u / 4;
+        const uint32_t dq = u % 4 ^ (tile_chunk_q8(dkey, 0) - dkey * 4);
+        const bool in = pg * kPage + dkey < it.kv_end;
+        uint64_t pb = base[0];
+#pragma unroll
+        for (int b = 1; b < PT; b++)
+            if (in && dkey / kPage == (uint32_t)b) pb = base[b];
+        const uint32_t off = (in ? (dkey % kPage) * D : 0u) + dq * 16;
+        lds_dma16((threadIdx.x < 128 ? kb8 : vb8) + pb + off, &ring[st][0] + 1024 * wave);
+        if (wave == 0 && lane < 16) {
+            const uint32_t skey = 4 * (lane & 7);
+            const bool sin = pg * kPage + skey < it.kv_end;
+            uint64_t spb = base[0];
+#pragma unroll
+            for (int b = 1; b < PT; b++)
+                if (sin && skey / kPage == (uint32_t)b) spb = base[b];
+            const uint32_t soff = kPage * D + (sin ? (skey % kPage) * 4 : 0u);
+            lds_dma16((lane < 8 ? kb8 : vb8) + spb + soff, &ring[st][QS]);
+        }
+    };
     auto issue = [&](int st, uint32_t pg) {
+        if constexpr (Q8) {
+            issue8(st, pg);
+            return;
+        }
         // Page bases are wave-uniform (scalar); a row past the end reads
         // page pg's first row, a key of this item.
         uint64_t base[PT];
@@ -1462,7 +1522,7 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
             for (int b = 1; b < PT; b++)
                 if (in && dkey / kPage == (uint32_t)b) pb = base[b];
             const uint32_t off = (in ? (dkey % kPage) * D : 0u) + dq * 8;
-            _Float16* const dst = &ring[st][0][0] + (256 * c + 64 * wave) * 8;  // this wave's 1 KB
+            _Float16* const dst = reinterpret_cast<_Float16*>(&ring[st][0]) + (256 * c + 64 * wave) * 8;  // this wave's 1 KB
             lds_dma16(kbase + pb + off, dst);
             lds_dma16(vbase + pb + off, dst + TH);
         }
@@ -1498,6 +1558,10 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     // Weights are exp2(s - mref) with mref = m - kLog2PScalePre: p already
     // scaled by 2^7, and lsum and the accumulators in the same units.
     float m = kMinScore, mref = kMinScore - kLog2PScalePre, lsum = 0.f;
+    // Q8: p enters PV as p * vs / vref and the accumulators hold the sum in
+    // units of vref, which starts at 1 and follows the largest value scale
+    // seen beyond that (as in attn_mfma_kernel): p * vs / vref <= 2^15.
+    float vref = 1.f, vinv = 1.f;
     float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
 #pragma unroll
     for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -1510,17 +1574,23 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
         // outstanding); after the barrier every wave's part has, and every
         // wave is done with tile ti-1, whose stage the next tile takes.
         const uint32_t ahead = min(n_tiles - 1 - ti, (uint32_t)(kPrefillStages - 2));
-        if (ahead >= 2)
-            __builtin_amdgcn_s_waitcnt(0x0f70 | 4 * CPT);  // vmcnt(4 CPT)
-        else if (ahead == 1)
-            __builtin_amdgcn_s_waitcnt(0x0f70 | 2 * CPT);  // vmcnt(2 CPT)
-        else
-            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+        if constexpr (Q8) {
+            if (wave == 0)
+                wait_tiles<2>(ahead);
+            else
+                wait_tiles<1>(ahead);
+        } else {
+            wait_tiles<2 * CPT>(ahead);
+        }
         __syncthreads();
         if (ti + kPrefillStages - 1 < n_tiles)
             issue(st == 0 ? kPrefillStages - 1 : st - 1, pg + (kPrefillStages - 1) * PT);
-        const _Float16* const kt = &ring[st][0][0];
-        const _Float16* const vt = &ring[st][1][0];
+        const _Float16* const kt = reinterpret_cast<const _Float16*>(&ring[st][0]);
+        const _Float16* const vt = kt + TH;
+        const uint8_t* const kt8 = &ring[st][0];
+        const uint8_t* const vt8 = kt8 + TK * D;
+        const float* const kst = reinterpret_cast<const float*>(&ring[st][QS]);  // Q8 scales
+        const float* const vst = kst + TK;
         if (pg * kPage < kend_w) {  // wave-uniform: the tile holds keys this wave needs
             // Pages b < nb of the tile are needed; one softmax update per tile.
             const uint32_t nb = min((uint32_t)PT, (kend_w - pg * kPage + kPage - 1) / kPage);
@@ -1534,13 +1604,26 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
                 float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int c = 0; c < QC; c++) {
-                    const half8_t kh =
-                        *reinterpret_cast<const half8_t*>(kt + tile_chunk<CH>(b * kPage + col, 4 * c + rg) * 8);
+                    half8_t kh;
+                    if constexpr (Q8) {  // 8 int8 of the row (chunk 2c + rg/2, half rg%2) as f16
+                        const uint2 w = *reinterpret_cast<const uint2*>(
+                            kt8 + tile_chunk_q8(b * kPage + col, 2 * c + (rg >> 1)) * 16 + (rg & 1) * 8);
+                        kh = __builtin_shufflevector(i8x4_f16(w.x), i8x4_f16(w.y), 0, 1, 2, 3, 4, 5, 6, 7);
+                    } else {
+                        kh = *reinterpret_cast<const half8_t*>(kt + tile_chunk<CH>(b * kPage + col, 4 * c + rg) * 8);
+                    }
                     st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
                     sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
                 }
 #pragma unroll
                 for (int j = 0; j < 4; j++) sc[b][j] = st[j] + sl[j] * kLoUnscale;
+                if constexpr (Q8) {  // key scales of keys 4*rg .. 4*rg+3
+                    const float4 ks = *reinterpret_cast<const float4*>(kst + b * kPage + 4 * rg);
+                    sc[b][0] *= ks.x;
+                    sc[b][1] *= ks.y;
+                    sc[b][2] *= ks.z;
+                    sc[b][3] *= ks.w;
+                }
             }
             if (!full) {
 #pragma unroll
@@ -1572,6 +1655,30 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
                     ol[c] *= alpha;
                 }
             }
+            float4 vs[Q8 ? PT : 1];
+            if constexpr (Q8) {
+                // Value scales of keys 4*rg .. 4*rg+3 of each page; past the
+                // reference vref, move it to the tile's largest (rows of
+                // pages past the end hold other keys' finite scales) and
+                // shrink the accumulators with it.
+                float vm = 0.f;
+#pragma unroll
+                for (int b = 0; b < PT; b++) {
+                    vs[b] = *reinterpret_cast<const float4*>(vst + b * kPage + 4 * rg);
+                    vm = fmaxf(fmaxf(vm, fmaxf(vs[b].x, vs[b].y)), fmaxf(vs[b].z, vs[b].w));
+                }
+                if (__any(vm > vref)) {
+                    vm = rows4_max(vm);
+                    const float f = vref / vm;
+#pragma unroll
+                    for (int c = 0; c < VC; c++) {
+                        o[c] *= f;
+                        ol[c] *= f;
+                    }
+                    vref = vm;
+                    vinv = 1.f / vm;
+                }
+            }
             half4_t ph[PT], pl[PT];
             float ps[PT];
 #pragma unroll
@@ -1580,6 +1687,12 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
 #pragma unroll
                 for (int j = 0; j < 4; j++) p[j] = fast_exp2(sc[b][j] - mref);
                 ps[b] = (p[0] + p[1]) + (p[2] + p[3]);
+                if constexpr (Q8) {
+                    p[0] *= vs[b].x * vinv;
+                    p[1] *= vs[b].y * vinv;
+                    p[2] *= vs[b].z * vinv;
+                    p[3] *= vs[b].w * vinv;
+                }
                 uint32_t h0, l0, h1, l1;
                 split_w16x2(p[0], p[1], h0, l0);
                 split_w16x2(p[2], p[3], h1, l1);
@@ -1599,6 +1712,19 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
             // one): k-slot 8*rg + 4*i + j of the pair is key 4*rg + j of its
             // page i, in both operands.
             const int vt_t = (lane >> 2) & 3, vt_a = lane & 3;
+            // Q8: one 8-bit transposing read (ds_read_b64_tr_b8: within 16
+            // lanes, lane 2e+a reads bytes 8a .. 8a+7 of its row and lane
+            // 8a'+b' receives byte b' of lanes a', 2+a', .., 14+a') gives
+            // dim c*16 + col of the pair's 8 keys: lane 2e+a reads dims c*16 +
+            // 8a .. of key 4*rg + e of page b (e < 4) or b+1.
+            auto vread8 = [&](int b, int c) {
+                const int e = (lane & 15) >> 1, av = lane & 1;
+                const uint32_t key = (e < 4 ? b : b + 1) * kPage + 4 * rg + (e & 3);
+                const v2i32_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                    (__attribute__((address_space(3))) v2i32_t*)(vt8 + tile_chunk_q8(key, c) * 16 + av * 8));
+                return __builtin_shufflevector(i8x4_f16((uint32_t)r.x), i8x4_f16((uint32_t)r.y), 0, 1, 2, 3, 4, 5, 6,
+                                               7);
+            };
             auto vread = [&](int b, int c) {
                 const _Float16* vp =
                     vt + tile_chunk<CH>(b * kPage + 4 * rg + vt_t, 2 * c + (vt_a >> 1)) * 8 + (vt_a & 1) * 4;
@@ -1614,7 +1740,11 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
                     const half8_t p8l = __builtin_shufflevector(pl[b], pl[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                     for (int c = 0; c < VC; c++) {
-                        const half8_t v8 = __builtin_shufflevector(vread(b, c), vread(b + 1, c), 0, 1, 2, 3, 4, 5, 6, 7);
+                        half8_t v8;
+                        if constexpr (Q8)
+                            v8 = vread8(b, c);
+                        else
+                            v8 = __builtin_shufflevector(vread(b, c), vread(b + 1, c), 0, 1, 2, 3, 4, 5, 6, 7);
                         o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8h, o[c], 0, 0, 0);
                         ol[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, ol[c], 0, 0, 0);
                     }
@@ -1640,7 +1770,7 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     const uint32_t row = it.row0 + r0 + col;
     if (it.part_slot == kNoSlot) {
         float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)row * a.out_row_stride + head * D;
-        const float scale = 1.f / lsum;  // lsum and o both carry the 2^7
+        const float scale = vref / lsum;  // lsum and o both carry the 2^7; Q8: o in units of vref
 #pragma unroll
         for (int c = 0; c < VC; c++) {
             float4 y;
@@ -1659,7 +1789,7 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
 #pragma unroll
         for (int c = 0; c < VC; c++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j]) * kPUnscalePre;
+            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j]) * (kPUnscalePre * vref);
     }
 }
 
@@ -1825,7 +1955,10 @@ hipError_t prefill_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hi
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         // head_dim 128 stages one page per tile (two spill registers).
         constexpr int PT = D == 128 ? 1 : kPrefillPages;
-        return go(attn_prefill_kernel<D, PT, INL>, blocks, 256, s, t, a, pa);
+        if constexpr (D == 64 && PT == 2)
+            if (a.pool.q8) return go(attn_prefill_kernel<D, PT, INL, true>, blocks, 256, s, t, a, pa);
+        if (a.pool.q8) return hipErrorInvalidValue;
+        return go(attn_prefill_kernel<D, PT, INL, false>, blocks, 256, s, t, a, pa);
     });
 }
 
@@ -1858,8 +1991,7 @@ hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStre
 template <int D>
 hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge,
                             const LaunchTiming& t) {
-    if (a.nq_tile == kPrefillRows) {  // prefill groups (f16 pools only)
-        if (a.pool.q8) return hipErrorInvalidValue;
+    if (a.nq_tile == kPrefillRows) {  // prefill groups (Q8 pools: head_dim 64 only)
         return merge ? merge_launch_t<D, kPrefillRows>(a, ip, ib, s, t) : prefill_launch_t<D>(a, ip, ib, s, t);
     }
     if (a.pool.q8) {  // single rows on the vector kernel, groups on the matrix cores

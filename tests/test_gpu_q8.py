@@ -117,11 +117,13 @@ def test_q8_decode_contexts(gpu, oracle_lib, shape, split):
     say(f"q8 {shape} split {split}: max abs err {err:.2e}")
 
 
-@pytest.mark.parametrize("nq", [2, 5, 16, 20])
+@pytest.mark.parametrize("nq", [2, 5, 16, 20, 64, 100])
 def test_q8_causal_groups(gpu, oracle_lib, nq):
     """Consecutive rows of one sequence share their K/V reads on the matrix
-    cores (int8 converted to f16 exactly, scales applied to scores and p);
-    groups over 16 rows split in two."""
+    cores (int8 converted to f16 exactly, scales applied to scores and p):
+    up to 16 rows on the group kernel, 17..64 on the prefill kernel (int8
+    tiles by DMA, V^T through the 8-bit transposing read), longer runs cut
+    into groups of 64."""
     rng = np.random.default_rng(93 + nq)
     m = MirrorQ8(opts(workloads.GPT2, n_layer=2))
     for split in (0, 64):
@@ -135,7 +137,21 @@ def test_q8_causal_groups(gpu, oracle_lib, nq):
             m.kv.free_seq(s)
 
 
-@pytest.mark.parametrize("nq", [1, 5, 16])
+def test_q8_long_groups_head_dim_128(gpu, oracle_lib):
+    """head_dim 128 on a Q8 cache keeps runs over 16 rows in groups of 16 on
+    the group kernel (the Q8 prefill tiles are for head_dim 64)."""
+    rng = np.random.default_rng(97)
+    m = MirrorQ8(opts(workloads.LONG, n_head=4))
+    s = m.kv.add_seq()
+    m.fill(s, 300, rng)
+    rows = [(s, p) for p in range(260, 300)]
+    q = rng.standard_normal((1, len(rows), m.c)).astype(np.float32)
+    for split in (0, 128):
+        got = m.kv.attention(torch.from_numpy(q).cuda(), rows, split_tokens=split).cpu().numpy()
+        assert_close(got, m.attention_oracle(rows, q), f"q8 hd128 40 rows split {split}")
+
+
+@pytest.mark.parametrize("nq", [1, 5, 16, 64])
 def test_q8_large_values(gpu, oracle_lib, nq):
     """Value scales far above 1 (|v| in the thousands) after a prefix of
     ordinary values: on the matrix cores p * scale would overflow f16 without
