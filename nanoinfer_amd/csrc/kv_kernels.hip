@@ -15,11 +15,16 @@
 //                      with the step's append fused into its prologue
 //   attn_mfma_kernel   the same for groups of 2..16 causal query rows of one
 //                      sequence, on the matrix cores
+//   attn_prefill_kernel  groups of 17..64 rows (prompt chunks), K/V tiles DMA'd
+//                      into an LDS ring shared by four waves (attn.metal:100-222)
+//   attn_q8_kernel     single rows on the int8 + scale (Q8) cache (kv8.metal)
 //   attn_merge_kernel  log-sum-exp merge of partitions (b_attn_merge, :403-424)
+//   qkv_kernel         the QKV projection with the append in its epilogue
+//                      (matvec_batch<..., BEPI_QKV>, batch.metal:94-165)
 //
-// Everything is HBM-bound streaming of f16 K/V.  Arithmetic is f32 (the
-// matrix-core kernel carries f32 operands as f16 hi + scaled lo parts);
-// softmax runs in the base-2 domain (scores pre-scaled by log2(e)/sqrt(D)).
+// Decode is HBM-bound streaming of f16 (or int8) K/V.  Arithmetic is f32 (the
+// matrix-core kernels carry f32 operands as f16 hi + lo parts); softmax runs
+// in the base-2 domain (scores pre-scaled by log2(e)/sqrt(D)).
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
