@@ -20,8 +20,10 @@ nanoinfer_amd/workloads.py, each KV byte once per step), from a run without
 per-launch events; ``roofline`` prices the attention launch alone, timed by
 HIP events the library records around each of its launches on the caller's
 stream in a second run of the same trace; ``per_layer_launches`` runs the
-trace a third time through per-layer append + attention calls, the way the
-reference dispatches; ``cpu_baseline`` times the oracle's restatement of the
+trace again one layer per launch, as a model's forward must (the step planned
+once, ni_kv_step_layer per layer), and ``per_layer_append_attention`` through
+separate per-layer append and attention calls; ``cpu_baseline`` times the
+oracle's restatement of the
 reference's CPU path (threaded, paged) on a bounded sample of the same trace.
 """
 from __future__ import annotations
@@ -281,15 +283,20 @@ def run_config3(args):
             res["roofline"]["traffic_vs_algorithmic"] = round(
                 tr["traffic_bytes_per_launch"] / tr["algorithmic_bytes_per_launch_same_steps"], 3)
             res["roofline"]["traffic_source"] = "profiles/attn_split_fused_config3.md (rocprofv3 --pmc, scaled)"
-    # The reference dispatches append and attention per layer; the same trace
-    # through ni_kv_append + ni_paged_decode_attention per layer.
+    # A model's forward runs a step's layers one at a time (layer l+1's q/k/v
+    # come from layer l's output); the reference encodes the step once and
+    # dispatches each layer's KV write and attention (batch.rs:280-306,
+    # 390-416).  The same trace with the step planned once and one fused
+    # append + attention launch per layer (ni_kv_step_layer), and through
+    # separate ni_kv_append + ni_paged_decode_attention calls per layer.
     if not args.skip_per_layer:
-        rl = _drive("config3", args, launch=drivers.NI_DRIVE_PER_LAYER)
-        gbs = rl["bytes"] / rl["seconds"] / 1e9
-        res["per_layer_launches"] = {"value": round(gbs, 2), "unit": "GB/s",
-                                     "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
-                                     "ms_per_step": round(rl["seconds"] / rl["steps"] * 1e3, 5),
-                                     "abi_calls_per_step": round(rl["launches"] / rl["steps"], 1)}
+        for key, mode in (("per_layer_launches", drivers.NI_DRIVE_STEP_LAYERS),
+                          ("per_layer_append_attention", drivers.NI_DRIVE_PER_LAYER)):
+            rl = _drive("config3", args, launch=mode)
+            gbs = rl["bytes"] / rl["seconds"] / 1e9
+            res[key] = {"value": round(gbs, 2), "unit": "GB/s", "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
+                        "ms_per_step": round(rl["seconds"] / rl["steps"] * 1e3, 5),
+                        "abi_calls_per_step": round(rl["launches"] / rl["steps"], 1)}
     if args.cpu_seconds > 0:
         threads = args.threads or min(os.cpu_count() or 1, 16)
         log(f"bench: planning the trace for the CPU baseline")

@@ -109,7 +109,8 @@ enum ni_drive_workload {
 };
 enum ni_drive_launch {
     NI_DRIVE_STEP = 0,     /* one ni_kv_step per iteration (all layers per launch) */
-    NI_DRIVE_PER_LAYER = 1 /* ni_kv_append + ni_paged_decode_attention per layer */
+    NI_DRIVE_PER_LAYER = 1, /* ni_kv_append + ni_paged_decode_attention per layer */
+    NI_DRIVE_STEP_LAYERS = 2 /* ni_kv_step_begin, one ni_kv_step_layer per layer, ni_kv_step_end */
 };
 
 typedef struct ni_drive_opts {

@@ -186,6 +186,24 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
                int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
                int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream);
 
+/* The same step one layer at a time, as a model's forward runs it: the
+ * reference encodes a step once (Batch::encode_step, batch.rs:280-306: check,
+ * reserve, lay out the rows) and then dispatches each layer's KV write and
+ * attention between that layer's other kernels (batch.rs:390-416).
+ * ni_kv_step_begin checks the work items and reserves pages exactly as
+ * ni_kv_step (same errors; nothing is open after an error) and plans the step
+ * once; ni_kv_step_layer(layer) then appends that layer's new rows and runs
+ * its attention in one launch over that plan (q/k/v/out hold the layer's rows
+ * only, row r at base + r*row_stride); ni_kv_step_end commits seq_len +=
+ * n_new.  Layers may come in any order, each once; calls on one stream (a
+ * staged plan is uploaded for the first call's stream and waited for on the
+ * others').  While a step is open, ni_kv_step, ni_kv_decode_steps,
+ * ni_kv_truncate, ni_kv_free_seq and ni_kv_commit return NI_ERR_BAD_ARG. */
+int ni_kv_step_begin(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t split_tokens);
+int ni_kv_step_layer(ni_kv* kv, int32_t layer, const float* q, const float* k, const float* v, int64_t row_stride,
+                     float* out, int64_t out_row_stride, ni_stream stream);
+int ni_kv_step_end(ni_kv* kv);
+
 /* Batch::decode_resident's KV part (batch.rs:322-363): `steps` decode steps
  * of the sequences seqs[0..n), enqueued at once with no host wait.  Pages
  * for every step are reserved first (each sequence to seq_len + steps; the

@@ -109,6 +109,12 @@ def _declare(L):
                                             _i64, _u32, _vp]
     L.ni_kv_step.restype = C.c_int
     L.ni_kv_step.argtypes = [_vp, C.POINTER(ni_work), _u32, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _u32, _vp]
+    L.ni_kv_step_begin.restype = C.c_int
+    L.ni_kv_step_begin.argtypes = [_vp, C.POINTER(ni_work), _u32, _u32]
+    L.ni_kv_step_layer.restype = C.c_int
+    L.ni_kv_step_layer.argtypes = [_vp, C.c_int32, _vp, _vp, _vp, _i64, _vp, _i64, _vp]
+    L.ni_kv_step_end.restype = C.c_int
+    L.ni_kv_step_end.argtypes = [_vp]
     L.ni_kv_decode_steps.restype = C.c_int
     L.ni_kv_decode_steps.argtypes = [_vp, C.POINTER(_u32), _u32, _u32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64,
                                      _i64, _u32, _vp]

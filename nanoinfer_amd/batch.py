@@ -317,6 +317,35 @@ class PagedKv:
                                        _stream_ptr(stream)))
         return out
 
+    def step_begin(self, work, split_tokens: int = 0):
+        """Check, reserve and plan one step (``work`` as in :meth:`step`) whose
+        layers then run one :meth:`step_layer` call each, as a model's forward
+        does (batch.rs:280-306 encodes once, batch.rs:390-416 dispatches per
+        layer); :meth:`step_end` commits it."""
+        w = np.ascontiguousarray(np.asarray(work, dtype=np.uint32).reshape(-1, 3))
+        self._check(self._L.ni_kv_step_begin(self._h, w.ctypes.data_as(C.POINTER(_abi.ni_work)), w.shape[0],
+                                             split_tokens))
+
+    def step_layer(self, layer: int, q, k, v, out=None, stream=None):
+        """Layer ``layer`` of the open step: its new rows appended and its
+        queried rows attended in one launch; q/k/v/out are [rows, C]."""
+        import torch
+
+        kp, rs, _ = _f32_arg(k, "k", False)
+        vp, rs2, _ = _f32_arg(v, "v", False)
+        qp, rs3, _ = _f32_arg(q, "q", False)
+        if not rs == rs2 == rs3:
+            raise ValueError("q, k and v must share a row stride")
+        if out is None:
+            out = torch.zeros_like(q)
+        op, ors, _ = _f32_arg(out, "out", False)
+        self._check(self._L.ni_kv_step_layer(self._h, layer, qp, kp, vp, rs, op, ors, _stream_ptr(stream)))
+        return out
+
+    def step_end(self):
+        """Commit the open step: every work item's sequence grows by n_new."""
+        self._check(self._L.ni_kv_step_end(self._h))
+
     def decode_steps(self, seqs, q, k, v, out=None, split_tokens: int = 0, stream=None):
         """decode_resident's KV part: q/k/v are [steps, n_layer, len(seqs), C];
         step t appends and attends position seq_len + t of every sequence."""

@@ -397,6 +397,21 @@ struct Runner {
                 return kv_fail(rc, "ni_kv_step");
             return NI_OK;
         }
+        if (o.launch == NI_DRIVE_STEP_LAYERS) {
+            // The step planned once, then one append + attention launch per
+            // layer, as a model's forward would call it between layers.
+            if (int rc = ni_kv_step_begin(kv, w, n, o.split_tokens)) return kv_fail(rc, "ni_kv_step_begin");
+            for (uint32_t l = 0; l < L; l++) {
+                calls++;
+                if (int rc = ni_kv_step_layer(kv, (int32_t)l, d.q + l * ls, d.k + l * ls, d.v + l * ls, C,
+                                              d.out + l * ls, C, stream)) {
+                    (void)ni_kv_step_end(kv);
+                    return kv_fail(rc, "ni_kv_step_layer");
+                }
+            }
+            if (int rc = ni_kv_step_end(kv)) return kv_fail(rc, "ni_kv_step_end");
+            return NI_OK;
+        }
         // Per layer, as the reference's forward dispatches: reserve, then for
         // each layer append its rows and attend its queried rows, then commit.
         rows.clear();
@@ -648,7 +663,9 @@ int run_qkv(Runner& r, ni_drive_result* res) {
 
 extern "C" int ni_drive_run(const ni_drive_opts* o, ni_drive_result* res) {
     if (!o || !res) return drive_fail(NI_ERR_BAD_ARG, "NULL argument");
-    if (o->launch > NI_DRIVE_PER_LAYER) return drive_fail(NI_ERR_BAD_ARG, "unknown launch mode %u", o->launch);
+    if (o->launch > NI_DRIVE_STEP_LAYERS) return drive_fail(NI_ERR_BAD_ARG, "unknown launch mode %u", o->launch);
+    if (o->workload == NI_DRIVE_QKV && o->launch == NI_DRIVE_STEP_LAYERS)
+        return drive_fail(NI_ERR_BAD_ARG, "the qkv workload runs NI_DRIVE_STEP or NI_DRIVE_PER_LAYER");
     if (o->kv.flags & NI_KV_HOST_ONLY) return drive_fail(NI_ERR_BAD_ARG, "ni_drive_run needs a device handle");
     *res = ni_drive_result{};
     Runner r(*o);

@@ -55,6 +55,7 @@ struct StagingSlot {
     hipEvent_t done = nullptr;      // the kernels that read this slot finished
     hipEvent_t uploaded = nullptr;  // the slot's upload finished (copy stream)
     bool pending = false;
+    bool held = false;  // the plan of an open step: not handed out again before ni_kv_step_end
 };
 
 // Work of one data-path call, before serialisation.
@@ -87,6 +88,20 @@ struct Plan {
         fused = false;
         wide = false;
     }
+};
+
+// Byte offsets of each part of a serialised plan.
+struct Offsets {
+    size_t app, orphans, items, merges, pitems, pmerges, table, total;
+};
+
+// Where the kernels find a plan: in the launch arguments (small plans) or in
+// a staging slot uploaded on the copy stream.
+struct PlanRef {
+    const void* inl = nullptr;
+    uint32_t inl_bytes = 0;
+    const uint8_t* dev = nullptr;
+    StagingSlot* slot = nullptr;
 };
 
 // A query row as the planner sees it.  [new_begin, new_end) are the positions
@@ -135,6 +150,19 @@ struct ni_kv {
     std::vector<uint32_t> seq_need;   // seq -> pages needed this call
     std::vector<uint32_t> step_mark;  // seq -> stamp of the last step that listed it
     uint32_t step_stamp = 0;
+
+    // A step planned by ni_kv_step_begin and run one layer per
+    // ni_kv_step_layer call until ni_kv_step_end.
+    struct OpenStep {
+        bool open = false;
+        Plan plan;
+        std::vector<uint8_t> blob;
+        std::vector<std::pair<uint32_t, uint32_t>> commit;  // (seq, n_new) for ni_kv_step_end
+        bool placed = false;  // plan serialised and reachable (at the first layer call)
+        Offsets off{};
+        PlanRef ref;
+        hipStream_t stream = nullptr;  // of the last layer call
+    } step;
 
     int fail(int code, const char* fmt, ...) __attribute__((format(printf, 3, 4))) {
         char buf[512];
@@ -407,6 +435,7 @@ struct ProfileScope {
 // Reserve a staging slot of at least `bytes`; waits for the slot's previous
 // use to finish.
 int acquire_slot(ni_kv* kv, size_t bytes, StagingSlot** out) {
+    if (kv->ring[kv->ring_next].held) kv->ring_next = (kv->ring_next + 1) % kRingSlots;  // at most one is held
     StagingSlot& sl = kv->ring[kv->ring_next];
     kv->ring_next = (kv->ring_next + 1) % kRingSlots;
     if (sl.pending) {
@@ -446,10 +475,6 @@ int ensure_partials(ni_kv* kv, size_t bytes) {
     return NI_OK;
 }
 
-struct Offsets {
-    size_t app, orphans, items, merges, pitems, pmerges, table, total;
-};
-
 Offsets layout(const Plan& P) {
     Offsets o;
     o.app = 0;
@@ -463,20 +488,9 @@ Offsets layout(const Plan& P) {
     return o;
 }
 
-// Where the kernels find this call's plan: in the launch arguments (small
-// plans) or in a staging slot uploaded on the copy stream.
-struct PlanRef {
-    const void* inl = nullptr;
-    uint32_t inl_bytes = 0;
-    const uint8_t* dev = nullptr;
-    StagingSlot* slot = nullptr;
-};
-
-// Serialise the plan and make it reachable from `s`.
-int place_plan(ni_kv* kv, hipStream_t s, Offsets* off, PlanRef* ref) {
-    const Plan& P = kv->plan;
+// Serialise plan P into `blob` and make it reachable from `s`.
+int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t s, Offsets* off, PlanRef* ref) {
     *off = layout(P);
-    auto& blob = kv->blob;
     blob.resize(off->total);
     if (!P.app.empty()) memcpy(blob.data() + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
     if (!P.orphans.empty())
@@ -522,11 +536,12 @@ int release_plan(ni_kv* kv, const PlanRef& ref, hipStream_t s) {
     return NI_OK;
 }
 
-// Append + attention + merge over an already built plan.
-int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const float* v, int64_t kv_row_stride,
-             int64_t kv_layer_stride, const float* q, int64_t q_row_stride, int64_t q_layer_stride, float* out,
-             int64_t out_row_stride, int64_t out_layer_stride, hipStream_t s) {
-    Plan& P = kv->plan;
+// Append + attention + merge of layers layer0 .. layer0+n_lay-1 over plan P,
+// already placed (off, ref).
+int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref, uint32_t layer0, uint32_t n_lay,
+               const float* k, const float* v, int64_t kv_row_stride, int64_t kv_layer_stride, const float* q,
+               int64_t q_row_stride, int64_t q_layer_stride, float* out, int64_t out_row_stride,
+               int64_t out_layer_stride, hipStream_t s) {
     const uint32_t D = kv->o.head_dim, H = kv->o.n_head;
     // Partials: the single-row/group launch's slots, then the prefill launch's.
     const size_t main_floats = (size_t)P.n_slots * n_lay * H * P.nq_tile * (D + 2);
@@ -535,10 +550,6 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
         int rc = ensure_partials(kv, (main_floats + pre_floats) * sizeof(float));
         if (rc) return rc;
     }
-    Offsets off;
-    PlanRef ref;
-    int rc = place_plan(kv, s, &off, &ref);
-    if (rc) return rc;
     if (!P.app.empty() && !P.fused) {
         AppendLaunch a;
         a.pool = kv->geom();
@@ -629,7 +640,23 @@ int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const f
             if (e != hipSuccess) return kv->hip_fail(e, "prefill merge kernel");
         }
     }
-    return release_plan(kv, ref, s);
+    return NI_OK;
+}
+
+// Place kv->plan and run it over layers layer0 .. layer0+n_lay-1.
+int run_plan(ni_kv* kv, uint32_t layer0, uint32_t n_lay, const float* k, const float* v, int64_t kv_row_stride,
+             int64_t kv_layer_stride, const float* q, int64_t q_row_stride, int64_t q_layer_stride, float* out,
+             int64_t out_row_stride, int64_t out_layer_stride, hipStream_t s) {
+    Offsets off;
+    PlanRef ref;
+    int rc = place_plan(kv, kv->plan, kv->blob, s, &off, &ref);
+    if (rc) return rc;
+    rc = run_placed(kv, kv->plan, off, ref, layer0, n_lay, k, v, kv_row_stride, kv_layer_stride, q, q_row_stride,
+                    q_layer_stride, out, out_row_stride, out_layer_stride, s);
+    // Even after a failed launch: the slot is reused only once this point
+    // of the stream is reached.
+    int rc2 = release_plan(kv, ref, s);
+    return rc ? rc : rc2;
 }
 
 void reset_plan(ni_kv* kv) {
@@ -642,6 +669,8 @@ void reset_plan(ni_kv* kv) {
 static int enqueue_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
                         const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
                         int64_t out_layer_stride, uint32_t split_tokens, hipStream_t stream);
+static int prepare_step(ni_kv* kv, const ni_work* work, uint32_t n_work);
+static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t split_tokens, uint32_t n_lay);
 
 // ============================================================= C ABI
 
@@ -784,6 +813,7 @@ int ni_kv_add_seq(ni_kv* kv, uint32_t* seq) {
 
 int ni_kv_free_seq(ni_kv* kv, uint32_t s) {
     if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->step.open) return kv->fail(NI_ERR_BAD_ARG, "a step begun by ni_kv_step_begin is still open");
     if (int rc = check_seq(kv, s)) return rc;
     truncate_seq(kv, s, 0);
     kv->live[s] = 0;
@@ -806,6 +836,7 @@ int ni_kv_is_live(const ni_kv* kv, uint32_t s, int* live) {
 
 int ni_kv_truncate(ni_kv* kv, uint32_t s, uint32_t len) {
     if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->step.open) return kv->fail(NI_ERR_BAD_ARG, "a step begun by ni_kv_step_begin is still open");
     if (int rc = check_seq(kv, s)) return rc;
     return truncate_seq(kv, s, len);
 }
@@ -819,6 +850,7 @@ int ni_kv_reserve(ni_kv* kv, uint32_t s, uint32_t len) {
 
 int ni_kv_commit(ni_kv* kv, uint32_t s, uint32_t n) {
     if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->step.open) return kv->fail(NI_ERR_BAD_ARG, "a step begun by ni_kv_step_begin is still open");
     if (int rc = check_seq(kv, s)) return rc;
     if (!kv->live[s]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", s);
     const uint64_t len = (uint64_t)kv->seq_len[s] + n;
@@ -904,7 +936,7 @@ static int qkv_run(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, con
         }
     Offsets off;
     PlanRef ref;
-    if (int rc = place_plan(kv, s, &off, &ref)) return rc;
+    if (int rc = place_plan(kv, kv->plan, kv->blob, s, &off, &ref)) return rc;
     QkvLaunch q;
     q.pool = kv->geom();
     q.x = x;
@@ -965,7 +997,7 @@ int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint1
     Offsets off;
     PlanRef ref;
     hipStream_t s = (hipStream_t)stream;
-    if (int rc = place_plan(kv, s, &off, &ref)) return rc;
+    if (int rc = place_plan(kv, kv->plan, kv->blob, s, &off, &ref)) return rc;
     GatherLaunch g;
     g.pool = kv->geom();
     g.k_out = k_out;
@@ -1004,7 +1036,7 @@ int ni_kv_gather_q8(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, in
     Offsets off;
     PlanRef ref;
     hipStream_t s = (hipStream_t)stream;
-    if (int rc = place_plan(kv, s, &off, &ref)) return rc;
+    if (int rc = place_plan(kv, kv->plan, kv->blob, s, &off, &ref)) return rc;
     GatherQ8Launch g;
     g.pool = kv->geom();
     g.k_out = k_out;
@@ -1060,32 +1092,78 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
         if (int rc = check_f32_operand(kv, "q", q, row_stride, layer_stride, true)) return rc;
         if (int rc = check_f32_operand(kv, "out", out, out_row_stride, out_layer_stride, true)) return rc;
     }
-    reset_plan(kv);
-    if (++kv->step_stamp == 0) {  // stamps wrapped: forget every old mark
-        std::fill(kv->step_mark.begin(), kv->step_mark.end(), 0u);
-        kv->step_stamp = 1;
-    }
-    // Batch::encode_step (batch.rs:280-305): check each item, grow its pages,
-    // lay out its rows.
-    uint64_t n_rows = 0;
-    for (uint32_t w = 0; w < n_work; w++) {
-        const ni_work& it = work[w];
-        if (int rc = check_seq(kv, it.seq)) return rc;
-        if (!kv->live[it.seq]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", it.seq);
-        if (it.n_new == 0) return kv->fail(NI_ERR_EMPTY_WORK, "empty work item");
-        if (it.n_query > it.n_new)
-            return kv->fail(NI_ERR_BAD_ARG, "work item %u: n_query %u > n_new %u", w, it.n_query, it.n_new);
-        if (kv->step_mark[it.seq] == kv->step_stamp)
-            return kv->fail(NI_ERR_BAD_ARG, "sequence %u appears twice in one step", it.seq);
-        kv->step_mark[it.seq] = kv->step_stamp;
-        const uint32_t len = kv->seq_len[it.seq];
-        if (int rc = ensure_pages(kv, it.seq, (uint64_t)len + it.n_new)) return rc;
-        n_rows += it.n_new;
-    }
-    if (n_rows > kv->o.max_rows)
-        return kv->fail(NI_ERR_TOO_MANY_ROWS, "%llu rows > max_rows %u", (unsigned long long)n_rows, kv->o.max_rows);
+    if (kv->step.open) return kv->fail(NI_ERR_BAD_ARG, "a step begun by ni_kv_step_begin is still open");
+    if (int rc = prepare_step(kv, work, n_work)) return rc;
     return enqueue_step(kv, work, n_work, q, k, v, row_stride, layer_stride, out, out_row_stride, out_layer_stride,
                         split_tokens, (hipStream_t)stream);
+}
+
+int ni_kv_step_begin(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t split_tokens) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->step.open) return kv->fail(NI_ERR_BAD_ARG, "a step is already open");
+    if (n_work && !work) return kv->fail(NI_ERR_BAD_ARG, "work is NULL");
+    if (int rc = prepare_step(kv, work, n_work)) return rc;
+    // Partitions and launch shape for one layer per launch.
+    if (int rc = build_step_plan(kv, work, n_work, split_tokens, 1)) return rc;
+    auto& st = kv->step;
+    std::swap(st.plan, kv->plan);
+    kv->plan.clear();
+    st.commit.clear();
+    for (uint32_t w = 0; w < n_work; w++) st.commit.push_back({work[w].seq, work[w].n_new});
+    st.placed = false;
+    st.ref = PlanRef{};
+    st.stream = nullptr;
+    st.open = true;
+    return NI_OK;
+}
+
+int ni_kv_step_layer(ni_kv* kv, int32_t layer, const float* q, const float* k, const float* v, int64_t row_stride,
+                     float* out, int64_t out_row_stride, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    auto& st = kv->step;
+    if (!st.open) return kv->fail(NI_ERR_BAD_ARG, "no step is open (ni_kv_step_begin)");
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    if (layer < 0 || (uint32_t)layer >= kv->o.n_layer)
+        return kv->fail(NI_ERR_BAD_ARG, "layer %d out of range (one layer per call)", layer);
+    const Plan& P = st.plan;
+    if (!P.app.empty()) {
+        if (int rc = check_f32_operand(kv, "k", k, row_stride, 0, false)) return rc;
+        if (int rc = check_f32_operand(kv, "v", v, row_stride, 0, false)) return rc;
+    }
+    if (!P.items.empty() || !P.pitems.empty()) {
+        if (int rc = check_f32_operand(kv, "q", q, row_stride, 0, false)) return rc;
+        if (int rc = check_f32_operand(kv, "out", out, out_row_stride, 0, false)) return rc;
+    }
+    const hipStream_t s = (hipStream_t)stream;
+    if (!st.placed) {
+        if (int rc = place_plan(kv, P, st.blob, s, &st.off, &st.ref)) return rc;
+        st.placed = true;
+        if (st.ref.slot) st.ref.slot->held = true;
+    } else if (st.ref.slot && s != st.stream) {
+        // A staged plan was uploaded for the first layer's stream.
+        hipError_t e = hipStreamWaitEvent(s, st.ref.slot->uploaded, 0);
+        if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
+    }
+    st.stream = s;
+    return run_placed(kv, P, st.off, st.ref, (uint32_t)layer, 1, k, v, row_stride, 0, q, row_stride, 0, out,
+                      out_row_stride, 0, s);
+}
+
+int ni_kv_step_end(ni_kv* kv) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    auto& st = kv->step;
+    if (!st.open) return kv->fail(NI_ERR_BAD_ARG, "no step is open (ni_kv_step_begin)");
+    st.open = false;
+    int rc = NI_OK;
+    if (st.placed) rc = release_plan(kv, st.ref, st.stream);
+    if (st.ref.slot) st.ref.slot->held = false;
+    st.placed = false;
+    st.ref = PlanRef{};
+    // batch.rs:270: the step's rows now belong to their sequences.
+    for (const auto& c : st.commit) kv->seq_len[c.first] += c.second;
+    st.commit.clear();
+    st.plan.clear();
+    return rc;
 }
 
 int ni_kv_decode_steps(ni_kv* kv, const uint32_t* seqs, uint32_t n, uint32_t steps, const float* q, const float* k,
@@ -1093,6 +1171,7 @@ int ni_kv_decode_steps(ni_kv* kv, const uint32_t* seqs, uint32_t n, uint32_t ste
                        int64_t out_row_stride, int64_t out_layer_stride, int64_t out_step_stride,
                        uint32_t split_tokens, ni_stream stream) {
     if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->step.open) return kv->fail(NI_ERR_BAD_ARG, "a step begun by ni_kv_step_begin is still open");
     if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
     if (n == 0 || steps == 0) return NI_OK;
     if (!seqs) return kv->fail(NI_ERR_BAD_ARG, "seqs is NULL");
@@ -1140,9 +1219,36 @@ int ni_kv_decode_steps(ni_kv* kv, const uint32_t* seqs, uint32_t n, uint32_t ste
 
 // The launch half of ni_kv_step: lay out the validated, reserved work's rows,
 // plan, launch, and commit seq_len += n_new (batch.rs:270).
-static int enqueue_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
-                        const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
-                        int64_t out_layer_stride, uint32_t split_tokens, hipStream_t stream) {
+// Batch::encode_step (batch.rs:280-305): check each item, grow its pages.
+static int prepare_step(ni_kv* kv, const ni_work* work, uint32_t n_work) {
+    if (++kv->step_stamp == 0) {  // stamps wrapped: forget every old mark
+        std::fill(kv->step_mark.begin(), kv->step_mark.end(), 0u);
+        kv->step_stamp = 1;
+    }
+    uint64_t n_rows = 0;
+    for (uint32_t w = 0; w < n_work; w++) {
+        const ni_work& it = work[w];
+        if (int rc = check_seq(kv, it.seq)) return rc;
+        if (!kv->live[it.seq]) return kv->fail(NI_ERR_NOT_LIVE, "sequence %u is not live", it.seq);
+        if (it.n_new == 0) return kv->fail(NI_ERR_EMPTY_WORK, "empty work item");
+        if (it.n_query > it.n_new)
+            return kv->fail(NI_ERR_BAD_ARG, "work item %u: n_query %u > n_new %u", w, it.n_query, it.n_new);
+        if (kv->step_mark[it.seq] == kv->step_stamp)
+            return kv->fail(NI_ERR_BAD_ARG, "sequence %u appears twice in one step", it.seq);
+        kv->step_mark[it.seq] = kv->step_stamp;
+        const uint32_t len = kv->seq_len[it.seq];
+        if (int rc = ensure_pages(kv, it.seq, (uint64_t)len + it.n_new)) return rc;
+        n_rows += it.n_new;
+    }
+    if (n_rows > kv->o.max_rows)
+        return kv->fail(NI_ERR_TOO_MANY_ROWS, "%llu rows > max_rows %u", (unsigned long long)n_rows, kv->o.max_rows);
+    return NI_OK;
+}
+
+// The step's rows (batch.rs:300-306: sequence s's n_new rows at positions
+// seq_len .. seq_len+n_new-1) and its plan in kv->plan, partitioned for
+// launches of n_lay layers.
+static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t split_tokens, uint32_t n_lay) {
     reset_plan(kv);
     // Fuse the append into the attention launch when every sequence has a
     // single query group: then exactly one workgroup per (layer, head, page)
@@ -1164,7 +1270,13 @@ static int enqueue_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const f
             if (i >= it.n_new - it.n_query) kv->qrows.push_back({row, it.seq, pos, len, len + it.n_new, first});
         }
     }
-    if (int rc = plan_attention(kv, split_tokens, kv->o.n_layer)) return rc;
+    return plan_attention(kv, split_tokens, n_lay);
+}
+
+static int enqueue_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
+                        const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
+                        int64_t out_layer_stride, uint32_t split_tokens, hipStream_t stream) {
+    if (int rc = build_step_plan(kv, work, n_work, split_tokens, kv->o.n_layer)) return rc;
     int rc = run_plan(kv, 0, kv->o.n_layer, k, v, row_stride, layer_stride, q, row_stride, layer_stride, out,
                       out_row_stride, out_layer_stride, stream);
     if (rc) return rc;

@@ -3,8 +3,12 @@
 // loop (`spec`) on the device, launched per step or per layer, printed as
 // one JSON line.
 //
-//   ni_drive [serve|spec|qkv|prefill] [--per-layer] [--steps K] [--warmup W] [--split T]
-//            [--all-prompt-rows] [--seed S] [--rows N] [--q8]
+//   ni_drive [serve|spec|qkv|prefill] [--per-layer|--step-layers] [--steps K] [--warmup W]
+//            [--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]
+//
+// --per-layer: ni_kv_append + ni_paged_decode_attention per layer;
+// --step-layers: ni_kv_step_begin, one ni_kv_step_layer per layer,
+// ni_kv_step_end; neither: one ni_kv_step per iteration (all layers).
 //
 // prefill: 16 sequences append and attend N-row prompts (default 512) from
 // empty, every row queried, rolled back each iteration.
@@ -43,14 +47,15 @@ int main(int argc, char** argv) {
         else if (!strcmp(a, "--rows")) o.qkv_rows = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--q8")) q8 = true;
         else if (!strcmp(a, "--per-layer")) o.launch = NI_DRIVE_PER_LAYER;
+        else if (!strcmp(a, "--step-layers")) o.launch = NI_DRIVE_STEP_LAYERS;
         else if (!strcmp(a, "--all-prompt-rows")) o.serve.query_all_prompt_rows = 1;
         else if (!strcmp(a, "--steps")) o.steps = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--warmup")) o.warmup = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--split")) o.split_tokens = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--seed")) o.data_seed = o.serve.seed = strtoull(val(a), nullptr, 10);
         else {
-            fprintf(stderr, "usage: ni_drive [serve|spec|qkv|prefill] [--per-layer] [--steps K] [--warmup W] [--split T] "
-                            "[--all-prompt-rows] [--seed S] [--rows N] [--q8]\n");
+            fprintf(stderr, "usage: ni_drive [serve|spec|qkv|prefill] [--per-layer|--step-layers] [--steps K] [--warmup W] "
+                            "[--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]\n");
             return 2;
         }
     }
@@ -115,7 +120,7 @@ int main(int argc, char** argv) {
            "\"gpu_ms_per_step\": %.5f, \"host_us_per_step\": %.1f, \"abi_calls_per_step\": %.1f, "
            "\"seq_tokens_per_s\": %.1f, \"algorithmic_bytes_per_step\": %.0f, \"mean_live\": %.2f, "
            "\"mean_context\": %.1f, \"kv\": \"%s\"}\n",
-           workload.c_str(), o.launch == NI_DRIVE_STEP ? "step" : "per-layer", r.steps, o.warmup, gbs,
+           workload.c_str(), o.launch == NI_DRIVE_STEP ? "step" : o.launch == NI_DRIVE_PER_LAYER ? "per-layer" : "step-layers", r.steps, o.warmup, gbs,
            100.0 * gbs / 8000.0, r.seconds / r.steps * 1e3, r.gpu_seconds / r.steps * 1e3, r.host_us_per_step,
            (double)r.launches / r.steps, r.seq_tokens / r.seconds, r.bytes / r.steps, r.mean_live, r.mean_context, q8 ? "q8" : "f16");
     return 0;

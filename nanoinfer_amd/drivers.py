@@ -51,7 +51,7 @@ class ni_drive_result(C.Structure):
 
 
 NI_DRIVE_SERVE, NI_DRIVE_SPEC, NI_DRIVE_FIXED, NI_DRIVE_QKV = 0, 1, 2, 3
-NI_DRIVE_STEP, NI_DRIVE_PER_LAYER = 0, 1
+NI_DRIVE_STEP, NI_DRIVE_PER_LAYER, NI_DRIVE_STEP_LAYERS = 0, 1, 2
 
 
 def lib():

@@ -128,12 +128,21 @@ def step_rows(kv, work):
     return np.asarray(rows, np.uint32).reshape(-1, 2), np.asarray(qrows, np.int64)
 
 
-def mirror_step(m: "Mirror", work, q: np.ndarray, k: np.ndarray, v: np.ndarray, split_tokens: int = 0):
-    """ni_kv_step on the device and the same step on the oracle; returns
-    (device out, oracle out, queried rows)."""
+def mirror_step(m: "Mirror", work, q: np.ndarray, k: np.ndarray, v: np.ndarray, split_tokens: int = 0,
+                per_layer: bool = False):
+    """ni_kv_step on the device (per_layer: ni_kv_step_begin, one
+    ni_kv_step_layer per layer, ni_kv_step_end) and the same step on the
+    oracle; returns (device out, oracle out, queried rows)."""
     rows, qrows = step_rows(m.kv, work)
-    out = m.kv.step(work, torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
-                    split_tokens=split_tokens)
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+    if per_layer:
+        out = torch.zeros_like(qd)
+        m.kv.step_begin(work, split_tokens=split_tokens)
+        for l in range(m.opts.n_layer):
+            m.kv.step_layer(l, qd[l], kd[l], vd[l], out=out[l])
+        m.kv.step_end()
+    else:
+        out = m.kv.step(work, qd, kd, vd, split_tokens=split_tokens)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     t = m.table()

@@ -95,14 +95,16 @@ def test_truncate_rollback_matches_sequential(gpu):
     assert np.array_equal(out, want)
 
 
+@pytest.mark.parametrize("per_layer", [False, True], ids=["all_layers", "per_layer"])
 @pytest.mark.parametrize("prefill_queries", ["all", "last"])
-def test_continuous_batching_trace(gpu, oracle_lib, prefill_queries):
+def test_continuous_batching_trace(gpu, oracle_lib, prefill_queries, per_layer):
     """Scaled config 3: Poisson arrivals, admission by free pages, decode rows
     plus budgeted prefill chunks, retire and reuse pages; every step checked
     against the oracle.  "all": attention at every prefill row (many query
     groups per sequence, separate append launch); "last": only the row that
     ends a prompt (the append fused into the attention launch, mid-prompt
-    chunks appended by the launch's extra blocks)."""
+    chunks appended by the launch's extra blocks).  per_layer: each step
+    planned once and run one launch per layer (ni_kv_step_layer)."""
     rng = np.random.default_rng(32)
     opts = gpt2(kv_blocks=160, max_seqs=8, max_rows=128)
     m = Mirror(opts)
@@ -113,7 +115,7 @@ def test_continuous_batching_trace(gpu, oracle_lib, prefill_queries):
         st = trace.plan()
         n = int(st.work[:, 1].sum())
         q, k, v = (rng.standard_normal((12, n, 768)).astype(np.float32) for _ in range(3))
-        got, want, qrows = mirror_step(m, st.work, q, k, v)
+        got, want, qrows = mirror_step(m, st.work, q, k, v, per_layer=per_layer)
         worst = max(worst, assert_close(got[:, qrows], want[:, qrows], f"step {step}"))
         trace.commit()
     say(f"continuous trace: {trace.done} retired, max abs err {worst:.2e}")
@@ -124,9 +126,11 @@ def test_continuous_batching_trace(gpu, oracle_lib, prefill_queries):
     assert np.array_equal(kg, kw) and np.array_equal(vg, vw)
 
 
-def test_spec_verify_trace(gpu, oracle_lib):
+@pytest.mark.parametrize("per_layer", [False, True], ids=["all_layers", "per_layer"])
+def test_spec_verify_trace(gpu, oracle_lib, per_layer):
     """Scaled config 5: append g + 4 drafts, 5 causal queries, accept
-    U[0,4], truncate; pages freed by rollback are reused."""
+    U[0,4], truncate; pages freed by rollback are reused.  per_layer: each
+    step planned once and run one launch per layer."""
     rng = np.random.default_rng(33)
     ctx, _ = workloads.config5_contexts(n_seqs=6, lo=20, hi=300)
     m = Mirror(gpt2(kv_blocks=200, max_seqs=6, n_ctx=1024))
@@ -138,7 +142,7 @@ def test_spec_verify_trace(gpu, oracle_lib):
         st = spec.plan()
         n = int(st.work[:, 1].sum())
         q, k, v = (rng.standard_normal((12, n, 768)).astype(np.float32) for _ in range(3))
-        got, want, qrows = mirror_step(m, st.work, q, k, v)
+        got, want, qrows = mirror_step(m, st.work, q, k, v, per_layer=per_layer)
         assert_close(got[:, qrows], want[:, qrows], f"spec step {step}")
         spec.commit()
     for s in seqs:

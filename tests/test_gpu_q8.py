@@ -169,10 +169,12 @@ def test_q8_large_values(gpu, oracle_lib, nq):
         say(f"q8 large values nq {nq} split {split}: max abs err {err:.3e}")
 
 
-def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib):
+@pytest.mark.parametrize("per_layer", [False, True], ids=["all_layers", "per_layer"])
+def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib, per_layer):
     """ni_kv_step on a Q8 cache: decode rows, a prompt chunk queried at its
     last row, a 5-row verify group and a mid-prompt chunk (no query), all in
-    one fused launch; then truncate, free and reuse pages."""
+    one fused launch (per_layer: one per layer over one plan); then
+    truncate, free and reuse pages."""
     rng = np.random.default_rng(92)
     m = MirrorQ8(opts(workloads.GPT2, n_layer=3))
     a, b, c, d = (m.kv.add_seq() for _ in range(4))
@@ -183,7 +185,16 @@ def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib):
         rows, qrows = step_rows(m.kv, work)
         n = len(rows)
         q, k, v = (rng.standard_normal((3, n, m.c)).astype(np.float32) for _ in range(3))
-        got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v))).cpu().numpy()
+        qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+        if per_layer:
+            out = torch.zeros_like(qd)
+            m.kv.step_begin(work)
+            for l in (2, 0, 1):  # any order
+                m.kv.step_layer(l, qd[l], kd[l], vd[l], out=out[l])
+            m.kv.step_end()
+            got = out.cpu().numpy()
+        else:
+            got = m.kv.step(work, qd, kd, vd).cpu().numpy()
         # the oracle appends with the tables the step reserved
         m.append_oracle(rows, k, v)
         want = m.attention_oracle(rows[qrows], q[:, qrows])

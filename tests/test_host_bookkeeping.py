@@ -124,3 +124,40 @@ def test_commit_past_reserve_is_refused():
     assert e.value.code == _abi.NI_ERR_NOT_RESERVED
     kv.commit(s, 16)
     assert kv.seq_len(s) == 16
+
+
+def test_per_layer_step_bookkeeping():
+    """ni_kv_step_begin / _end on a host-only handle: begin reserves like
+    ni_kv_step (the same errors, nothing open after one), end commits
+    seq_len += n_new, and while a step is open the calls that free pages or
+    move seq_len are refused, as is a second begin; a layer call needs the
+    device."""
+    kv, ref = make(16, 4, 160)
+    a, b = kv.add_seq(), kv.add_seq()
+    kv.reserve(a, 20)
+    kv.commit(a, 20)
+    with pytest.raises(na.KvError) as e:
+        kv.step_end()
+    assert "no step is open" in str(e.value)
+    kv.step_begin([(a, 1, 1), (b, 37, 37)])
+    assert kv.seq_len(a) == 20 and kv.seq_len(b) == 0
+    assert len(kv.block_table(a)) == 2 and len(kv.block_table(b)) == 3
+    for call in (lambda: kv.step_begin([(a, 1, 1)]), lambda: kv.truncate(a, 0), lambda: kv.free_seq(b),
+                 lambda: kv.commit(a, 1)):
+        with pytest.raises(na.KvError) as e:
+            call()
+        assert e.value.code == _abi.NI_ERR_BAD_ARG and "open" in str(e.value)
+    with pytest.raises(na.KvError) as e:
+        kv._check(kv._L.ni_kv_step_layer(kv._h, 0, None, None, None, 0, None, 0, None))
+    assert e.value.code == _abi.NI_ERR_NO_DEVICE
+    kv.step_end()
+    assert kv.seq_len(a) == 21 and kv.seq_len(b) == 37
+    # The reference's errors on begin; nothing stays open after them.
+    with pytest.raises(na.KvError) as e:
+        kv.step_begin([(a, 200, 1)])
+    assert e.value.code == _abi.NI_ERR_CONTEXT_FULL
+    with pytest.raises(na.KvError) as e:
+        kv.step_begin([(3, 1, 1)])
+    assert e.value.code == _abi.NI_ERR_NOT_LIVE
+    kv.truncate(a, 5)
+    assert kv.seq_len(a) == 5 and len(kv.block_table(a)) == 1
