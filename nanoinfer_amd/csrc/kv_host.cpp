@@ -37,6 +37,10 @@ constexpr uint32_t kRingSlots = 4;
 // Plans are uploaded on the handle's own copy stream and the caller's stream
 // waits for the upload with an event, so the copy overlaps the previous
 // step's kernels instead of sitting between them.
+// 1: every plan goes through the staging ring (none in the kernel arguments).
+#ifndef NI_STAGE_ALL_PLANS
+#define NI_STAGE_ALL_PLANS 0
+#endif
 #ifndef NI_PLAN_COPY_STREAM
 #define NI_PLAN_COPY_STREAM 1
 #endif
@@ -502,7 +506,7 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
         memcpy(blob.data() + off->pmerges, P.pmerges.data(), P.pmerges.size() * sizeof(MergeItem));
     if (!P.table.empty()) memcpy(blob.data() + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
     *ref = PlanRef{};
-    if (off->total <= kInlinePlanBytes) {
+    if (!NI_STAGE_ALL_PLANS && off->total <= kInlinePlanBytes) {
         ref->inl = blob.data();
         ref->inl_bytes = (uint32_t)off->total;
         return NI_OK;
