@@ -192,3 +192,27 @@ def test_step_errors_match_reference(gpu):
     small.step([(a, 1, 1)], t1, t1, t1)  # b's page is reused
     assert small.seq_len(a) == 17
     small.sync()
+
+
+def test_per_layer_step_head_dim_128(gpu, oracle_lib):
+    """One launch per layer at head_dim 128 (config 4's head shape): decode
+    rows, a 5-row verify group, a queried 40-row prompt chunk (its own launch
+    on the prefill path) and a chunk with no query, over contexts that need
+    split-K partitions; every layer's output against the oracle and the
+    appended rows gathered bit for bit."""
+    rng = np.random.default_rng(51)
+    opts = na.BatchOpts(n_layer=3, n_head=4, head_dim=128, kv_blocks=400, max_seqs=6, n_ctx=4096, max_rows=256)
+    m = Mirror(opts)
+    seqs = [m.kv.add_seq() for _ in range(5)]
+    for s, L in zip(seqs, (1500, 700, 33, 0, 2100)):
+        if L:
+            m.fill(s, L, rng)
+    for rnd in range(2):
+        work = [(seqs[0], 1, 1), (seqs[1], 5, 5), (seqs[2], 40, 40), (seqs[3], 23, 0), (seqs[4], 1, 1)]
+        n = sum(w[1] for w in work)
+        q, k, v = (rng.standard_normal((3, n, m.c)).astype(np.float32) for _ in range(3))
+        got, want, qrows = mirror_step(m, work, q, k, v, split_tokens=512 if rnd else 0, per_layer=True)
+        assert_close(got[:, qrows], want[:, qrows], f"head_dim 128 per-layer round {rnd}")
+    rows = [(s, p) for s in seqs for p in range(m.kv.seq_len(s))]
+    (kg, vg), (kw, vw) = m.gather(rows)
+    assert np.array_equal(kg, kw) and np.array_equal(vg, vw)
