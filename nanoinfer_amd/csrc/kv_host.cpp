@@ -371,6 +371,8 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
             if (hi > lo) {
                 it.app0 = g.app_first + (lo - g.new_begin);
                 it.napp = hi - lo;
+                it.app_pos = lo;
+                it.app_src = P.app[it.app0].src_row;
                 P.napp_total += it.napp;
             }
         }

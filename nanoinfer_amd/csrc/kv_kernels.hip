@@ -321,16 +321,50 @@ struct PageRegs {
     u32x4 v[PB][LPP];
 };
 
+// A fused launch's new rows of one item, (layer, head): positions pos ..
+// pos+n-1, K/V input rows k/v + (p - pos) * row_stride (already offset to the
+// lane's 8 dims).  The wave that streams their page takes them from the input
+// (converted as the append converts them), stores them to the pool and uses
+// them: no separate append before the attention, no barrier.
+struct NewRows {
+    const float* k;
+    const float* v;
+    int64_t row_stride;
+    uint32_t pos, n;
+};
+
 template <int PB, int LPP>
 __device__ __forceinline__ void load_pages(PageRegs<PB, LPP>& r, const uint32_t* __restrict__ tab, uint32_t pg,
                                            uint32_t pg_end, const uint16_t* __restrict__ kbase,
-                                           const uint16_t* __restrict__ vbase, uint64_t page_stride, int lane) {
+                                           const uint16_t* __restrict__ vbase, uint64_t page_stride, int lane,
+                                           const NewRows& nr, int kl) {
+    constexpr uint32_t KPL = kPage / LPP;  // key rows per load
 #pragma unroll
     for (int b = 0; b < PB; b++) {
         if (pg + b < pg_end) {
             const uint64_t phys = tab[pg + b];
             const u32x4* kp = reinterpret_cast<const u32x4*>(kbase + phys * page_stride) + lane;
             const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
+            const uint32_t p0 = (pg + b) * kPage;
+            if (nr.n && p0 < nr.pos + nr.n && p0 + kPage > nr.pos) {  // wave-uniform: the page holds new rows
+#pragma unroll
+                for (int i = 0; i < LPP; i++) {
+                    const uint32_t d = p0 + i * KPL + kl - nr.pos;  // unsigned: >= n unless new
+                    if (d < nr.n) {
+                        const float4* ks = reinterpret_cast<const float4*>(nr.k + (int64_t)d * nr.row_stride);
+                        const float4* vs = reinterpret_cast<const float4*>(nr.v + (int64_t)d * nr.row_stride);
+                        const uint4 kw = pack8(ks[0], ks[1]), vw = pack8(vs[0], vs[1]);
+                        *const_cast<uint4*>(reinterpret_cast<const uint4*>(kp + i * 64)) = kw;
+                        *const_cast<uint4*>(reinterpret_cast<const uint4*>(vp + i * 64)) = vw;
+                        r.k[b][i] = u32x4{kw.x, kw.y, kw.z, kw.w};
+                        r.v[b][i] = u32x4{vw.x, vw.y, vw.z, vw.w};
+                    } else {
+                        r.k[b][i] = load16(kp + i * 64);
+                        r.v[b][i] = load16(vp + i * 64);
+                    }
+                }
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < LPP; i++) {
                 r.k[b][i] = load16(kp + i * 64);
@@ -395,17 +429,27 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
     const uint32_t full_end = min(it.pos0 + 1, it.kv_end);
     constexpr uint32_t STRIDE = W * PB;
 
+    // Fused, head_dim 64: the item's new rows come from the k/v input as
+    // their pages stream.  head_dim 128 appends them first (streaming them
+    // costs 37 registers there, a wave per SIMD).
+    NewRows nr{};
     if constexpr (FUSED) {
         if (it.napp) {
-            item_append<D>(a, plan, it, lay, head, layer_off, page_stride, 64 * W);
-            __syncthreads();
+            if constexpr (D == 64) {
+                const int64_t off =
+                    (int64_t)lay * a.kv_layer_stride + (int64_t)it.app_src * a.kv_row_stride + head * D + ds * 8;
+                nr = NewRows{a.k + off, a.v + off, a.kv_row_stride, it.app_pos, it.napp};
+            } else {
+                item_append<D>(a, plan, it, lay, head, layer_off, page_stride, 64 * W);
+                __syncthreads();
+            }
         }
     }
 
     // First pages in flight before the query loads.
     PageRegs<PB, LPP> cur;
     uint32_t pg = pg_begin + wave * PB;
-    if (pg < pg_end) load_pages(cur, tab, pg, pg_end, kbase, vbase, page_stride, lane);
+    if (pg < pg_end) load_pages(cur, tab, pg, pg_end, kbase, vbase, page_stride, lane, nr, kl);
 
     float q[NQ][8];
     {
@@ -437,7 +481,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
     for (; pg < pg_end; pg += STRIDE) {
 #if NI_ATTN_PREFETCH
         PageRegs<PB, LPP> nxt;
-        if (pg + STRIDE < pg_end) load_pages(nxt, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane);
+        if (pg + STRIDE < pg_end) load_pages(nxt, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane, nr, kl);
 #endif
         float s[NQ][PB][LPP];
 #pragma unroll
@@ -498,7 +542,7 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
 #if NI_ATTN_PREFETCH
         cur = nxt;
 #else
-        if (pg + STRIDE < pg_end) load_pages(cur, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane);
+        if (pg + STRIDE < pg_end) load_pages(cur, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane, nr, kl);
 #endif
     }
 

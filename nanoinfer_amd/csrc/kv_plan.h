@@ -59,8 +59,10 @@ struct AttnItem {
     uint32_t kv_end;    // one past the last key: min(partition end, pos0 + nq)
     uint32_t part_slot; // partial-result slot, or kNoSlot (write out directly)
     uint32_t app0;      // fused launches: first append entry of this step's new
-    uint32_t napp;      //   rows inside [kv_begin, kv_end), and their count
-    uint32_t pad[3];
+    uint32_t napp;      //   rows inside [kv_begin, kv_end), and their count,
+    uint32_t app_pos;   //   the position of the first of them
+    uint32_t app_src;   //   and its k/v input row (the others follow consecutively)
+    uint32_t pad;
 };
 
 // A group split into n_parts partitions, merged by log-sum-exp.
