@@ -12,7 +12,8 @@
 //   kv_gather_kernel   page slots -> f16 rows in the reference layout (kv_slot reads, :24-26)
 //   attn_split_kernel  paged flash-decoding of single query rows, one workgroup
 //                      per (item, layer, head) (b_attn_split, batch.metal:349-400),
-//                      with the step's append fused into its prologue
+//                      with the step's append fused in (head_dim 64: the new
+//                      rows taken from the input as their pages stream)
 //   attn_mfma_kernel   the same for groups of 2..16 causal query rows of one
 //                      sequence, on the matrix cores
 //   attn_prefill_kernel  groups of 17..64 rows (prompt chunks), K/V tiles DMA'd
