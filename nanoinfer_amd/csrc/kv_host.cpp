@@ -37,6 +37,11 @@ constexpr uint32_t kRingSlots = 4;
 // Plans are uploaded on the handle's own copy stream and the caller's stream
 // waits for the upload with an event, so the copy overlaps the previous
 // step's kernels instead of sitting between them.
+// Query groups (matrix-core kernel) take wide workgroups from this many
+// (item, layer, head) units on, instead of splitting into partitions.
+#ifndef NI_WIDE_MIN_GROUP_UNITS
+#define NI_WIDE_MIN_GROUP_UNITS 256
+#endif
 // 1: every plan goes through the staging ring (none in the kernel arguments).
 #ifndef NI_STAGE_ALL_PLANS
 #define NI_STAGE_ALL_PLANS 0
@@ -311,20 +316,25 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     // Between kWideMinUnits and kFillWorkgroups units of single-row items
     // (head_dim 64: a launch of one layer of 43..170 sequences), workgroups
     // of kWideWaves waves share each item's pages instead of splitting it:
-    // no partials, no merge launch.
+    // no partials, no merge launch.  Query groups of up to one matrix tile
+    // (a verify step's rows) do the same from kWideMinGroupUnits units.
     uint32_t part = split_tokens;
     if (part == 0) {
         constexpr uint64_t kFillWorkgroups = 2048;
         constexpr uint64_t kWideMinUnits = 512;
+        constexpr uint64_t kWideMinGroupUnits = NI_WIDE_MIN_GROUP_UNITS;
         constexpr uint32_t kLongItem = 4096;
         static const uint32_t kChoices[] = {1024, 512, 256, 128};
         const uint64_t per_unit = (uint64_t)n_lay * kv->o.n_head;
         const uint64_t units = (uint64_t)groups.size() * per_unit;
-        bool single = true;
-        for (const Group& g : groups) single &= g.nq == 1;
+        bool single = true, tiles = true;  // every group one row; every group within one matrix tile
+        for (const Group& g : groups) {
+            single &= g.nq == 1;
+            tiles &= g.nq <= kMfmaTile;
+        }
         if (units >= kFillWorkgroups) {
             part = kLongItem;
-        } else if (single && units >= kWideMinUnits && kv->o.head_dim == 64) {
+        } else if (tiles && units >= (single ? kWideMinUnits : kWideMinGroupUnits) && kv->o.head_dim == 64) {
             part = kLongItem;
             P.wide = true;
         } else {

@@ -1989,6 +1989,18 @@ template <int D, bool Q8>
 hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
+    if constexpr (D == 64) {
+        if (a.wide) {  // kWideWaves waves share each item's pages
+            constexpr int WW = kWideWaves;
+            return with_plan(a, ip, ib, [&](auto pa) {
+                constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+                if (a.napp_total || a.n_orphan_blocks)
+                    return go(attn_mfma_kernel<D, WW, kMfmaPages, true, INL, Q8>, blocks, 64 * WW, s, t, a, pa);
+                return go(attn_mfma_kernel<D, WW, kMfmaPages, false, INL, Q8>, blocks, 64 * WW, s, t, a, pa);
+            });
+        }
+    }
+    if (a.wide) return hipErrorInvalidValue;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         if (a.napp_total || a.n_orphan_blocks)

@@ -59,11 +59,13 @@ def test_config3_full_size_trace(gpu, oracle_lib):
         f"max abs err {worst:.2e}")
 
 
-def test_config5_full_size_trace(gpu, oracle_lib):
+@pytest.mark.parametrize("per_layer", [False, True], ids=["all_layers", "per_layer"])
+def test_config5_full_size_trace(gpu, oracle_lib, per_layer):
     """Config 5: 32 sequences with contexts U[128, 1024] (the benchmark's
     seed), each step appending g + 4 drafts and querying them as one causal
     5-row group, accepting U[0,4] and truncating the rest.  5 steps against
-    the oracle."""
+    the oracle.  per_layer: one launch per layer, whose 384 (item, head)
+    units run on 8-wave workgroups sharing each item's pages."""
     rng = np.random.default_rng(42)
     ctx, _ = workloads.config5_contexts()
     m = Mirror(na.BatchOpts(**workloads.GPT2, kv_blocks=2400, max_seqs=32, n_ctx=1104, max_rows=512))
@@ -77,7 +79,7 @@ def test_config5_full_size_trace(gpu, oracle_lib):
         n = int(st.work[:, 1].sum())
         assert n == 5 * len(seqs)
         q, k, v = (rng.standard_normal((12, n, m.c)).astype(np.float32) for _ in range(3))
-        got, want, qrows = mirror_step(m, st.work, q, k, v)
+        got, want, qrows = mirror_step(m, st.work, q, k, v, per_layer=per_layer)
         worst = max(worst, assert_close(got[:, qrows], want[:, qrows], f"config 5 step {step}"))
         spec.commit()
         say(f"config 5 step {step}: max abs err {worst:.2e}")

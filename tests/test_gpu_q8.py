@@ -211,6 +211,31 @@ def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib, per_layer):
     assert_close(got, m.attention_oracle(rows, q), "after reuse")
 
 
+def test_q8_verify_groups_per_layer_wide(gpu, oracle_lib):
+    """A verify step on a Q8 cache one launch per layer: 24 sequences x 12
+    heads = 288 units of 5-row groups, enough for 8-wave workgroups sharing
+    each item's pages (no partitions); every layer against the oracle, then
+    the appended bytes."""
+    rng = np.random.default_rng(93)
+    m = MirrorQ8(opts(workloads.GPT2, n_layer=2, max_seqs=24, kv_blocks=800))
+    seqs = [m.kv.add_seq() for _ in range(24)]
+    for s in seqs:
+        m.fill(s, int(rng.integers(20, 400)), rng)
+    work = [(s, 5, 5) for s in seqs]
+    rows, qrows = step_rows(m.kv, work)
+    q, k, v = (rng.standard_normal((2, len(rows), m.c)).astype(np.float32) for _ in range(3))
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+    out = torch.zeros_like(qd)
+    m.kv.step_begin(work)
+    for l in range(2):
+        m.kv.step_layer(l, qd[l], kd[l], vd[l], out=out[l])
+    m.kv.step_end()
+    got = out.cpu().numpy()
+    m.append_oracle(rows, k, v)
+    assert_close(got[:, qrows], m.attention_oracle(rows[qrows], q[:, qrows]), "wide Q8 groups")
+    m.check_bytes(rows)
+
+
 def test_q8_refusals(gpu):
     kv = na.PagedKv(na.BatchOpts(n_layer=1, n_head=2, head_dim=64, kv_blocks=8, max_seqs=2, n_ctx=64, q8=True))
     s = kv.add_seq()
