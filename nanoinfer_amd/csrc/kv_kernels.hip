@@ -2030,7 +2030,7 @@ hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStre
     if (blocks == 0) return hipSuccess;
     if constexpr (D == 64) {
         if (a.wide) {
-            constexpr int WW = kWideWaves;
+            constexpr int WW = kWideWavesQ8;
             return with_plan(a, ip, ib, [&](auto pa) {
                 constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
                 constexpr int PB = NI_Q8_PAGES;
@@ -2142,7 +2142,9 @@ hipError_t launch_attention(const AttnLaunch& a, const void* ip, uint32_t ib, hi
 
 uint32_t orphan_blocks(const AttnLaunch& a) {
     const uint64_t threads = (uint64_t)a.n_lay * a.n_orphans * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);
-    const uint64_t per_block = 64ull * (a.wide ? kWideWaves : kWaves);
+    // Threads per workgroup of the launch the orphan blocks join.
+    const bool q8_rows = a.pool.q8 && a.nq_tile == 1;
+    const uint64_t per_block = 64ull * (a.wide ? (q8_rows ? kWideWavesQ8 : kWideWaves) : kWaves);
     return (uint32_t)((threads + per_block - 1) / per_block);
 }
 

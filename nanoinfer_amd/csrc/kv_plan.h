@@ -37,6 +37,12 @@ constexpr uint32_t kPrefillRows = 64;
 #define NI_WIDE_WAVES 8
 #endif
 constexpr uint32_t kWideWaves = NI_WIDE_WAVES;
+// The same for single rows on the Q8 cache (attn_q8_kernel), one layer per
+// launch config 3: 5 waves 2634 GB/s, 6 2602, 8 2444.
+#ifndef NI_Q8_WIDE_WAVES
+#define NI_Q8_WIDE_WAVES 5
+#endif
+constexpr uint32_t kWideWavesQ8 = NI_Q8_WIDE_WAVES;
 constexpr uint32_t kMaxGroupRows = NI_ATTN_MFMA ? kMfmaTile : 8;  // most query rows sharing one K/V stream
 
 // Where one appended row goes: pool page `page`, position `slot` (0..15) in it.

@@ -236,6 +236,39 @@ def test_q8_verify_groups_per_layer_wide(gpu, oracle_lib):
     m.check_bytes(rows)
 
 
+def test_q8_rows_per_layer_wide_with_orphans(gpu, oracle_lib):
+    """One launch per layer on a Q8 cache with 48 sequences x 12 heads = 576
+    units of single rows (wide workgroups sharing each item's pages): decode
+    rows, prompt chunks queried at their last row, and chunks of sequences
+    without a query (appended by the launch's extra blocks); every layer
+    against the oracle, then the stored bytes of every appended row."""
+    rng = np.random.default_rng(94)
+    m = MirrorQ8(opts(workloads.GPT2, n_layer=2, max_seqs=48, kv_blocks=1600))
+    seqs = [m.kv.add_seq() for _ in range(48)]
+    for i, s in enumerate(seqs):
+        if i % 6:
+            m.fill(s, int(rng.integers(16, 500)), rng)
+    for rnd in range(2):
+        work = []
+        for i, s in enumerate(seqs):
+            if i % 6 == 0:
+                work.append((s, 37, 1 if i % 12 else 0))  # a prompt chunk: queried at its last row, or not at all
+            else:
+                work.append((s, 1, 1))
+        rows, qrows = step_rows(m.kv, work)
+        q, k, v = (rng.standard_normal((2, len(rows), m.c)).astype(np.float32) for _ in range(3))
+        qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+        out = torch.zeros_like(qd)
+        m.kv.step_begin(work)
+        for l in range(2):
+            m.kv.step_layer(l, qd[l], kd[l], vd[l], out=out[l])
+        m.kv.step_end()
+        got = out.cpu().numpy()
+        m.append_oracle(rows, k, v)
+        assert_close(got[:, qrows], m.attention_oracle(rows[qrows], q[:, qrows]), f"wide Q8 rows round {rnd}")
+        m.check_bytes(rows)
+
+
 def test_q8_refusals(gpu):
     kv = na.PagedKv(na.BatchOpts(n_layer=1, n_head=2, head_dim=64, kv_blocks=8, max_seqs=2, n_ctx=64, q8=True))
     s = kv.add_seq()
