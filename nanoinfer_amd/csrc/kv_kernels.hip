@@ -1049,6 +1049,9 @@ constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f, kLog2PScale = 14.f
 #ifndef NI_MFMA_MIN_WAVES
 #define NI_MFMA_MIN_WAVES 4
 #endif
+#ifndef NI_MFMA_K_LDS
+#define NI_MFMA_K_LDS 1
+#endif
 // Q8: the pool holds int8 values with a scale per (position, head); K
 // values enter the products as f16 (int8 converts exactly), the key scale
 // multiplies the scores and the value scale multiplies p before its split.
@@ -1067,6 +1070,10 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     // Per-wave V tile, row major with tile_chunk's chunk swizzle: rows go in
     // with 16-byte writes, V^T comes out through transposing reads.
     __shared__ __attribute__((aligned(16))) _Float16 vt[W][PB * kPage * D];
+    // f16: K rows load coalesced (as V) and reach the A operand through a
+    // per-wave tile of the same layout.
+    constexpr bool KT = !Q8 && NI_MFMA_K_LDS;
+    __shared__ __attribute__((aligned(16))) _Float16 kt[KT ? W : 1][KT ? PB * kPage * D : 8];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1152,8 +1159,14 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 r.vs[b] = *reinterpret_cast<const float4*>(vb + kPage * D + 16 * rg);
             } else {
                 const uint16_t* kp = kbase + phys * page_stride + col * D + 8 * rg;
+                if constexpr (KT) {  // key i*KPL + lane/LPK, dims (lane%LPK)*8 (QC == LPP)
+                    const u32x4* kq = reinterpret_cast<const u32x4*>(kbase + phys * page_stride) + lane;
 #pragma unroll
-                for (int c = 0; c < QC; c++) r.k[b][c] = load16(reinterpret_cast<const u32x4*>(kp + c * 32));
+                    for (int c = 0; c < QC; c++) r.k[b][c] = load16(kq + c * 64);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < QC; c++) r.k[b][c] = load16(reinterpret_cast<const u32x4*>(kp + c * 32));
+                }
                 const u32x4* vp = reinterpret_cast<const u32x4*>(vbase + phys * page_stride) + lane;
 #pragma unroll
                 for (int i = 0; i < LPP; i++) r.v[b][i] = load16(vp + i * 64);
@@ -1223,8 +1236,17 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                         __builtin_shufflevector(v2, v3, 0, 1, 2, 3, 4, 5, 6, 7);
                 } else {
                     *reinterpret_cast<u32x4*>(my_vt + tile_chunk<CH>(key, lane % LPK) * 8) = val;
+                    if constexpr (KT) {
+                        const u32x4 kv = pg * kPage + key < it.kv_end ? cur.k[b][i] : u32x4{0, 0, 0, 0};
+                        *reinterpret_cast<u32x4*>(kt[wave] + tile_chunk<CH>(key, lane % LPK) * 8) = kv;
+                    }
                 }
             }
+        }
+        if constexpr (KT) {  // the K tile is read back by other lanes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         // S^T = K Q^T per page; scores of keys 4*rg+j of each page.
         float s[PB][4];
@@ -1238,6 +1260,8 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 if constexpr (Q8) {
                     const half4_t k0 = i8x4_f16(cur.k[b][c][0]), k1 = i8x4_f16(cur.k[b][c][1]);
                     kh = half8_t{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+                } else if constexpr (KT) {  // key col, dims c*32 + 8*rg .. +7
+                    kh = *reinterpret_cast<const half8_t*>(kt[wave] + tile_chunk<CH>(b * kPage + col, 4 * c + rg) * 8);
                 } else {
                     kh = __builtin_bit_cast(half8_t, cur.k[b][c]);
                 }
