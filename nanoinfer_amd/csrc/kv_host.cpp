@@ -119,6 +119,7 @@ struct PlanRef {
 struct QRow {
     uint32_t row, seq, pos;
     uint32_t new_begin, new_end, app_first;
+    uint32_t pre = 0;  // fused step: a prompt chunk queried at more rows than one matrix tile (prefill launch)
 };
 
 }  // namespace
@@ -290,6 +291,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     struct Group {
         uint32_t seq, row0, pos0, nq;
         uint32_t new_begin, new_end, app_first;
+        uint32_t pre;  // runs in the prefill launch whatever its size
     };
     std::vector<Group> groups;
     groups.reserve(qr.size());
@@ -304,7 +306,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
                 continue;
             }
         }
-        groups.push_back({r.seq, r.row, r.pos, 1, r.new_begin, r.new_end, r.app_first});
+        groups.push_back({r.seq, r.row, r.pos, 1, r.new_begin, r.new_end, r.app_first, r.pre});
     }
     // Partition size: the caller's, or (0) automatic.  Splitting costs a
     // merge launch (~5-7 us) and the partials' round trip, so it pays only
@@ -330,7 +332,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         bool single = true, tiles = true;  // every group one row; every group within one matrix tile
         for (const Group& g : groups) {
             single &= g.nq == 1;
-            tiles &= g.nq <= kMfmaTile;
+            tiles &= g.nq <= kMfmaTile && !g.pre;
         }
         if (units >= kFillWorkgroups) {
             part = kLongItem;
@@ -365,8 +367,8 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     }
     uint32_t max_nq = 1;
     // An item [b, e) of a fused step appends this call's new rows in [b, e).
-    // (Prefill groups only occur in unfused calls: a fused step has at most
-    // max_group_rows queries per sequence.)
+    // (In a fused step a sequence queried at more than max_group_rows rows
+    // forms prefill groups only; the launch's extra blocks append its rows.)
     auto item = [&](const Group& g, uint32_t tab, uint32_t b, uint32_t e, uint32_t slot) {
         AttnItem it{};
         it.tab = tab;
@@ -376,7 +378,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         it.kv_begin = b;
         it.kv_end = e;
         it.part_slot = slot;
-        if (P.fused) {
+        if (P.fused && !g.pre) {  // (a prefill group's rows are appended by the extra blocks)
             const uint32_t lo = std::max(b, g.new_begin), hi = std::min(e, g.new_end);
             if (hi > lo) {
                 it.app0 = g.app_first + (lo - g.new_begin);
@@ -386,10 +388,10 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
                 P.napp_total += it.napp;
             }
         }
-        (g.nq > kMfmaTile ? P.pitems : P.items).push_back(it);
+        (g.pre || g.nq > kMfmaTile ? P.pitems : P.items).push_back(it);
     };
     for (const Group& g : groups) {
-        const bool pre = g.nq > kMfmaTile;
+        const bool pre = g.pre || g.nq > kMfmaTile;
         if (!pre) max_nq = std::max(max_nq, g.nq);
         const uint32_t L = g.pos0 + g.nq;
         const uint32_t n_parts = (L + part - 1) / part;
@@ -1269,8 +1271,21 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
     // Fuse the append into the attention launch when every sequence has a
     // single query group: then exactly one workgroup per (layer, head, page)
     // touches this step's new rows.
-    bool fused = true;
-    for (uint32_t w = 0; w < n_work; w++) fused &= work[w].n_query <= max_group_rows(kv);
+    // With the prefill kernel, a sequence queried at more rows than that (a
+    // prompt chunk with every row queried) has its rows appended by the
+    // launch's extra blocks like a sequence without queries, and all its
+    // query groups run in the prefill launch that follows; the others still
+    // fuse.
+    const bool prefill = NI_ATTN_MFMA && NI_ATTN_PREFILL && (!is_q8(kv->o) || kv->o.head_dim == 64);
+    // A step of prompt chunks only keeps the append launch of its own (the
+    // plain append kernel moves those rows faster than extra blocks of an
+    // attention launch: 16 x 512 prefill 3521 against 3340 GB/s).
+    bool fused = true, small = false, big = false;
+    for (uint32_t w = 0; w < n_work; w++) {
+        small |= work[w].n_query > 0 && work[w].n_query <= max_group_rows(kv);
+        big |= work[w].n_query > max_group_rows(kv);
+    }
+    if (big) fused = prefill && small;
     kv->plan.fused = fused;
     uint32_t row = 0;
     for (uint32_t w = 0; w < n_work; w++) {
@@ -1282,8 +1297,9 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
             const uint32_t pos = len + i;
             const AppendEntry e{row, pg[pos / kPage], pos % kPage, 0};
             kv->plan.app.push_back(e);
-            if (fused && it.n_query == 0) kv->plan.orphans.push_back(e);
-            if (i >= it.n_new - it.n_query) kv->qrows.push_back({row, it.seq, pos, len, len + it.n_new, first});
+            const bool pre = fused && it.n_query > max_group_rows(kv);
+            if (fused && (it.n_query == 0 || pre)) kv->plan.orphans.push_back(e);
+            if (i >= it.n_new - it.n_query) kv->qrows.push_back({row, it.seq, pos, len, len + it.n_new, first, pre});
         }
     }
     return plan_attention(kv, split_tokens, n_lay);
