@@ -1038,7 +1038,8 @@ constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f, kLog2PScale = 14.f
 // query slots, v_mfma_f32_16x16x32_f16, q split into f16 hi + lo), the
 // online softmax on S^T's columns, and O^T += V^T P^T (v_mfma_f32_16x16x16_f16,
 // p split hi + lo), V rows through a per-wave LDS tile read back transposed
-// (ds_read_b64_tr_b16).  Lane l owns
+// (ds_read_b64_tr_b16), and on f16 pools K rows through another, loaded
+// coalesced and read back as the A operand.  Lane l owns
 // query column l % 16 of S^T and O^T, rows 4*(l/16) .. +3 (MFMA output
 // layout), so the softmax state of a query lives in lanes q, q+16, q+32, q+48.
 // Waves take the item's pages round-robin and merge through LDS at the end,
