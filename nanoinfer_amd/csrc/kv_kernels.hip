@@ -678,16 +678,55 @@ __global__ __launch_bounds__(64 * W) void attn_q8_kernel(const AttnLaunch a, con
     const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
     constexpr uint32_t STRIDE = W * PB;
 
+    // Fused, in the wide (one layer per launch) workgroups: the item's new
+    // rows come from the k/v input as their pages stream, quantised as the
+    // append quantises them (the row's amax reduced over its LPK lanes; a max
+    // does not depend on the order).  Otherwise they are appended first
+    // (streaming them costs ~24 registers, 7 -> 5 waves per SIMD, which all
+    // layers in one launch lose: 5202 against 4638 GB/s; one layer per
+    // launch gains, 2641 -> 2823).
+    constexpr bool STREAM = D == 64 && W == (int)kWideWavesQ8 && (int)kWideWavesQ8 != NI_ATTN_WAVES;
+    NewRows nr{};
     if constexpr (FUSED) {
         if (it.napp) {
-            item_append_q8<D>(a, plan, it, lay, head, layer_off, a.pool.page_halves, 64 * W);
-            __syncthreads();
+            if constexpr (STREAM) {
+                const int64_t off =
+                    (int64_t)lay * a.kv_layer_stride + (int64_t)it.app_src * a.kv_row_stride + head * D + ds * 16;
+                nr = NewRows{a.k + off, a.v + off, a.kv_row_stride, it.app_pos, it.napp};
+            } else {
+                item_append_q8<D>(a, plan, it, lay, head, layer_off, a.pool.page_halves, 64 * W);
+                __syncthreads();
+            }
         }
     }
 
     struct Regs {
         u32x4 k[PB][LPP], v[PB][LPP];
         float ks[PB][LPP], vs[PB][LPP];
+    };
+    // A new row's 16 values of this lane (all lanes take part: the amax
+    // crosses lanes), its int8 bytes and scale; stored to the pool when new.
+    auto quant16 = [&](const float* src, bool isnew, uint8_t* blk, uint32_t key, u32x4& w, float& scale) {
+        float4 x[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            x[m] = isnew ? reinterpret_cast<const float4*>(src)[m] : float4{0.f, 0.f, 0.f, 0.f};
+        float am = 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            am = fmaxf(am, fmaxf(fmaxf(fabsf(x[m].x), fabsf(x[m].y)), fmaxf(fabsf(x[m].z), fabsf(x[m].w))));
+#pragma unroll
+        for (int off = 1; off < LPK; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
+        scale = am / 127.f;
+        const float inv = scale > 0.f ? 1.f / scale : 0.f;
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            w[m] = q8_byte(x[m].x, inv) | q8_byte(x[m].y, inv) << 8 | q8_byte(x[m].z, inv) << 16 |
+                   q8_byte(x[m].w, inv) << 24;
+        if (isnew) {
+            *reinterpret_cast<u32x4*>(blk + key * D + ds * 16) = w;
+            if (ds == 0) reinterpret_cast<float*>(blk + kPage * D)[key] = scale;
+        }
     };
     auto load = [&](uint32_t pg, Regs& r) {
 #pragma unroll
@@ -696,6 +735,32 @@ __global__ __launch_bounds__(64 * W) void attn_q8_kernel(const AttnLaunch a, con
                 const uint64_t phys = tab[pg + b];
                 const uint8_t* kb = kbase + phys * page_bytes;
                 const uint8_t* vb = vbase + phys * page_bytes;
+                const uint32_t p0 = (pg + b) * kPage;
+                if (nr.n && p0 < nr.pos + nr.n && p0 + kPage > nr.pos) {  // wave-uniform: new rows in the page
+#pragma unroll
+                    for (int i = 0; i < LPP; i++) {
+                        const uint32_t key = i * KPL + kl;
+                        const uint32_t d = p0 + key - nr.pos;  // unsigned: >= n unless new
+                        const bool isnew = d < nr.n;
+                        const int64_t ro = (int64_t)(isnew ? d : 0u) * nr.row_stride;
+                        u32x4 wk, wv;
+                        float sk, sv;
+                        quant16(nr.k + ro, isnew, const_cast<uint8_t*>(kb), key, wk, sk);
+                        quant16(nr.v + ro, isnew, const_cast<uint8_t*>(vb), key, wv, sv);
+                        if (isnew) {
+                            r.k[b][i] = wk;
+                            r.v[b][i] = wv;
+                            r.ks[b][i] = sk;
+                            r.vs[b][i] = sv;
+                        } else {
+                            r.k[b][i] = load16(reinterpret_cast<const u32x4*>(kb) + lane + i * 64);
+                            r.v[b][i] = load16(reinterpret_cast<const u32x4*>(vb) + lane + i * 64);
+                            r.ks[b][i] = reinterpret_cast<const float*>(kb + kPage * D)[key];
+                            r.vs[b][i] = reinterpret_cast<const float*>(vb + kPage * D)[key];
+                        }
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int i = 0; i < LPP; i++) {
                     r.k[b][i] = load16(reinterpret_cast<const u32x4*>(kb) + lane + i * 64);
