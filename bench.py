@@ -9,22 +9,29 @@ U[16,256], GPT-2 attention shape (12 layers x 12 heads x 64), f16 KV in
 full slots), pages freed on completion and reused.  One step = one
 ni_kv_step over every layer: append every row of the iteration (decode rows
 and budgeted prefill chunks) and run decode attention for every running
-sequence (the last prompt row of a finished prefill included).  The first
-W steps (the ramp-up) are warmup; K steps are timed.
+sequence (the last prompt row of a finished prefill included).
+
+Whatever --steps/--warmup say, the timed window sits in the trace's steady
+state: a fixed untimed ramp of RAMP_STEPS append-only steps (rows reserved,
+appended and committed, no attention) comes first, then W warmup steps, then
+the K timed steps (trace steps RAMP_STEPS+W .. RAMP_STEPS+W+K-1).
 
 The host loop is the C++ serving driver (ni_drive_run: the scheduler of
 metal_serve.rs restated in C++, calling the C ABI), as a compiled caller of
 the library runs it.  Prints ONE JSON line.  ``value`` is algorithmic HBM
 bytes per second over the timed steps (bytes formula in
-nanoinfer_amd/workloads.py, each KV byte once per step), from a run without
-per-launch events; ``roofline`` prices the attention launch alone, timed by
-HIP events the library records around each of its launches on the caller's
-stream in a second run of the same trace; ``per_layer_launches`` runs the
-trace again one layer per launch, as a model's forward must (the step planned
-once, ni_kv_step_layer per layer), and ``per_layer_append_attention`` through
-separate per-layer append and attention calls; ``cpu_baseline`` times the
-oracle's restatement of the
-reference's CPU path (threaded, paged) on a bounded sample of the same trace.
+nanoinfer_amd/workloads.py, each KV byte once per step), the median of REPS
+identical runs without per-launch events (``repetitions`` lists them);
+``copy_ceiling`` is a plain device copy timed in the same process;
+``roofline`` prices the attention launch alone, timed by HIP events the
+library records around each of its launches on the caller's stream in one
+more run of the same window, with ``traffic`` from the committed rocprofv3
+counter summary only when that summary covers the same window;
+``per_layer_launches`` runs the window one layer per launch, as a model's
+forward must (the step planned once, ni_kv_step_layer per layer), and
+``per_layer_append_attention`` through separate per-layer append and
+attention calls; ``cpu_baseline`` times the oracle's restatement of the
+reference's CPU path (threaded, paged) on the first steps of the same window.
 """
 from __future__ import annotations
 
@@ -57,28 +64,6 @@ TRAFFIC_PROFILES = {
 }
 
 
-def measured_traffic(workload="config3"):
-    """HBM bytes per launch of the attention kernel (with its merge, where
-    the workload splits) from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary (scaled by the copy calibration it records), with the
-    algorithmic bytes of the same profiled steps."""
-    vals = {}
-    path = TRAFFIC_PROFILES.get(workload)
-    if path is None:
-        return None
-    try:
-        for line in open(path):
-            if "=" in line and line.split("=")[0].strip() in ("traffic_bytes_per_launch",
-                                                              "algorithmic_bytes_per_launch_same_steps"):
-                k, v = line.split("=")
-                vals[k.strip()] = int(float(v))
-    except OSError:
-        return None
-    if len(vals) != 2:
-        return None
-    return vals
-
-
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,7 +75,8 @@ def parse():
                          "the append in its epilogue, ROWS rows per layer, default 64)")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = automatic)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (0 = skip)")
-    ap.add_argument("--threads", type=int, default=0, help="CPU baseline threads (0 = min(cpus, 16))")
+    ap.add_argument("--threads", type=int, default=0,
+                    help="CPU baseline threads (0 = available parallelism, as the reference's thread pools)")
     ap.add_argument("--no-profile", action="store_true", help="skip the run timed by per-launch HIP events")
     ap.add_argument("--skip-per-layer", action="store_true", help="config 3: skip the per-layer launch run")
     ap.add_argument("--seed", type=int, default=7)
@@ -137,98 +123,162 @@ def cfg3_opts(host_only=False):
                         max_rows=CFG3["max_rows"], host_only=host_only)
 
 
-def cfg3_trace(n_steps, seed):
-    """Plan the whole trace on a host-only handle (the same C++ allocator
-    makes the same decisions on the device handle)."""
-    import nanoinfer_amd as na
-    from nanoinfer_amd import workloads
+def available_parallelism() -> int:
+    """std::thread::available_parallelism() on Linux, by which the
+    reference's thread pools size themselves when asked for 0 threads
+    (crates/core/src/fastpool.rs:148, pool.rs:163): the CPUs of this
+    process's affinity mask, capped by a cgroup CPU quota (quota / period,
+    at least 1) where one is set."""
+    n = len(os.sched_getaffinity(0))
+    quotas = []
+    try:
+        rel = ""
+        for line in open("/proc/self/cgroup"):
+            if line.startswith("0::"):
+                rel = line.strip()[3:]
+        # cgroup v2: every level from the process's group up to the root
+        path = "/sys/fs/cgroup" + rel
+        while True:
+            try:
+                q, per = open(os.path.join(path, "cpu.max")).read().split()[:2]
+                if q != "max":
+                    quotas.append(max(1, int(q) // int(per)))
+            except (OSError, ValueError):
+                pass
+            if os.path.normpath(path) == "/sys/fs/cgroup":
+                break
+            path = os.path.dirname(path)
+    except OSError:
+        pass
+    try:  # cgroup v1
+        q = int(open("/sys/fs/cgroup/cpu/cpu.cfs_quota_us").read())
+        per = int(open("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read())
+        if q > 0 and per > 0:
+            quotas.append(max(1, q // per))
+    except (OSError, ValueError):
+        pass
+    return min([n] + quotas)
 
-    host = na.PagedKv(cfg3_opts(host_only=True))
-    tr = workloads.ContinuousBatching(host, seed=seed, max_batch=CFG3["max_batch"], prompt=CFG3["prompt"],
-                                      out=CFG3["out"], rate=CFG3["rate"], budget=CFG3["budget"],
-                                      max_rows=CFG3["max_rows"])
-    steps = []
-    for _ in range(n_steps):
-        st = tr.plan()
-        # commit what the device handle's ni_kv_step will commit
-        for seq, n_new, _ in st.work:
-            host.reserve(int(seq), host.seq_len(int(seq)) + int(n_new))
-            host.commit(int(seq), int(n_new))
-        tr.commit()
-        steps.append(st)
-    return steps
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
-def cpu_baseline_cfg3(steps, warmup, seconds, threads):
-    """The oracle's restatement of the reference CPU path on the same trace:
-    warmup steps append only (untimed), then whole steps until `seconds`."""
+def cpu_baseline_cfg3(args, ramp, threads, reps=5):
+    """The oracle's restatement of the reference's x86 CPU path on the bench's
+    own window of the config-3 trace.
+
+    The trace comes from the same C++ scheduler the device run uses (ni_serve
+    on a host-only handle, so the same admissions, retirements and rows), its
+    tables from the oracle's allocator.  The ramp and warmup steps append only
+    (untimed; numpy's float16 conversion, bit-identical to the reference's
+    f32_to_f16 on these finite inputs, checked below).  Then each step of the
+    window runs the CPU step (narrow + attend_f16_portable with fastops::exp
+    over kv_slot, (query, head) units on `threads` threads): the first
+    repetition records each step's table and rows until it has spent
+    seconds / reps (at most the window's `steps` steps), and the other
+    repetitions replay the same steps.  Returns the median repetition."""
     import oracle
-    from nanoinfer_amd import workloads
+    import nanoinfer_amd as na
+    from nanoinfer_amd import drivers, workloads
 
     opts = cfg3_opts(host_only=True)
+    host = na.PagedKv(opts)
+    sv = drivers.Serve(host, seed=args.seed, rate=CFG3["rate"], max_batch=CFG3["max_batch"], prompt=CFG3["prompt"],
+                       out=CFG3["out"], budget=CFG3["budget"], max_rows=CFG3["max_rows"])
     alloc = oracle.Alloc(opts.kv_blocks, opts.max_seqs, opts.n_ctx)
-    c = opts.n_head * opts.head_dim
-    pools = oracle.PagedPools(opts.n_layer, opts.kv_blocks, c)
-    runner = oracle.CpuStep(threads)
-    rng = np.random.default_rng(1)
-    big = CFG3["max_rows"]
-    q = rng.standard_normal((opts.n_layer, big, c), dtype=np.float32)
-    k = rng.standard_normal((opts.n_layer, big, c), dtype=np.float32)
-    v = rng.standard_normal((opts.n_layer, big, c), dtype=np.float32)
+    c, L, mb = opts.n_head * opts.head_dim, opts.n_layer, opts.max_rows
+    pools = oracle.PagedPools(L, opts.kv_blocks, c)
+    kpool = pools.k.reshape(L, -1, c)
+    vpool = pools.v.reshape(L, -1, c)
+    rng = np.random.default_rng(args.seed)
+    q, k, v = (rng.standard_normal((L, mb, c), dtype=np.float32) for _ in range(3))
     out = np.zeros_like(q)
-    done_bytes = 0
-    done_tokens = 0
-    t_cpu = 0.0
-    n_timed = 0
-    for i, st in enumerate(steps):
-        for s in st.retire:
+    k16, v16 = k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)
+    assert np.array_equal(k16.reshape(-1), oracle.f32_to_f16(k.reshape(-1)))
+    assert np.array_equal(v16.reshape(-1), oracle.f32_to_f16(v.reshape(-1)))
+    runner = oracle.CpuStep(threads)
+    budget = args.cpu_seconds / reps
+    recorded, t_first = [], 0.0
+    for i in range(ramp + args.warmup + args.steps):
+        work, ctx, adm, ret = sv.plan()
+        for s in ret:
             alloc.free_seq(s)
-        for s in st.admit:
+        for s in adm:
             assert alloc.add_seq() == s
-        rows_s, rows_p, qrows = [], [], []
-        for seq, n_new, n_q in st.work:
+        rs, rp, qr = [], [], []
+        for seq, n_new, n_q in work:
             seq, n_new, n_q = int(seq), int(n_new), int(n_q)
-            L = alloc.seq_len(seq)
-            assert alloc.ensure(seq, L + n_new) == 0
+            ln = alloc.seq_len(seq)
+            assert alloc.ensure(seq, ln + n_new) == 0
+            host.reserve(seq, ln + n_new)
             for j in range(n_new):
                 if j >= n_new - n_q:
-                    qrows.append(len(rows_s))
-                rows_s.append(seq)
-                rows_p.append(L + j)
-        n = len(rows_s)
-        rs = np.asarray(rows_s, np.uint32)
-        rp = np.asarray(rows_p, np.uint32)
-        timed = i >= warmup
-        qr = np.asarray(qrows if timed else [], np.uint32)
-        t0 = time.perf_counter()
-        runner.run(pools, alloc.table(), alloc.max_blocks, rs, rp, qr, q, k, v, out, opts.n_head, opts.head_dim)
-        dt = time.perf_counter() - t0
-        for seq, n_new, _ in st.work:
+                    qr.append(len(rs))
+                rs.append(seq)
+                rp.append(ln + j)
+        rs, rp = np.asarray(rs, np.uint32), np.asarray(rp, np.uint32)
+        tab = alloc.table()
+        if i < ramp + args.warmup:
+            slots = tab[rs, rp // 16].astype(np.int64) * 16 + rp % 16
+            kpool[:, slots, :] = k16[:, : len(rs), :]
+            vpool[:, slots, :] = v16[:, : len(rs), :]
+        else:
+            qr = np.asarray(qr, np.uint32)
+            t0 = time.perf_counter()
+            runner.run(pools, tab, alloc.max_blocks, rs, rp, qr, q, k, v, out, opts.n_head, opts.head_dim)
+            t_first += time.perf_counter() - t0
+            b = workloads.step_bytes(work, ctx, L, c)
+            recorded.append((tab, rs, rp, qr, b["total"], b["seq_tokens"]))
+        for seq, n_new, _ in work:
             alloc.commit(int(seq), int(n_new))
-        if timed:
-            b = workloads.step_bytes(st.work, st.ctx_after, opts.n_layer, c)
-            done_bytes += b["total"]
-            done_tokens += b["seq_tokens"]
-            t_cpu += dt
-            n_timed += 1
-            if t_cpu >= seconds:
-                break
-    return {"seconds": t_cpu, "bytes": done_bytes, "tokens": done_tokens, "steps": n_timed, "threads": runner.threads}
+            host.commit(int(seq), int(n_new))
+        sv.commit()
+        if recorded and t_first >= budget:
+            break
+    times = [t_first]
+    for _ in range(reps - 1):
+        t = 0.0
+        for tab, rs, rp, qr, _, _ in recorded:
+            t0 = time.perf_counter()
+            runner.run(pools, tab, alloc.max_blocks, rs, rp, qr, q, k, v, out, opts.n_head, opts.head_dim)
+            t += time.perf_counter() - t0
+        times.append(t)
+    return {"seconds": float(np.median(times)), "rep_seconds": times, "bytes": sum(r[4] for r in recorded),
+            "tokens": sum(r[5] for r in recorded), "steps": len(recorded), "threads": runner.threads}
 
 
-def _drive(name, args, launch=None, profile_mask=0):
+def _drive(name, args, launch=None, profile_mask=0, ramp=0):
     """One ni_drive_run of a preset: the C++ driver's host loop (the
     scheduler, ni_kv_step and its bookkeeping) with inputs resident in HBM."""
     from nanoinfer_amd import drivers
 
     launch = drivers.NI_DRIVE_STEP if launch is None else launch
     o = drivers.preset(name, args.steps, args.warmup, launch=launch, split=args.split, seed=args.seed,
-                       profile_mask=profile_mask)
+                       profile_mask=profile_mask, ramp=ramp)
     r = drivers.drive(o)
     gbs = r["bytes"] / r["seconds"] / 1e9
     log(f"bench: {name} launch {launch}{' (profiled)' if profile_mask else ''}: {gbs:.1f} GB/s, "
-        f"{r['seconds'] / r['steps'] * 1e6:.1f} us/step, host {r['host_us_per_step']:.1f} us/step")
+        f"{r['seconds'] / r['steps'] * 1e6:.1f} us/step, host {r['host_us_per_step']:.1f} us/step, "
+        f"{r['mean_live']:.2f} live, mean context {r['mean_context']:.1f}")
     return r
+
+
+def _median_run(name, args, reps, launch=None, ramp=0):
+    """`reps` identical runs; the run of median throughput and the spread."""
+    runs = [_drive(name, args, launch=launch, ramp=ramp) for _ in range(reps)]
+    gbs = [r["bytes"] / r["seconds"] / 1e9 for r in runs]
+    order = np.argsort(gbs)
+    med = runs[int(order[len(runs) // 2])]
+    spread = {"reps": reps, "gbs": [round(g, 2) for g in gbs], "median_gbs": round(float(np.median(gbs)), 2),
+              "stdev_gbs": round(float(np.std(gbs, ddof=1)) if reps > 1 else 0.0, 2)}
+    return med, spread
 
 
 def _line(args, r, workload, cfg, data):
@@ -258,57 +308,143 @@ def _roofline(rp, kernel, with_merge):
     return out
 
 
+def copy_ceiling(nbytes=2 << 30, reps=5):
+    """A plain device-to-device copy of `nbytes` (torch's copy_, the runtime's
+    copy kernel) timed with events on torch's stream: read + write bytes per
+    second, median of `reps` copies after one untimed copy."""
+    import torch
+
+    x = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        y.copy_(x)
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) / 1e3)
+    del x, y
+    torch.cuda.empty_cache()
+    t = float(np.median(ts))
+    return {"value": round(2 * nbytes / t / 1e9, 1), "unit": "GB/s", "bytes_read": nbytes, "bytes_written": nbytes,
+            "method": f"torch copy_ of {nbytes >> 20} MiB device to device, HIP events, median of {reps}"}
+
+
+def hbm_peak_reported():
+    """The HBM peak the device itself reports: 2 transfers per memory clock
+    (DDR) x bus width, from hipDeviceGetAttribute."""
+    from nanoinfer_amd import drivers
+
+    clk, bits = drivers.device_memory(0)
+    return {"mem_clock_khz": clk, "bus_width_bits": bits, "ddr_peak_gbs": round(2 * clk * 1e3 * bits / 8 / 1e9, 1)}
+
+
+# Config 3's timed window: an untimed append-only ramp of RAMP_STEPS trace
+# steps brings the 64 slots to their steady state (slots full from step ~100,
+# contexts stationary from ~300; the trace's initial synchronised admissions
+# have mixed by ~1000), then W warmup steps and the K timed steps.
+RAMP_STEPS = 1000
+REPS = 5
+
+
+def measured_traffic(workload, args, ramp):
+    """HBM bytes per launch of the attention kernel (with its merge, where
+    the workload splits) from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (scaled by the copy calibration it records), with the
+    algorithmic bytes of the same steps -- only when the summary was taken
+    over this run's window (the `window` line matches), else None."""
+    vals, window = {}, None
+    path = TRAFFIC_PROFILES.get(workload)
+    if path is None:
+        return None
+    want = f"{workload} ramp={ramp} warmup={args.warmup} steps={args.steps} seed={args.seed} split={args.split}"
+    try:
+        for line in open(path):
+            if "=" not in line:
+                continue
+            key, _, val = line.partition("=")
+            key = key.strip()
+            if key == "window":
+                window = val.strip()
+            elif key in ("traffic_bytes_per_launch", "algorithmic_bytes_per_launch_same_steps"):
+                vals[key] = int(float(val))
+    except OSError:
+        return None
+    if len(vals) != 2 or window != want:
+        return None
+    return vals
+
+
 def run_config3(args):
     from nanoinfer_amd import drivers
 
-    r = _drive("config3", args)
+    ramp = RAMP_STEPS
+    r, spread = _median_run("config3", args, REPS, ramp=ramp)
     res = _line(args, r, "config3: continuous batching, 64 slots, Poisson arrivals 1/step, prompt U[32,512], "
                          "output U[16,256], GPT-2 12x12x64, 16-token pages, 3080-page pool",
                 dict(n_layer=12, n_head=12, head_dim=64, kv_pages=cfg3_pages(), max_batch=CFG3["max_batch"],
                      prefill_budget=CFG3["budget"], prefill_attention="last prompt row only",
                      split_tokens=args.split, host_loop="C++ driver (ni_drive_run: ni_serve + ni_kv_step)",
                      launches_per_step="one ni_kv_step: append fused into the attention launch, all layers",
+                     ramp_steps=ramp, ramp="untimed, append only (the steps' rows reserved, appended and "
+                                           "committed, no attention), before the warmup",
+                     timed_trace_steps=[ramp + args.warmup, ramp + args.warmup + args.steps - 1],
                      mean_live_seqs=round(r["mean_live"], 2), mean_context=round(r["mean_context"], 1),
                      algorithmic_bytes_per_step=int(r["bytes"] / r["steps"])),
                 "synthetic (seeded N(0,1) q/k/v resident in HBM, seeded Poisson request trace)")
+    res["repetitions"] = spread
+    res["copy_ceiling"] = copy_ceiling()
+    try:
+        res["hbm_peak_reported"] = hbm_peak_reported()
+    except RuntimeError as e:
+        log(f"bench: {e}")
     if not args.no_profile:
         # ni_kv_step fuses the append into the attention launch whenever every
         # sequence has one query group (always here): the launch's bytes are
         # the whole step's.
-        rp = _drive("config3", args, profile_mask=1 << 1)
+        rp = _drive("config3", args, profile_mask=(1 << 1) | (1 << 2), ramp=ramp)
+        if rp["kernel_launches"][1] != rp["steps"] or rp["kernel_launches"][2] != 0:
+            raise RuntimeError(f"expected one fused launch per step and no merge, got {rp['kernel_launches']}")
         res["roofline"] = _roofline(rp, "attn_split_kernel<64,1,4,2,fused>", with_merge=False)
-        tr = measured_traffic()
+        tr = measured_traffic("config3", args, ramp)
         if tr:
             res["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
             res["roofline"]["traffic_vs_algorithmic"] = round(
                 tr["traffic_bytes_per_launch"] / tr["algorithmic_bytes_per_launch_same_steps"], 3)
-            res["roofline"]["traffic_source"] = "profiles/attn_split_fused_config3.md (rocprofv3 --pmc, scaled)"
+            res["roofline"]["traffic_source"] = ("profiles/attn_split_fused_config3.md (rocprofv3 --pmc over the "
+                                                 "same trace steps, scaled by a plain copy's counters)")
     # A model's forward runs a step's layers one at a time (layer l+1's q/k/v
     # come from layer l's output); the reference encodes the step once and
     # dispatches each layer's KV write and attention (batch.rs:280-306,
-    # 390-416).  The same trace with the step planned once and one fused
+    # 390-416).  The same window with the step planned once and one fused
     # append + attention launch per layer (ni_kv_step_layer), and through
     # separate ni_kv_append + ni_paged_decode_attention calls per layer.
     if not args.skip_per_layer:
         for key, mode in (("per_layer_launches", drivers.NI_DRIVE_STEP_LAYERS),
                           ("per_layer_append_attention", drivers.NI_DRIVE_PER_LAYER)):
-            rl = _drive("config3", args, launch=mode)
+            rl, sp = _median_run("config3", args, 3, launch=mode, ramp=ramp)
             gbs = rl["bytes"] / rl["seconds"] / 1e9
             res[key] = {"value": round(gbs, 2), "unit": "GB/s", "pct_of_peak": round(100 * gbs / PEAK_GBS, 2),
                         "ms_per_step": round(rl["seconds"] / rl["steps"] * 1e3, 5),
-                        "abi_calls_per_step": round(rl["launches"] / rl["steps"], 1)}
+                        "host_us_per_step": round(rl["host_us_per_step"], 1),
+                        "abi_calls_per_step": round(rl["launches"] / rl["steps"], 1), "repetitions": sp}
     if args.cpu_seconds > 0:
-        threads = args.threads or min(os.cpu_count() or 1, 16)
-        log(f"bench: planning the trace for the CPU baseline")
-        steps = cfg3_trace(args.warmup + args.steps, args.seed)
+        threads = args.threads or available_parallelism()
         log(f"bench: CPU baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
-        cb = cpu_baseline_cfg3(steps, args.warmup, args.cpu_seconds, threads)
+        cb = cpu_baseline_cfg3(args, ramp, threads)
+        w0 = ramp + args.warmup
         res["cpu_baseline"] = {
             "value": round(cb["bytes"] / cb["seconds"] / 1e9, 3), "unit": "GB/s",
             "seq_tokens_per_s": round(cb["tokens"] / cb["seconds"], 1), "cores": cb["threads"], "kind": "port",
-            "sample": f"steps {args.warmup}..{args.warmup + cb['steps'] - 1} of the same trace "
-                      f"({cb['seconds']:.1f} s; the oracle's C restatement of the reference x86 CPU path: "
-                      f"narrow + attend_f16_portable + fastops::exp over kv_slot, units on a thread pool)",
+            "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+            "threads_rule": "available_parallelism (affinity mask, cgroup quota), as the reference's pools",
+            "repetitions": {"reps": len(cb["rep_seconds"]), "seconds": [round(t, 3) for t in cb["rep_seconds"]]},
+            "sample": f"trace steps {w0}..{w0 + cb['steps'] - 1} (the first {cb['steps']} of the GPU's timed steps), "
+                      f"median of {len(cb['rep_seconds'])} repetitions ({cb['seconds']:.2f} s each): the oracle's C "
+                      f"restatement of the reference x86 CPU path (narrow + attend_f16_portable + fastops::exp over "
+                      f"kv_slot, (query, head) units on a thread pool)",
         }
     return res
 
@@ -333,17 +469,18 @@ SECONDARY["config3q8"] = ("config3: continuous batching (bench default trace); Q
 
 def run_secondary(args):
     desc, cfg = SECONDARY[args.workload]
-    r = _drive(args.workload, args)
+    r, spread = _median_run(args.workload, args, REPS)
     res = _line(args, r, desc, dict(cfg, mean_context=round(r["mean_context"], 1),
                                     algorithmic_bytes_per_step=int(r["bytes"] / r["steps"]),
                                     host_loop="C++ driver (ni_drive_run)"),
                 "synthetic (seeded normal q/k/v resident in HBM)")
+    res["repetitions"] = spread
     if not args.no_profile:
         rp = _drive(args.workload, args, profile_mask=(1 << 1) | (1 << 2))
         res["roofline"] = _roofline(rp, "attn_q8_kernel (+ attn_merge_kernel when split)" if args.workload.endswith("q8")
                                     else "attn_split_kernel / attn_mfma_kernel (+ attn_merge_kernel when split)",
                                     with_merge=True)
-        tr = measured_traffic(args.workload)
+        tr = measured_traffic(args.workload, args, 0)
         if tr:
             res["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]
             res["roofline"]["traffic_vs_algorithmic"] = round(

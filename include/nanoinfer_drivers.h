@@ -123,7 +123,12 @@ typedef struct ni_drive_opts {
     uint32_t spec_k;        /* drafts per round */
     uint64_t spec_seed;     /* contexts; acceptance draws use data_seed */
     uint32_t spec_window;   /* see ni_spec_set_window (0 = none) */
-    uint32_t warmup;        /* untimed iterations */
+    /* untimed iterations before the warmup that only append (each
+     * iteration's rows reserved, appended for every layer and committed in
+     * work order, as ni_kv_step would: the same pages and bytes) and run no
+     * attention: they bring a trace to its steady state cheaply */
+    uint32_t ramp;
+    uint32_t warmup;        /* untimed iterations (full steps) */
     uint32_t steps;         /* timed iterations */
     uint32_t split_tokens;  /* 0 = automatic */
     uint64_t data_seed;     /* q/k/v contents */
@@ -153,6 +158,11 @@ typedef struct ni_drive_result {
 
 int ni_drive_run(const ni_drive_opts* opts, ni_drive_result* result);
 const char* ni_drive_last_error(void);
+
+/* The device's memory interface as HIP reports it (hipDeviceGetAttribute:
+ * peak memory clock in kHz and bus width in bits), for a harness that
+ * states the HBM peak it measures against. */
+int ni_drive_device_memory(int device, int* mem_clock_khz, int* bus_width_bits);
 
 #ifdef __cplusplus
 }

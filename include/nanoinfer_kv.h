@@ -195,9 +195,10 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
  * once; ni_kv_step_layer(layer) then appends that layer's new rows and runs
  * its attention in one launch over that plan (q/k/v/out hold the layer's rows
  * only, row r at base + r*row_stride); ni_kv_step_end commits seq_len +=
- * n_new.  Layers may come in any order, each once; calls on one stream (a
- * staged plan is uploaded for the first call's stream and waited for on the
- * others').  While a step is open, ni_kv_step, ni_kv_decode_steps,
+ * n_new.  Layers may come in any order, each once, all on the stream of
+ * the first layer's call (the layers share the step's plan and split
+ * partials; another stream returns NI_ERR_BAD_ARG and nothing is
+ * launched).  While a step is open, ni_kv_step, ni_kv_decode_steps,
  * ni_kv_truncate, ni_kv_free_seq and ni_kv_commit return NI_ERR_BAD_ARG. */
 int ni_kv_step_begin(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t split_tokens);
 int ni_kv_step_layer(ni_kv* kv, int32_t layer, const float* q, const float* k, const float* v, int64_t row_stride,

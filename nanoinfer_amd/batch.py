@@ -83,34 +83,60 @@ def _rows(rows) -> tuple:
     return arr, arr.ctypes.data_as(C.POINTER(_abi.ni_row)), n
 
 
-def _f32_arg(t, name, layered):
-    """(pointer, row_stride, layer_stride) of a float32 device tensor laid out
-    [n_layer][rows][C] (layered) or [rows][C]."""
+def _f32_arg(t, name, layered, rows, c, n_layer):
+    """(row_stride, layer_stride) of a float32 tensor laid out
+    [n_layer][>= rows][c] (layered) or [>= rows][c], unit stride in its last
+    dimension.  The C ABI sees only pointers and strides, so a short tensor is
+    refused here, before any device access (`_on_device` checks placement
+    once every layout has passed)."""
     import torch
 
-    if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32:
+    if not isinstance(t, torch.Tensor) or t.dtype != torch.float32:
         raise TypeError(f"{name} must be a float32 CUDA tensor")
     if layered:
         if t.dim() != 3 or t.stride(2) != 1:
             raise ValueError(f"{name} must be [n_layer, rows, C] with unit stride in C")
-        return t.data_ptr(), t.stride(1), t.stride(0)
+        if t.shape[0] != n_layer or t.shape[1] < rows or t.shape[2] != c:
+            raise ValueError(f"{name} is {list(t.shape)}: needs [{n_layer}, >= {rows}, {c}]")
+        return t.stride(1), t.stride(0)
     if t.dim() != 2 or t.stride(1) != 1:
         raise ValueError(f"{name} must be [rows, C] with unit stride in C")
-    return t.data_ptr(), t.stride(0), 0
+    if t.shape[0] < rows or t.shape[1] != c:
+        raise ValueError(f"{name} is {list(t.shape)}: needs [>= {rows}, {c}]")
+    return t.stride(0), 0
+
+
+def _on_device(device, **tensors):
+    """Every tensor on the GPU, on the cache's device."""
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise TypeError(f"{name} must be a float32 CUDA tensor")
+        if device is not None and t.device.index != device:
+            raise ValueError(f"{name} is on cuda:{t.device.index}, the cache on cuda:{device}")
 
 
 def _weights(w, bias, c, d_in):
-    """Check W [3C, d_in] (contiguous float32 CUDA) and bias; the bias pointer."""
+    """Check the layout of W [3C, d_in] (contiguous float32) and bias."""
     import torch
 
-    if not isinstance(w, torch.Tensor) or not w.is_cuda or w.dtype != torch.float32 or not w.is_contiguous() \
+    if not isinstance(w, torch.Tensor) or w.dtype != torch.float32 or not w.is_contiguous() \
             or tuple(w.shape) != (3 * c, d_in):
         raise ValueError(f"w must be a contiguous float32 CUDA tensor [{3 * c}, {d_in}]")
-    if bias is None:
-        return None
-    if not bias.is_cuda or bias.dtype != torch.float32 or not bias.is_contiguous() or bias.numel() != 3 * c:
+    if bias is not None and (not isinstance(bias, torch.Tensor) or bias.dtype != torch.float32
+                             or not bias.is_contiguous() or bias.numel() != 3 * c):
         raise ValueError(f"bias must be a contiguous float32 CUDA tensor of {3 * c} values")
-    return bias.data_ptr()
+
+
+def _work(work) -> np.ndarray:
+    w = np.ascontiguousarray(np.asarray(work, dtype=np.uint32).reshape(-1, 3))
+    return w
+
+
+def _work_rows(w: np.ndarray) -> int:
+    """Rows a step's work numbers (sum of n_new)."""
+    return int(w[:, 1].astype(np.int64).sum())
 
 
 class PagedKv:
@@ -127,6 +153,13 @@ class PagedKv:
         if opts.page_order is not None:
             self._order = np.ascontiguousarray(np.asarray(opts.page_order, dtype=np.uint32))
             o.page_order = self._order.ctypes.data_as(C.POINTER(C.c_uint32))
+        # The device a handle lives on is the current one at creation.
+        self.device = None
+        if not opts.host_only:
+            import torch
+
+            self.device = torch.cuda.current_device()
+        self._open_rows = None  # rows of the step opened by step_begin
         h = C.c_void_p()
         rc = self._L.ni_kv_create(C.byref(o), C.byref(h))
         if rc != 0:
@@ -158,6 +191,12 @@ class PagedKv:
     def _check(self, rc):
         if rc != 0:
             raise KvError(rc, self._L.ni_kv_last_error(self._h).decode())
+
+    def _f32(self, t, name, layered, rows, c=None):
+        return _f32_arg(t, name, layered, rows, self.opts.n_embd if c is None else c, self.opts.n_layer)
+
+    def _on_device(self, **tensors):
+        _on_device(self.device, **tensors)
 
     @property
     def max_blocks(self) -> int:
@@ -218,11 +257,13 @@ class PagedKv:
         """Write f32 K/V rows as f16 into their pages (b_kv_write)."""
         arr, rp, n = _rows(rows)
         layered = layer == ALL_LAYERS
-        kp, rs, ls = _f32_arg(k, "k", layered)
-        vp, rs2, ls2 = _f32_arg(v, "v", layered)
+        rs, ls = self._f32(k, "k", layered, n)
+        rs2, ls2 = self._f32(v, "v", layered, n)
         if (rs, ls) != (rs2, ls2):
             raise ValueError("k and v must share strides")
-        self._check(self._L.ni_kv_append(self._h, layer, rp, n, kp, vp, rs, ls, _stream_ptr(stream)))
+        self._on_device(k=k, v=v)
+        self._check(self._L.ni_kv_append(self._h, layer, rp, n, k.data_ptr(), v.data_ptr(), rs, ls,
+                                         _stream_ptr(stream)))
 
     def qkv_append(self, rows, x, w, bias=None, q_out=None, layer: int = 0, stream=None):
         """The QKV projection with the append in its epilogue (BEPI_QKV):
@@ -231,12 +272,18 @@ class PagedKv:
         import torch
 
         arr, rp, n = _rows(rows)
-        xp, xs, _ = _f32_arg(x, "x", False)
-        wt = _weights(w, bias, self.opts.n_embd, x.shape[1])
+        if not isinstance(x, torch.Tensor) or x.dim() != 2:
+            raise ValueError("x must be a [rows, d_in] tensor")
+        xs, _ = self._f32(x, "x", False, n, c=x.shape[1])
+        _weights(w, bias, self.opts.n_embd, x.shape[1])
+        if q_out is not None:
+            self._f32(q_out, "q_out", False, n)
+        self._on_device(x=x, w=w, bias=bias, q_out=q_out)
         if q_out is None:
             q_out = torch.zeros((n, self.opts.n_embd), dtype=torch.float32, device=x.device)
-        qp, qs, _ = _f32_arg(q_out, "q_out", False)
-        self._check(self._L.ni_kv_qkv_append(self._h, layer, rp, n, xp, xs, x.shape[1], w.data_ptr(), wt, qp, qs,
+        qs, _ = self._f32(q_out, "q_out", False, n)
+        self._check(self._L.ni_kv_qkv_append(self._h, layer, rp, n, x.data_ptr(), xs, x.shape[1], w.data_ptr(),
+                                             None if bias is None else bias.data_ptr(), q_out.data_ptr(), qs,
                                              _stream_ptr(stream)))
         return q_out
 
@@ -244,12 +291,18 @@ class PagedKv:
         """The same projection, every output column to out [n, 3C] (f32)."""
         import torch
 
-        xp, xs, _ = _f32_arg(x, "x", False)
-        wt = _weights(w, bias, self.opts.n_embd, x.shape[1])
+        if not isinstance(x, torch.Tensor) or x.dim() != 2:
+            raise ValueError("x must be a [rows, d_in] tensor")
+        xs, _ = self._f32(x, "x", False, x.shape[0], c=x.shape[1])
+        _weights(w, bias, self.opts.n_embd, x.shape[1])
+        if out is not None:
+            self._f32(out, "out", False, x.shape[0], c=3 * self.opts.n_embd)
+        self._on_device(x=x, w=w, bias=bias, out=out)
         if out is None:
             out = torch.zeros((x.shape[0], 3 * self.opts.n_embd), dtype=torch.float32, device=x.device)
-        op, os_, _ = _f32_arg(out, "out", False)
-        self._check(self._L.ni_kv_qkv_project(self._h, xp, xs, x.shape[0], x.shape[1], w.data_ptr(), wt, op, os_,
+        os_, _ = self._f32(out, "out", False, x.shape[0], c=3 * self.opts.n_embd)
+        self._check(self._L.ni_kv_qkv_project(self._h, x.data_ptr(), xs, x.shape[0], x.shape[1], w.data_ptr(),
+                                              None if bias is None else bias.data_ptr(), out.data_ptr(), os_,
                                               _stream_ptr(stream)))
         return out
 
@@ -289,12 +342,15 @@ class PagedKv:
 
         arr, rp, n = _rows(rows)
         layered = layer == ALL_LAYERS
+        qrs, qls = self._f32(q, "q", layered, n)
+        if out is not None:
+            self._f32(out, "out", layered, n)
+        self._on_device(q=q, out=out)
         if out is None:
             out = torch.zeros_like(q)
-        qp, qrs, qls = _f32_arg(q, "q", layered)
-        op, ors, ols = _f32_arg(out, "out", layered)
-        self._check(self._L.ni_paged_decode_attention(self._h, layer, qp, qrs, qls, rp, n, op, ors, ols,
-                                                      split_tokens, _stream_ptr(stream)))
+        ors, ols = self._f32(out, "out", layered, n)
+        self._check(self._L.ni_paged_decode_attention(self._h, layer, q.data_ptr(), qrs, qls, rp, n, out.data_ptr(),
+                                                      ors, ols, split_tokens, _stream_ptr(stream)))
         return out
 
     def step(self, work, q, k, v, out=None, split_tokens: int = 0, stream=None):
@@ -303,18 +359,22 @@ class PagedKv:
         are [n_layer, rows, C]."""
         import torch
 
-        w = np.ascontiguousarray(np.asarray(work, dtype=np.uint32).reshape(-1, 3))
+        w = _work(work)
         wp = w.ctypes.data_as(C.POINTER(_abi.ni_work))
-        kp, rs, ls = _f32_arg(k, "k", True)
-        vp, rs2, ls2 = _f32_arg(v, "v", True)
-        qp, rs3, ls3 = _f32_arg(q, "q", True)
+        n = _work_rows(w)
+        rs3, ls3 = self._f32(q, "q", True, n)
+        rs, ls = self._f32(k, "k", True, n)
+        rs2, ls2 = self._f32(v, "v", True, n)
         if not (rs == rs2 == rs3 and ls == ls2 == ls3):
             raise ValueError("q, k and v must share strides")
+        if out is not None:
+            self._f32(out, "out", True, n)
+        self._on_device(q=q, k=k, v=v, out=out)
         if out is None:
             out = torch.zeros_like(q)
-        op, ors, ols = _f32_arg(out, "out", True)
-        self._check(self._L.ni_kv_step(self._h, wp, w.shape[0], qp, kp, vp, rs, ls, op, ors, ols, split_tokens,
-                                       _stream_ptr(stream)))
+        ors, ols = self._f32(out, "out", True, n)
+        self._check(self._L.ni_kv_step(self._h, wp, w.shape[0], q.data_ptr(), k.data_ptr(), v.data_ptr(), rs, ls,
+                                       out.data_ptr(), ors, ols, split_tokens, _stream_ptr(stream)))
         return out
 
     def step_begin(self, work, split_tokens: int = 0):
@@ -322,28 +382,35 @@ class PagedKv:
         layers then run one :meth:`step_layer` call each, as a model's forward
         does (batch.rs:280-306 encodes once, batch.rs:390-416 dispatches per
         layer); :meth:`step_end` commits it."""
-        w = np.ascontiguousarray(np.asarray(work, dtype=np.uint32).reshape(-1, 3))
+        w = _work(work)
         self._check(self._L.ni_kv_step_begin(self._h, w.ctypes.data_as(C.POINTER(_abi.ni_work)), w.shape[0],
                                              split_tokens))
+        self._open_rows = _work_rows(w)
 
     def step_layer(self, layer: int, q, k, v, out=None, stream=None):
         """Layer ``layer`` of the open step: its new rows appended and its
         queried rows attended in one launch; q/k/v/out are [rows, C]."""
         import torch
 
-        kp, rs, _ = _f32_arg(k, "k", False)
-        vp, rs2, _ = _f32_arg(v, "v", False)
-        qp, rs3, _ = _f32_arg(q, "q", False)
+        n = self._open_rows or 0
+        rs3, _ = self._f32(q, "q", False, n)
+        rs, _ = self._f32(k, "k", False, n)
+        rs2, _ = self._f32(v, "v", False, n)
         if not rs == rs2 == rs3:
             raise ValueError("q, k and v must share a row stride")
+        if out is not None:
+            self._f32(out, "out", False, n)
+        self._on_device(q=q, k=k, v=v, out=out)
         if out is None:
             out = torch.zeros_like(q)
-        op, ors, _ = _f32_arg(out, "out", False)
-        self._check(self._L.ni_kv_step_layer(self._h, layer, qp, kp, vp, rs, op, ors, _stream_ptr(stream)))
+        ors, _ = self._f32(out, "out", False, n)
+        self._check(self._L.ni_kv_step_layer(self._h, layer, q.data_ptr(), k.data_ptr(), v.data_ptr(), rs,
+                                             out.data_ptr(), ors, _stream_ptr(stream)))
         return out
 
     def step_end(self):
         """Commit the open step: every work item's sequence grows by n_new."""
+        self._open_rows = None
         self._check(self._L.ni_kv_step_end(self._h))
 
     def decode_steps(self, seqs, q, k, v, out=None, split_tokens: int = 0, stream=None):
@@ -353,14 +420,19 @@ class PagedKv:
 
         s = np.ascontiguousarray(np.asarray(seqs, dtype=np.uint32).reshape(-1))
         sp = s.ctypes.data_as(C.POINTER(C.c_uint32))
-        for name, t in (("q", q), ("k", k), ("v", v)):
-            if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32 or t.dim() != 4 \
-                    or t.stride(3) != 1:
+        if out is None and isinstance(q, torch.Tensor):
+            out = torch.zeros_like(q)
+        for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+            if not isinstance(t, torch.Tensor) or t.dtype != torch.float32 or t.dim() != 4 or t.stride(3) != 1:
                 raise ValueError(f"{name} must be a float32 CUDA tensor [steps, n_layer, rows, C] with unit stride in C")
+            if t.shape[1] != self.opts.n_layer or t.shape[2] < s.size or t.shape[3] != self.opts.n_embd:
+                raise ValueError(f"{name} is {list(t.shape)}: needs [steps, {self.opts.n_layer}, >= {s.size}, "
+                                 f"{self.opts.n_embd}]")
         if not (q.stride() == k.stride() == v.stride()) or not (q.shape == k.shape == v.shape):
             raise ValueError("q, k and v must share shapes and strides")
-        if out is None:
-            out = torch.zeros_like(q)
+        if out.shape[0] < q.shape[0]:
+            raise ValueError(f"out holds {out.shape[0]} steps, q {q.shape[0]}")
+        self._on_device(q=q, k=k, v=v, out=out)
         self._check(self._L.ni_kv_decode_steps(self._h, sp, s.size, q.shape[0], q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                                q.stride(2), q.stride(1), q.stride(0), out.data_ptr(), out.stride(2),
                                                out.stride(1), out.stride(0), split_tokens, _stream_ptr(stream)))

@@ -389,8 +389,29 @@ struct Runner {
         return NI_OK;
     }
 
-    // One iteration's KV work through the chosen launch path.
-    int launch(const ni_work* w, uint32_t n) {
+    // A ramp iteration: the work's rows reserved, appended for every layer in
+    // one call and committed, in work order (ni_kv_step's page order and
+    // row numbering), with no attention.
+    int append_only(const ni_work* w, uint32_t n) {
+        rows.clear();
+        for (uint32_t i = 0; i < n; i++) {
+            uint32_t len = 0;
+            ni_kv_seq_len(kv, w[i].seq, &len);
+            if (int rc = ni_kv_reserve(kv, w[i].seq, len + w[i].n_new)) return kv_fail(rc, "reserve");
+            for (uint32_t j = 0; j < w[i].n_new; j++) rows.push_back({w[i].seq, len + j});
+        }
+        if (!rows.empty())
+            if (int rc = ni_kv_append(kv, NI_ALL_LAYERS, rows.data(), (uint32_t)rows.size(), d.k, d.v, C, ls, stream))
+                return kv_fail(rc, "append");
+        for (uint32_t i = 0; i < n; i++)
+            if (int rc = ni_kv_commit(kv, w[i].seq, w[i].n_new)) return kv_fail(rc, "commit");
+        return NI_OK;
+    }
+
+    // One iteration's KV work through the chosen launch path (append_only:
+    // a ramp iteration).
+    int launch(const ni_work* w, uint32_t n, bool ramp = false) {
+        if (ramp) return append_only(w, n);
         if (o.launch == NI_DRIVE_STEP) {
             calls++;
             if (int rc = ni_kv_step(kv, w, n, d.q, d.k, d.v, C, ls, d.out, C, ls, o.split_tokens, stream))
@@ -446,11 +467,16 @@ using Clock = std::chrono::steady_clock;
 
 double seconds_since(Clock::time_point t) { return std::chrono::duration<double>(Clock::now() - t).count(); }
 
-// Time `iterate(timed)` over warmup + steps iterations.
+enum Phase { RAMP, WARMUP, TIMED };
+
+// Run `iterate(phase)` over ramp + warmup + steps iterations; time the last
+// `steps`.
 template <typename Fn>
 int timed_run(Runner& r, ni_drive_result* res, Fn&& iterate) {
+    for (uint32_t i = 0; i < r.o.ramp; i++)
+        if (int rc = iterate(RAMP)) return rc;
     for (uint32_t i = 0; i < r.o.warmup; i++)
-        if (int rc = iterate(false)) return rc;
+        if (int rc = iterate(WARMUP)) return rc;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
         return drive_fail(NI_ERR_HIP, "hipEventCreate failed");
@@ -465,7 +491,7 @@ int timed_run(Runner& r, ni_drive_result* res, Fn&& iterate) {
     (void)hipEventRecord(e0, r.stream);
     for (uint32_t i = 0; i < r.o.steps; i++) {
         const auto h0 = Clock::now();
-        if (int rc = iterate(true)) return rc;
+        if (int rc = iterate(TIMED)) return rc;
         host += seconds_since(h0);
     }
     (void)hipEventRecord(e1, r.stream);
@@ -492,11 +518,11 @@ int run_serve(Runner& r, ni_drive_result* res) {
     ni_serve* sv = nullptr;
     if (int rc = ni_serve_create(r.kv, &r.o.serve, &sv)) return rc;
     double live = 0, ctx = 0;
-    int rc = timed_run(r, res, [&](bool timed) -> int {
+    int rc = timed_run(r, res, [&](Phase ph) -> int {
         ni_serve_iter it{};
         if (int e = ni_serve_plan(sv, &it)) return e;
-        if (int e = r.launch(it.work, it.n_work)) return e;
-        if (timed) {
+        if (int e = r.launch(it.work, it.n_work, ph == RAMP)) return e;
+        if (ph == TIMED) {
             res->bytes += step_bytes(it.work, it.n_work, it.ctx_after, r.L, r.C, r.kvb);
             for (uint32_t i = 0; i < it.n_work; i++)
                 if (it.work[i].n_query) {
@@ -527,15 +553,15 @@ int run_spec(Runner& r, ni_drive_result* res) {
     if (int rc = ni_spec_create(r.kv, seqs.data(), (uint32_t)seqs.size(), r.o.spec_k, r.o.data_seed, &sp)) return rc;
     ni_spec_set_window(sp, r.o.spec_window);
     double ctx = 0;
-    int rc = timed_run(r, res, [&](bool timed) -> int {
+    int rc = timed_run(r, res, [&](Phase ph) -> int {
         const ni_work* w = nullptr;
         const uint32_t* ca = nullptr;
         uint32_t n = 0;
         if (int e = ni_spec_plan(sp, &w, &n, &ca)) return e;
-        if (int e = r.launch(w, n)) return e;
+        if (int e = r.launch(w, n, ph == RAMP)) return e;
         const uint32_t* acc = nullptr;
         if (int e = ni_spec_commit(sp, &acc)) return e;
-        if (timed) {
+        if (ph == TIMED) {
             res->bytes += step_bytes(w, n, ca, r.L, r.C, r.kvb);
             for (uint32_t i = 0; i < n; i++) {
                 res->seq_tokens += acc[i] + 1;  // tokens a verify round yields
@@ -569,12 +595,12 @@ int run_fixed(Runner& r, ni_drive_result* res) {
         flops += 4.0 * r.C * r.L * ((double)R * (ctx - R) + (double)R * (R + 1) / 2);
     }
     const double bytes = step_bytes(work.data(), (uint32_t)work.size(), r.o.fixed_ctx, r.L, r.C, r.kvb);
-    int rc = timed_run(r, res, [&](bool timed) -> int {
-        if (int e = r.launch(work.data(), (uint32_t)work.size())) return e;
+    int rc = timed_run(r, res, [&](Phase ph) -> int {
+        if (int e = r.launch(work.data(), (uint32_t)work.size(), ph == RAMP)) return e;
         // Roll back, so the next iteration appends the same positions.
         for (uint32_t i = 0; i < r.o.fixed_n; i++)
             if (int e = ni_kv_truncate(r.kv, seqs[i], r.o.fixed_ctx[i] - R)) return r.kv_fail(e, "truncate");
-        if (timed) {
+        if (ph == TIMED) {
             res->bytes += bytes;
             res->flops += flops;
             res->seq_tokens += (double)r.o.fixed_n * R;
@@ -631,7 +657,8 @@ int run_qkv(Runner& r, ni_drive_result* res) {
     const double flops = 2.0 * L * n * (double)d_in * F;
     float* x = r.d.q;    // [n][d_in]
     float* y = r.d.k;    // unfused: [n][3C]
-    int rc = timed_run(r, res, [&](bool timed) -> int {
+    // The projection has no append-only form: ramp iterations run whole.
+    int rc = timed_run(r, res, [&](Phase ph) -> int {
         for (uint32_t l = 0; l < L; l++) {
             const float* wl = w + (size_t)l * F * d_in;
             const float* bl = bias + (size_t)l * F;
@@ -648,7 +675,7 @@ int run_qkv(Runner& r, ni_drive_result* res) {
                     return r.kv_fail(e, "ni_kv_append");
             }
         }
-        if (timed) {
+        if (ph == TIMED) {
             res->bytes += bytes;
             res->flops += flops;
             res->seq_tokens += n;
@@ -660,6 +687,14 @@ int run_qkv(Runner& r, ni_drive_result* res) {
 }
 
 }  // namespace
+
+extern "C" int ni_drive_device_memory(int device, int* mem_clock_khz, int* bus_width_bits) {
+    if (!mem_clock_khz || !bus_width_bits) return drive_fail(NI_ERR_BAD_ARG, "NULL argument");
+    if (hipDeviceGetAttribute(mem_clock_khz, hipDeviceAttributeMemoryClockRate, device) != hipSuccess ||
+        hipDeviceGetAttribute(bus_width_bits, hipDeviceAttributeMemoryBusWidth, device) != hipSuccess)
+        return drive_fail(NI_ERR_HIP, "hipDeviceGetAttribute failed for device %d", device);
+    return NI_OK;
+}
 
 extern "C" int ni_drive_run(const ni_drive_opts* o, ni_drive_result* res) {
     if (!o || !res) return drive_fail(NI_ERR_BAD_ARG, "NULL argument");

@@ -147,6 +147,10 @@ struct ni_kv {
     hipStream_t copy_stream = nullptr;
     float* partials = nullptr;
     size_t partials_bytes = 0;
+    // Outgrown partials buffers: launches already enqueued may still use
+    // them, so they are freed only at ni_kv_destroy (each buffer is 1.5x the
+    // last, so together they stay below twice the current one).
+    std::vector<float*> partials_retired;
 
     uint32_t profile = 0;  // bit k: bracket kernel k's launches with events
     std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[NI_K_COUNT];
@@ -478,18 +482,19 @@ int acquire_slot(ni_kv* kv, size_t bytes, StagingSlot** out) {
     return NI_OK;
 }
 
-int ensure_partials(ni_kv* kv, size_t bytes) {
+int ensure_partials(ni_kv* kv, size_t bytes, float** out) {
+    *out = kv->partials;
     if (bytes <= kv->partials_bytes) return NI_OK;
-    // In-flight kernels may still read the old buffer.
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return kv->hip_fail(e, "hipDeviceSynchronize");
-    if (kv->partials) (void)hipFree(kv->partials);
-    kv->partials = nullptr;
-    kv->partials_bytes = 0;
-    size_t cap = align_up(bytes + bytes / 2, 1 << 20);
-    e = hipMalloc(reinterpret_cast<void**>(&kv->partials), cap);
+    // Launches already enqueued may still use the old buffer: retire it
+    // (no host wait here) rather than free it.
+    const size_t cap = align_up(bytes + bytes / 2, 1 << 20);
+    float* p = nullptr;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&p), cap);
     if (e != hipSuccess) return kv->hip_fail(e, "hipMalloc(partials)");
+    if (kv->partials) kv->partials_retired.push_back(kv->partials);
+    kv->partials = p;
     kv->partials_bytes = cap;
+    *out = p;
     return NI_OK;
 }
 
@@ -564,8 +569,9 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
     // Partials: the single-row/group launch's slots, then the prefill launch's.
     const size_t main_floats = (size_t)P.n_slots * n_lay * H * P.nq_tile * (D + 2);
     const size_t pre_floats = (size_t)P.n_pslots * n_lay * H * kPrefillRows * (D + 2);
+    float* partials = nullptr;
     if (main_floats + pre_floats > 0) {
-        int rc = ensure_partials(kv, (main_floats + pre_floats) * sizeof(float));
+        int rc = ensure_partials(kv, (main_floats + pre_floats) * sizeof(float), &partials);
         if (rc) return rc;
     }
     if (!P.app.empty() && !P.fused) {
@@ -605,7 +611,7 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
         a.off_items = (uint32_t)off.items;
         a.off_table = (uint32_t)off.table;
         a.off_merges = (uint32_t)off.merges;
-        a.partials = kv->partials;
+        a.partials = partials;
         a.n_items = (uint32_t)P.items.size();
         a.n_merges = (uint32_t)P.merges.size();
         a.layer0 = layer0;
@@ -640,7 +646,7 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
         a.off_items = (uint32_t)off.pitems;
         a.off_table = (uint32_t)off.table;
         a.off_merges = (uint32_t)off.pmerges;
-        a.partials = kv->partials ? kv->partials + main_floats : nullptr;
+        a.partials = partials ? partials + main_floats : nullptr;
         a.n_items = (uint32_t)P.pitems.size();
         a.n_merges = (uint32_t)P.pmerges.size();
         a.layer0 = layer0;
@@ -806,6 +812,7 @@ void ni_kv_destroy(ni_kv* kv) {
             }
         for (hipEvent_t e : kv->ev_pool) (void)hipEventDestroy(e);
         if (kv->partials) (void)hipFree(kv->partials);
+        for (float* p : kv->partials_retired) (void)hipFree(p);
         if (kv->kpool) (void)hipFree(kv->kpool);
         if (kv->copy_stream) (void)hipStreamDestroy(kv->copy_stream);
     }
@@ -1153,16 +1160,16 @@ int ni_kv_step_layer(ni_kv* kv, int32_t layer, const float* q, const float* k, c
         if (int rc = check_f32_operand(kv, "out", out, out_row_stride, 0, false)) return rc;
     }
     const hipStream_t s = (hipStream_t)stream;
+    // Every layer's launch uses the step's one set of split partials and its
+    // one staged plan, so the layers of a step run in order on one stream.
+    if (st.placed && s != st.stream)
+        return kv->fail(NI_ERR_BAD_ARG, "every layer of a step must run on the stream of its first layer");
     if (!st.placed) {
         if (int rc = place_plan(kv, P, st.blob, s, &st.off, &st.ref)) return rc;
         st.placed = true;
+        st.stream = s;
         if (st.ref.slot) st.ref.slot->held = true;
-    } else if (st.ref.slot && s != st.stream) {
-        // A staged plan was uploaded for the first layer's stream.
-        hipError_t e = hipStreamWaitEvent(s, st.ref.slot->uploaded, 0);
-        if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
     }
-    st.stream = s;
     return run_placed(kv, P, st.off, st.ref, (uint32_t)layer, 1, k, v, row_stride, 0, q, row_stride, 0, out,
                       out_row_stride, 0, s);
 }

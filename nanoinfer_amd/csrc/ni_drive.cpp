@@ -4,7 +4,9 @@
 // one JSON line.
 //
 //   ni_drive [serve|spec|qkv|prefill] [--per-layer|--step-layers] [--steps K] [--warmup W]
-//            [--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]
+//            [--ramp R] [--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]
+//
+// --ramp: R append-only iterations (no attention) before the warmup.
 //
 // --per-layer: ni_kv_append + ni_paged_decode_attention per layer;
 // --step-layers: ni_kv_step_begin, one ni_kv_step_layer per layer,
@@ -51,11 +53,12 @@ int main(int argc, char** argv) {
         else if (!strcmp(a, "--all-prompt-rows")) o.serve.query_all_prompt_rows = 1;
         else if (!strcmp(a, "--steps")) o.steps = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--warmup")) o.warmup = (uint32_t)atoi(val(a));
+        else if (!strcmp(a, "--ramp")) o.ramp = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--split")) o.split_tokens = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--seed")) o.data_seed = o.serve.seed = strtoull(val(a), nullptr, 10);
         else {
             fprintf(stderr, "usage: ni_drive [serve|spec|qkv|prefill] [--per-layer|--step-layers] [--steps K] [--warmup W] "
-                            "[--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]\n");
+                            "[--ramp R] [--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]\n");
             return 2;
         }
     }
@@ -115,12 +118,12 @@ int main(int argc, char** argv) {
     if (workload == "prefill")
         fprintf(stderr, "ni_drive: prefill 16 x %u rows: %.2f attention TFLOP/s over the whole step, %.3f ms per step\n",
                 o.fixed_rows, r.flops / r.seconds / 1e12, r.seconds / r.steps * 1e3);
-    printf("{\"driver\": \"ni_drive\", \"workload\": \"%s\", \"launch\": \"%s\", \"steps\": %u, \"warmup\": %u, "
+    printf("{\"driver\": \"ni_drive\", \"workload\": \"%s\", \"launch\": \"%s\", \"steps\": %u, \"ramp\": %u, \"warmup\": %u, "
            "\"value\": %.2f, \"unit\": \"GB/s\", \"pct_of_peak\": %.2f, \"ms_per_step\": %.5f, "
            "\"gpu_ms_per_step\": %.5f, \"host_us_per_step\": %.1f, \"abi_calls_per_step\": %.1f, "
            "\"seq_tokens_per_s\": %.1f, \"algorithmic_bytes_per_step\": %.0f, \"mean_live\": %.2f, "
            "\"mean_context\": %.1f, \"kv\": \"%s\"}\n",
-           workload.c_str(), o.launch == NI_DRIVE_STEP ? "step" : o.launch == NI_DRIVE_PER_LAYER ? "per-layer" : "step-layers", r.steps, o.warmup, gbs,
+           workload.c_str(), o.launch == NI_DRIVE_STEP ? "step" : o.launch == NI_DRIVE_PER_LAYER ? "per-layer" : "step-layers", r.steps, o.ramp, o.warmup, gbs,
            100.0 * gbs / 8000.0, r.seconds / r.steps * 1e3, r.gpu_seconds / r.steps * 1e3, r.host_us_per_step,
            (double)r.launches / r.steps, r.seq_tokens / r.seconds, r.bytes / r.steps, r.mean_live, r.mean_context, q8 ? "q8" : "f16");
     return 0;

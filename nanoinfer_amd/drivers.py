@@ -36,7 +36,7 @@ class ni_serve_iter(C.Structure):
 class ni_drive_opts(C.Structure):
     _fields_ = [("workload", _u32), ("launch", _u32), ("kv", _abi.ni_kv_opts), ("serve", ni_serve_opts),
                 ("spec_seqs", _u32), ("spec_ctx_min", _u32), ("spec_ctx_max", _u32), ("spec_k", _u32),
-                ("spec_seed", C.c_uint64), ("spec_window", _u32), ("warmup", _u32), ("steps", _u32),
+                ("spec_seed", C.c_uint64), ("spec_window", _u32), ("ramp", _u32), ("warmup", _u32), ("steps", _u32),
                 ("split_tokens", _u32), ("data_seed", C.c_uint64), ("fixed_ctx", C.POINTER(_u32)),
                 ("fixed_n", _u32), ("kv_std", C.c_float), ("profile_mask", _u32), ("qkv_rows", _u32),
                 ("fixed_rows", _u32)]
@@ -78,6 +78,7 @@ def lib():
     L.ni_drive_run.argtypes = [C.POINTER(ni_drive_opts), C.POINTER(ni_drive_result)]
     L.ni_drive_last_error.restype = C.c_char_p
     L.ni_drive_last_error.argtypes = []
+    L.ni_drive_device_memory.argtypes = [C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]
     _lib = L
     return L
 
@@ -163,6 +164,13 @@ class Spec:
             self._h = None
 
 
+def device_memory(device: int = 0) -> tuple[int, int]:
+    """(peak memory clock in kHz, bus width in bits) as HIP reports them."""
+    clk, bits = C.c_int(), C.c_int()
+    _check(lib().ni_drive_device_memory(device, C.byref(clk), C.byref(bits)), "ni_drive_device_memory")
+    return clk.value, bits.value
+
+
 def drive(opts: ni_drive_opts) -> dict:
     """ni_drive_run: a whole synthetic run on the device (C++ host loop)."""
     r = ni_drive_result()
@@ -190,14 +198,16 @@ PREFILL_SEQS, PREFILL_ROWS = 16, 512
 
 
 def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, split: int = 0, seed: int = 7,
-           profile_mask: int = 0, query_all_prompt_rows: bool = False) -> ni_drive_opts:
-    """ni_drive_opts of benchmark configuration 2, 3, 4 or 5, the QKV projection (qkvN) or the prefill workload."""
+           profile_mask: int = 0, query_all_prompt_rows: bool = False, ramp: int = 0) -> ni_drive_opts:
+    """ni_drive_opts of benchmark configuration 2, 3, 4 or 5, the QKV projection (qkvN) or the prefill workload.
+    `ramp` untimed append-only iterations precede the `warmup` full ones."""
     from . import workloads
 
     o = ni_drive_opts()
     o._keep = []  # arrays the struct points into
     o.launch, o.steps, o.warmup, o.split_tokens, o.data_seed, o.profile_mask = launch, steps, warmup, split, seed, \
         profile_mask
+    o.ramp = ramp
     q8 = name.endswith("q8")  # the same workload on a Q8 cache
     if q8:
         name = name[:-2]

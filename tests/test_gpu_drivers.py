@@ -16,6 +16,8 @@ import numpy as np
 import pytest
 import torch
 
+import oracle
+
 import nanoinfer_amd as na
 from nanoinfer_amd import drivers, workloads
 
@@ -155,9 +157,21 @@ def test_decode_steps_equal_single_steps(gpu):
         h.reserve(s, L)
     for s, L in zip(seqs, lens):
         h.reserve(s, L + T)
+    # The same order on the oracle's allocator (batch.rs:159-254 restated):
+    # fill, then every sequence's pages for all steps, then the commits.
+    al = oracle.Alloc(opts.kv_blocks, opts.max_seqs, opts.n_ctx)
     for s, L in zip(seqs, lens):
-        assert a.seq_len(s) == b.seq_len(s) == L + T
-        assert a.block_table(s) == h.block_table(s)
+        assert al.add_seq() == s
+        assert al.ensure(s, L) == 0
+        al.commit(s, L)
+    for s, L in zip(seqs, lens):
+        assert al.ensure(s, L + T) == 0
+    for s in seqs:
+        al.commit(s, T)
+    assert a.free_block_count() == al.free_block_count() and a.blocks_used() == al.blocks_used()
+    for s, L in zip(seqs, lens):
+        assert a.seq_len(s) == b.seq_len(s) == al.seq_len(s) == L + T
+        assert a.block_table(s) == h.block_table(s) == al.block_table(s)
         rows = [(s, p) for p in range(max(0, L + T - 64), L + T)]
         ka, va = a.gather(rows)
         kb, vb = b.gather(rows)

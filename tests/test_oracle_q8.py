@@ -61,3 +61,63 @@ def test_q8_attention_reduces_to_f16_attention(oracle_lib):
     got = oracle.paged_q8_attention(pools8, 0, table, 8, np.zeros(3, np.uint32), rows_p, q)
     want = oracle.paged_attention(pools16, 0, table, 8, np.zeros(3, np.uint32), rows_p, q, H, D)
     assert np.abs(got - want).max() < 1e-3 * np.abs(want).max()
+
+
+def _np_attention_f64(q, k, v, n_kv, n_head, hd):
+    """Softmax attention of one row over keys 0..n_kv-1 in float64 (the
+    mathematics kv8.metal:50-95 computes: scores (q.k)/sqrt(hd), then the
+    probability-weighted sum of V)."""
+    out = np.zeros(n_head * hd)
+    for h in range(n_head):
+        sl = slice(h * hd, (h + 1) * hd)
+        s = (k[:n_kv, sl] @ q[sl].astype(np.float64)) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        out[sl] = (p / p.sum()) @ v[:n_kv, sl]
+    return out
+
+
+def test_q8_attention_matches_float64_with_spread_scales(oracle_lib):
+    """Scales spread over 1e-3..30 per (position, head), different for K and
+    V: the oracle's Q8 attention equals a float64 closed form over the
+    dequantised values kq*ks and vq*vs.  Two planted mistakes (on the CPU,
+    in the pools the oracle reads): key scales dropped, value scales
+    dropped -- each must move the result far outside the tolerance."""
+    rng = np.random.default_rng(82)
+    H, D, L, P = 3, 64, 150, 16
+    C = H * D
+    pages = -(-L // 16)
+    pools = oracle.PagedPoolsQ8(1, 32, H, D)
+    table = np.zeros((1, 32), np.uint32)
+    table[0, :pages] = rng.permutation(32)[:pages]
+    # per (position, head) target scales log-uniform in [1e-3, 30]
+    sk = np.exp(rng.uniform(np.log(1e-3), np.log(30), (L, H)))
+    sv = np.exp(rng.uniform(np.log(1e-3), np.log(30), (L, H)))
+    k = (rng.uniform(-1, 1, (L, H, D)) * 127 * sk[:, :, None]).astype(np.float32).reshape(L, C)
+    v = (rng.uniform(-1, 1, (L, H, D)) * 127 * sv[:, :, None]).astype(np.float32).reshape(L, C)
+    seqs = np.zeros(L, np.uint32)
+    poss = np.arange(L, dtype=np.uint32)
+    oracle.paged_q8_append(pools, 0, table, 32, seqs, poss, k, v)
+    (kq, vq), (ks, vs) = oracle.paged_q8_gather(pools, 0, table, 32, seqs, poss)
+    assert ks.min() < 3e-3 and ks.max() > 10 and vs.min() < 3e-3 and vs.max() > 10
+    kd = (kq.reshape(L, H, D).astype(np.float64) * ks[:, :, None]).reshape(L, C)
+    vd = (vq.reshape(L, H, D).astype(np.float64) * vs[:, :, None]).reshape(L, C)
+    # dequantised values are within half a step of the inputs (the scales are real)
+    assert (np.abs(kd - k).reshape(L, H, D) <= 0.5 * ks[:, :, None] * (1 + 1e-5)).all()
+    rows_p = np.array([0, 15, 16, 77, L - 1], np.uint32)
+    q = (rng.standard_normal((len(rows_p), C)) * 0.02).astype(np.float32)
+    want = np.stack([_np_attention_f64(q[i], kd, vd, int(p) + 1, H, D) for i, p in enumerate(rows_p)])
+    tol = lambda w: 1e-6 * np.abs(w).max() + 1e-6 * np.abs(w)  # noqa: E731
+    got = oracle.paged_q8_attention(pools, 0, table, 32, np.zeros(len(rows_p), np.uint32), rows_p, q)
+    assert (np.abs(got - want) <= tol(want)).all(), np.abs(got - want).max()
+    # planted: the oracle reading every key scale as 1
+    ks_saved, vs_saved = pools.ks.copy(), pools.vs.copy()
+    pools.ks[:] = 1.0
+    bad = oracle.paged_q8_attention(pools, 0, table, 32, np.zeros(len(rows_p), np.uint32), rows_p, q)
+    assert np.abs(bad - want).max() > 100 * tol(want).max()
+    # planted: the oracle reading every value scale as 1
+    pools.ks[:], pools.vs[:] = ks_saved, 1.0
+    bad = oracle.paged_q8_attention(pools, 0, table, 32, np.zeros(len(rows_p), np.uint32), rows_p, q)
+    assert np.abs(bad - want).max() > 100 * tol(want).max()
+    pools.vs[:] = vs_saved
+    again = oracle.paged_q8_attention(pools, 0, table, 32, np.zeros(len(rows_p), np.uint32), rows_p, q)
+    assert np.array_equal(again, got)
