@@ -186,6 +186,22 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
                int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
                int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream);
 
+/* ni_kv_step that allocates nothing.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, checks, errors and results as ni_kv_step (the same kernels over
+ * the same plan), but no hipMalloc, hipFree, staging upload or event
+ * creation: the split-K partials live in a file-scope device array of
+ * 32 MiB, one per GPU, held until the process ends, and the plan travels in
+ * the launch arguments.  A step whose plan exceeds 32 KB or whose partials
+ * exceed 32 MiB returns NI_ERR_BAD_ARG with the limit in the message (its
+ * pages stay reserved, as after any failed launch; nothing is launched).
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, other handles) race. */
+int ni_kv_step_noalloc(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
+                       const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
+                       int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream);
+
 /* The same step one layer at a time, as a model's forward runs it: the
  * reference encodes a step once (Batch::encode_step, batch.rs:280-306: check,
  * reserve, lay out the rows) and then dispatches each layer's KV write and

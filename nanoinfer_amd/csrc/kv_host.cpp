@@ -151,6 +151,11 @@ struct ni_kv {
     // them, so they are freed only at ni_kv_destroy (each buffer is 1.5x the
     // last, so together they stay below twice the current one).
     std::vector<float*> partials_retired;
+    // ni_kv_step_noalloc: this device's scratch array (null if its address
+    // could not be found), and set for the duration of such a call.
+    float* scratch = nullptr;
+    hipError_t scratch_err = hipSuccess;
+    bool no_alloc = false;
 
     uint32_t profile = 0;  // bit k: bracket kernel k's launches with events
     std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[NI_K_COUNT];
@@ -444,7 +449,8 @@ struct ProfileScope {
     int kernel;
     LaunchTiming t;
     ProfileScope(ni_kv* kv_, int k) : kv(kv_), kernel(k) {
-        if (!(kv->profile & (1u << k))) return;
+        // No event creation inside ni_kv_step_noalloc.
+        if (!(kv->profile & (1u << k)) || kv->no_alloc) return;
         t.start = take_event(kv);
         t.stop = take_event(kv);
         if (!t.start || !t.stop) t = LaunchTiming{};
@@ -483,6 +489,15 @@ int acquire_slot(ni_kv* kv, size_t bytes, StagingSlot** out) {
 }
 
 int ensure_partials(ni_kv* kv, size_t bytes, float** out) {
+    if (kv->no_alloc) {
+        if (bytes > kScratchBytes)
+            return kv->fail(NI_ERR_BAD_ARG,
+                            "the step needs %zu bytes of split partials; ni_kv_step_noalloc holds at most %zu "
+                            "(a larger split_tokens, or ni_kv_step)",
+                            bytes, kScratchBytes);
+        *out = kv->scratch;
+        return NI_OK;
+    }
     *out = kv->partials;
     if (bytes <= kv->partials_bytes) return NI_OK;
     // Launches already enqueued may still use the old buffer: retire it
@@ -525,6 +540,17 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
         memcpy(blob.data() + off->pmerges, P.pmerges.data(), P.pmerges.size() * sizeof(MergeItem));
     if (!P.table.empty()) memcpy(blob.data() + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
     *ref = PlanRef{};
+    if (kv->no_alloc) {
+        // No staging slot (it would be allocated): the plan travels inline.
+        if (off->total > kInlinePlanBytes)
+            return kv->fail(NI_ERR_BAD_ARG,
+                            "the step's plan is %zu bytes; ni_kv_step_noalloc passes plans of at most %u bytes "
+                            "with the launch (fewer sequences or shorter contexts per call, or ni_kv_step)",
+                            off->total, kInlinePlanBytes);
+        ref->inl = blob.data();
+        ref->inl_bytes = (uint32_t)off->total;
+        return NI_OK;
+    }
     if (!NI_STAGE_ALL_PLANS && off->total <= kInlinePlanBytes) {
         ref->inl = blob.data();
         ref->inl_bytes = (uint32_t)off->total;
@@ -783,6 +809,13 @@ int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
         }
         // Default priority: the copy stream only moves plans.
         if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->copy_stream, hipStreamNonBlocking);
+        // The no-allocation entry point's scratch on this device (a failure
+        // here disables only that entry point).
+        if (e == hipSuccess) {
+            void* p = nullptr;
+            kv->scratch_err = scratch_address(&p);
+            kv->scratch = kv->scratch_err == hipSuccess ? static_cast<float*>(p) : nullptr;
+        }
         if (e != hipSuccess) {
             g_create_error = std::string("device setup failed: ") + hipGetErrorString(e);
             ni_kv_destroy(kv);
@@ -1121,6 +1154,23 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
     if (int rc = prepare_step(kv, work, n_work)) return rc;
     return enqueue_step(kv, work, n_work, q, k, v, row_stride, layer_stride, out, out_row_stride, out_layer_stride,
                         split_tokens, (hipStream_t)stream);
+}
+
+int ni_kv_step_noalloc(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
+                       const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
+                       int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream) {
+    if (!kv) return NI_ERR_BAD_ARG;
+    if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
+    if (!kv->scratch)
+        return kv->fail(NI_ERR_HIP, "ni_kv_step_noalloc: no scratch on this device (hipGetSymbolAddress: %s)",
+                        hipGetErrorString(kv->scratch_err));
+    struct Scope {
+        ni_kv* kv;
+        explicit Scope(ni_kv* k_) : kv(k_) { kv->no_alloc = true; }
+        ~Scope() { kv->no_alloc = false; }
+    } scope(kv);
+    return ni_kv_step(kv, work, n_work, q, k, v, row_stride, layer_stride, out, out_row_stride, out_layer_stride,
+                      split_tokens, stream);
 }
 
 int ni_kv_step_begin(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t split_tokens) {

@@ -30,6 +30,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "kv_plan.h"
 
@@ -2184,6 +2186,35 @@ hipError_t attn_dispatch(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
 }  // namespace
 
 bool attention_supported(uint32_t head_dim) { return head_dim == 64 || head_dim == 128; }
+
+// Split-K partials of ni_kv_step_noalloc's launches: a file-scope device
+// array, so that entry point calls no allocator.  Each GPU the library runs
+// on holds its own copy until the process ends; every such call on a GPU
+// shares it (calls that overlap on one GPU race).  Nothing in it needs to
+// start at zero: a merge reads only the partials its own call's attention
+// launch wrote first, on the same stream.
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+hipError_t scratch_address(void** out) {
+    // In host code `scratch` names a host-side stand-in, not device memory:
+    // only the address hipGetSymbolAddress returns for the current device
+    // may reach a kernel or a copy.
+    static std::mutex mu;
+    static std::vector<void*> per_device;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((size_t)dev >= per_device.size()) per_device.resize((size_t)dev + 1, nullptr);
+    if (!per_device[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        per_device[dev] = p;
+    }
+    *out = per_device[dev];
+    return hipSuccess;
+}
 
 hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     const uint64_t threads = (uint64_t)a.n_lay * a.n_rows * 2 * ((a.pool.n_head * a.pool.head_dim) >> 3);

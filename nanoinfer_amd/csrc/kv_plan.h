@@ -201,6 +201,14 @@ struct AttnLaunch {
 // per-layer call's plan (64 sequences) is 5-9 KB.
 constexpr uint32_t kInlinePlanBytes = 32768, kInlinePlanSmall = 16384;
 
+// Device scratch of the no-allocation entry point (ni_kv_step_noalloc): the
+// split-K partials of its launches, in a file-scope device array of this
+// many bytes (kv_kernels.hip), one copy per GPU the library runs on.
+constexpr size_t kScratchBytes = 32u << 20;
+// The device address of that array on the current device, looked up once
+// per device (hipGetSymbolAddress) and kept.
+hipError_t scratch_address(void** out);
+
 // Kernel launchers (kv_kernels.hip).  They validate nothing; the host checks
 // every index the plan holds before calling them.
 // `inline_plan` (nullptr: the plan is at a.plan on the device) holds
