@@ -333,12 +333,59 @@ def copy_ceiling(nbytes=2 << 30, reps=5):
 
 
 def hbm_peak_reported():
-    """The HBM peak the device itself reports: 2 transfers per memory clock
-    (DDR) x bus width, from hipDeviceGetAttribute."""
+    """What the device reports of its memory interface (hipDeviceGetAttribute).
+    HIP gives the bus width and a memory clock but not the per-pin data rate,
+    so the peak is AMD's published figure; the bus width is the check."""
     from nanoinfer_amd import drivers
 
     clk, bits = drivers.device_memory(0)
-    return {"mem_clock_khz": clk, "bus_width_bits": bits, "ddr_peak_gbs": round(2 * clk * 1e3 * bits / 8 / 1e9, 1)}
+    return {"mem_clock_khz": clk, "bus_width_bits": bits,
+            "note": f"{bits}-bit bus x 8.0 Gb/s per pin (HBM3E) = {bits * 8 / 8:.0f} GB/s; AMD publishes 8.0 TB/s, "
+                    f"the peak used"}
+
+
+def stream_ceiling(nbytes=2 << 30, reps=5, blocks=(1024, 2048, 4096, 8192)):
+    """The library's streaming probe (ni_stream_probe: 16-byte non-temporal
+    loads, 4 in flight per thread) over `nbytes`, read and copy, each in a
+    grid stride and in one contiguous span per workgroup, for each launch
+    size; timed with events on torch's stream, median of `reps` after one
+    untimed pass.  The best pattern and size per kind is the ceiling."""
+    import torch
+
+    from nanoinfer_amd import _abi
+
+    L = _abi.lib()
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    st = torch.cuda.current_stream().cuda_stream
+    out, all_runs = {}, {}
+    for copy in (0, 1):
+        best = None
+        for span in (0, 2):
+            for b in blocks:
+                ts = []
+                for r in range(reps + 1):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    rc = L.ni_stream_probe(copy | span, src.data_ptr(), dst.data_ptr(), nbytes, b, st)
+                    e1.record()
+                    if rc != 0:
+                        raise RuntimeError(f"ni_stream_probe: status {rc}")
+                    e1.synchronize()
+                    if r:
+                        ts.append(e0.elapsed_time(e1) / 1e3)
+                gbs = (2 if copy else 1) * nbytes / float(np.median(ts)) / 1e9
+                all_runs[f"{'copy' if copy else 'read'}/{'span' if span else 'stride'}/{b}"] = round(gbs, 1)
+                if best is None or gbs > best[0]:
+                    best = (gbs, b, "span" if span else "stride")
+        out["copy" if copy else "read"] = {"value": round(best[0], 1), "unit": "GB/s", "blocks": best[1],
+                                           "pattern": best[2]}
+    del src, dst
+    torch.cuda.empty_cache()
+    out["all"] = all_runs
+    out["method"] = (f"ni_stream_probe over {nbytes >> 20} MiB (copy: read + write bytes), grid stride and one span "
+                     f"per workgroup, {list(blocks)} workgroups of 256 threads, median of {reps}")
+    return out
 
 
 # Config 3's timed window: an untimed append-only ramp of RAMP_STEPS trace
@@ -396,6 +443,7 @@ def run_config3(args):
                 "synthetic (seeded N(0,1) q/k/v resident in HBM, seeded Poisson request trace)")
     res["repetitions"] = spread
     res["copy_ceiling"] = copy_ceiling()
+    res["stream_ceiling"] = stream_ceiling()
     try:
         res["hbm_peak_reported"] = hbm_peak_reported()
     except RuntimeError as e:

@@ -247,7 +247,19 @@ int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes);
 /* quant.rs:25-54 on the device, elementwise (the conversion the append uses). */
 int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream);
 
-/* ---- measurement: HIP event timestamps of this handle's kernel launches ---- */
+/* ---- measurement ---- */
+/* The streaming rate the hot path is held against (no counterpart in the
+ * reference): `blocks` workgroups of 256 threads walk `bytes` (a multiple of
+ * 16, at least blocks * 4096) of src in 16-byte non-temporal loads.
+ * mode & NI_PROBE_COPY: each unit is also stored to dst (bytes long); else a
+ * read only (dst, at least bytes long, is in practice not written).
+ * mode & NI_PROBE_SPAN: each workgroup walks one contiguous span of the
+ * buffer; else a grid stride.  Enqueued on `stream`; time it with events. */
+#define NI_PROBE_COPY 1u
+#define NI_PROBE_SPAN 2u
+int ni_stream_probe(uint32_t mode, const void* src, void* dst, size_t bytes, uint32_t blocks, ni_stream stream);
+
+/* HIP event timestamps of this handle's kernel launches. */
 enum ni_kernel_id { NI_K_APPEND = 0, NI_K_ATTN = 1, NI_K_MERGE = 2, NI_K_QKV = 3, NI_K_COUNT = 4 };
 /* Bit k of kernel_mask times every launch of kernel k (ni_kernel_id): the
  * dispatch itself records the kernel's start and end into a pair of HIP

@@ -109,6 +109,8 @@ def _declare(L):
                                             _i64, _u32, _vp]
     L.ni_kv_step.restype = C.c_int
     L.ni_kv_step.argtypes = [_vp, C.POINTER(ni_work), _u32, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _u32, _vp]
+    L.ni_stream_probe.restype = C.c_int
+    L.ni_stream_probe.argtypes = [_u32, _vp, _vp, C.c_size_t, _u32, _vp]
     L.ni_kv_step_noalloc.restype = C.c_int
     L.ni_kv_step_noalloc.argtypes = L.ni_kv_step.argtypes
     L.ni_kv_step_begin.restype = C.c_int

@@ -1391,6 +1391,14 @@ int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream) {
     return e == hipSuccess ? NI_OK : NI_ERR_HIP;
 }
 
+int ni_stream_probe(uint32_t mode, const void* src, void* dst, size_t bytes, uint32_t blocks, ni_stream stream) {
+    if (!src || !dst || bytes % 16 || blocks == 0 || (mode & ~3u)) return NI_ERR_BAD_ARG;
+    if ((size_t)blocks * 256 * 16 > bytes) return NI_ERR_BAD_ARG;  // a read's dst holds a unit per thread
+    hipError_t e = launch_stream((mode & NI_PROBE_COPY) != 0, (mode & NI_PROBE_SPAN) != 0, src, dst, bytes, blocks,
+                                 (hipStream_t)stream);
+    return e == hipSuccess ? NI_OK : NI_ERR_HIP;
+}
+
 int ni_kv_profile(ni_kv* kv, uint32_t kernel_mask) {
     if (!kv) return NI_ERR_BAD_ARG;
     if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device");

@@ -263,6 +263,59 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict
     if (i < n) out[i] = static_cast<uint16_t>(f16_bits(in[i]));
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------- bandwidth probe
+
+// The memory system's streaming rate, beside which the hot path's roofline
+// fraction is read.  Threads move 16-byte units with non-temporal loads, 4
+// independent ones in flight per iteration.  SPAN = false: a grid stride
+// (unit i, i + G, ... for G threads in the grid); SPAN = true: workgroup b
+// walks its own contiguous 1/gridDim of the buffer, 16 KB per iteration
+// (the kind of run the attention kernel reads: whole blocks).  COPY stores
+// each unit to dst; otherwise the units are folded and the fold is stored
+// only if it equals a value it cannot reach in practice (the loads stay,
+// nothing is written).
+template <bool COPY, bool SPAN>
+__global__ __launch_bounds__(256) void stream_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                     uint64_t n16) {
+    uint64_t i, end, stride;
+    if (SPAN) {
+        const uint64_t span = (n16 + gridDim.x - 1) / gridDim.x;
+        i = (uint64_t)blockIdx.x * span + threadIdx.x;
+        end = min((uint64_t)(blockIdx.x + 1) * span, n16);
+        stride = 256;
+    } else {
+        i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+        end = n16;
+        stride = (uint64_t)gridDim.x * 256u;
+    }
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (; i + 3 * stride < end; i += 4 * stride) {
+        u32x4 a = __builtin_nontemporal_load(src + i);
+        u32x4 b = __builtin_nontemporal_load(src + i + stride);
+        u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+        u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+        if (COPY) {
+            __builtin_nontemporal_store(a, dst + i);
+            __builtin_nontemporal_store(b, dst + i + stride);
+            __builtin_nontemporal_store(c, dst + i + 2 * stride);
+            __builtin_nontemporal_store(d, dst + i + 3 * stride);
+        } else {
+            acc ^= a ^ b ^ c ^ d;
+        }
+    }
+    for (; i < end; i += stride) {
+        u32x4 a = __builtin_nontemporal_load(src + i);
+        if (COPY)
+            __builtin_nontemporal_store(a, dst + i);
+        else
+            acc ^= a;
+    }
+    if (!COPY && acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0x85ebca6bu && acc.w == 0xc2b2ae35u)
+        dst[(uint64_t)blockIdx.x * 256u + threadIdx.x] = acc;
+}
+
 // --------------------------------------------------------------- attention
 
 // Tuning knobs of the split kernel (compile-time; the defaults are the
@@ -282,8 +335,6 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict
 #ifndef NI_ATTN_LDS_PAD
 #define NI_ATTN_LDS_PAD 0    // extra LDS floats per workgroup (caps workgroups per CU)
 #endif
-
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ u32x4 load16(const u32x4* p) {
 #if NI_ATTN_NT
@@ -2271,6 +2322,20 @@ uint32_t orphan_blocks(const AttnLaunch& a) {
 
 hipError_t launch_merge(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     return attn_dispatch(a, ip, ib, s, true, t);
+}
+
+hipError_t launch_stream(bool copy, bool span, const void* src, void* dst, size_t bytes, uint32_t blocks,
+                         hipStream_t s) {
+    const uint64_t n16 = bytes / 16;
+    if (n16 == 0 || blocks == 0) return hipSuccess;
+    const auto* in = static_cast<const u32x4*>(src);
+    auto* out = static_cast<u32x4*>(dst);
+    const dim3 g(blocks), t(256);
+    if (copy && span) hipLaunchKernelGGL((stream_kernel<true, true>), g, t, 0, s, in, out, n16);
+    if (copy && !span) hipLaunchKernelGGL((stream_kernel<true, false>), g, t, 0, s, in, out, n16);
+    if (!copy && span) hipLaunchKernelGGL((stream_kernel<false, true>), g, t, 0, s, in, out, n16);
+    if (!copy && !span) hipLaunchKernelGGL((stream_kernel<false, false>), g, t, 0, s, in, out, n16);
+    return hipGetLastError();
 }
 
 hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s) {

@@ -229,6 +229,11 @@ hipError_t launch_attention(const AttnLaunch& a, const void* inline_plan, uint32
 hipError_t launch_merge(const AttnLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
                         const LaunchTiming& t = {});
 hipError_t launch_f32_to_f16(const float* in, uint16_t* out, size_t n, hipStream_t s);
+// Streaming read (copy = false; dst receives nothing in practice but needs
+// blocks * 256 * 16 bytes) or copy of `bytes` (a multiple of 16), in a grid
+// stride or (span) one contiguous span per workgroup.
+hipError_t launch_stream(bool copy, bool span, const void* src, void* dst, size_t bytes, uint32_t blocks,
+                         hipStream_t s);
 hipError_t launch_qkv(const QkvLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
                       const LaunchTiming& t = {});
 // Blocks a fused launch needs for its orphan rows (n_orphans set).
