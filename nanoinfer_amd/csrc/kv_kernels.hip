@@ -953,14 +953,49 @@ __global__ __launch_bounds__(64 * W) void attn_q8_kernel(const AttnLaunch a, con
 // uses component c of both, so lane group g supplies k = 4g + c to A and B
 // alike.
 //
-// The tile is 32 rows x 16*FB features.  x and W arrive through LDS in
-// chunks of kQkvChunk values of d_in, each row segment loaded contiguously
-// (a wave-wide load covers 1 KB of one or two rows); the next chunk is in
-// registers while the current one is multiplied.  Wave w owns row block
-// w & 1 and half (w >> 1) of every chunk; the two halves are added in a
-// fixed order, so the result does not depend on scheduling.
+// Summation order, the same for every row count and both kernels below (so
+// a row's bits never depend on the batch it is projected in): slice s of
+// d_in belongs to part s % 8; part p's accumulator takes the 4 products of
+// each of its slices in increasing s (components x, y, z, w in turn), and
+// y = (((P0 + P1) + (P2 + P3)) + ((P4 + P5) + (P6 + P7))) + bias.
+constexpr int kQkvParts = 8;
+// Rows up to which qkv_small_kernel runs (kernel time per layer, GPT-2
+// 768 -> 2304: 1 row 4.66 against 7.11 us, 16 rows 6.15 against 7.61 us; from
+// 24 rows its 64-byte row pieces per load lose to the LDS-staged kernel's
+// whole-row reads: 24 rows 8.98 against 7.65 us, 64 rows 11.9 against 9.5).
+#ifndef NI_QKV_SMALL_ROWS
+#define NI_QKV_SMALL_ROWS 16
+#endif
+#ifndef NI_QKV_SMALL_RB
+#define NI_QKV_SMALL_RB 1      // 16-row blocks per workgroup of the small-batch kernel
+#endif
+
+// Large row counts: the tile is 32 rows x 16*FB features.  x and W arrive
+// through LDS in chunks of kQkvChunk values of d_in (8 slices, one per
+// part), each row segment loaded contiguously (a wave-wide load covers 1 KB
+// of one or two rows); the next chunk is in registers while the current one
+// is multiplied.  Wave w owns row block w & 1 and parts 4 (w >> 1) ..
+// 4 (w >> 1) + 3, i.e. half (w >> 1) of every chunk.
 constexpr int kQkvChunk = 128;
 constexpr int kQkvPad = kQkvChunk + 4;  // LDS row stride (floats): conflict-free 16-byte reads
+static_assert(kQkvChunk == 16 * kQkvParts, "one slice per part per chunk");
+
+// Output y of (row, feature f): q columns (or every column when not fused)
+// to `out`, k/v as f16 (the append's rounding) into the row's page slot.
+__device__ __forceinline__ void qkv_store(const QkvLaunch& a, const AppendEntry* entries, uint32_t row, uint32_t f,
+                                          float y) {
+    const uint32_t C = a.n_feat / 3, D = a.pool.head_dim;
+    if (!a.fused || f < C) {
+        a.out[(int64_t)row * a.out_row_stride + f] = y;
+    } else {
+        const AppendEntry en = entries[row];
+        const uint32_t is_v = f >= 2 * C;
+        const uint32_t c = f - C - is_v * C, head = c / D, d = c - head * D;
+        uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)a.layer * a.pool.layer_halves +
+                        (uint64_t)en.page * a.pool.page_halves + (uint64_t)head * a.pool.head_halves + en.slot * D + d;
+        *dst = (uint16_t)f16_bits(y);
+    }
+}
 
 template <int FB, int INL>
 __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
@@ -995,9 +1030,12 @@ __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanA
                                       : float4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    f4 acc[FB];
+    f4 acc[FB][4];  // the wave's 4 parts
 #pragma unroll
-    for (int fb = 0; fb < FB; fb++) acc[fb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int fb = 0; fb < FB; fb++)
+#pragma unroll
+        for (int pp = 0; pp < 4; pp++) acc[fb][pp] = f4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t n_slices = a.d_in / 16;
     fetch(0);
     for (uint32_t k0 = 0; k0 < a.d_in; k0 += KC) {
         __syncthreads();  // the previous chunk's products are done with LDS
@@ -1013,33 +1051,41 @@ __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanA
         }
         __syncthreads();
         if (k0 + KC < a.d_in) fetch(k0 + KC);
-        // This wave's half of the chunk: slices of 16; lane (i, g) holds k =
-        // 4g .. 4g+3 of the slice for row 16rb + i and for feature 16fb + i.
+        // This wave's half of the chunk: slices of 16, slice sl of the half
+        // is part 4 kh + sl; lane (i, g) holds k = 4g .. 4g+3 of the slice
+        // for row 16rb + i and for feature 16fb + i.  Slices past d_in (the
+        // last chunk's zeros) are skipped, as the small-batch kernel does.
 #pragma unroll
         for (int sl = 0; sl < KC / 32; sl++) {
+            const uint32_t slice = k0 / 16 + kh * (KC / 32) + sl;
+            if (slice >= n_slices) break;
             const int kk = (kh * (KC / 32) + sl) * 16 + 4 * g;
             const float4 xv = *reinterpret_cast<const float4*>(&xs[16 * rb + i][kk]);
 #pragma unroll
             for (int fb = 0; fb < FB; fb++) {
                 const float4 wv = *reinterpret_cast<const float4*>(&ws[16 * fb + i][kk]);
-                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, wv.x, acc[fb], 0, 0, 0);
-                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, wv.y, acc[fb], 0, 0, 0);
-                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, wv.z, acc[fb], 0, 0, 0);
-                acc[fb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, wv.w, acc[fb], 0, 0, 0);
+                acc[fb][sl] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, wv.x, acc[fb][sl], 0, 0, 0);
+                acc[fb][sl] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, wv.y, acc[fb][sl], 0, 0, 0);
+                acc[fb][sl] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, wv.z, acc[fb][sl], 0, 0, 0);
+                acc[fb][sl] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, wv.w, acc[fb][sl], 0, 0, 0);
             }
         }
     }
+    // Each wave's parts summed as (Pa + Pb) + (Pc + Pd); half 1's sum goes
+    // to LDS for half 0's waves.
+    f4 half[FB];
+#pragma unroll
+    for (int fb = 0; fb < FB; fb++) half[fb] = (acc[fb][0] + acc[fb][1]) + (acc[fb][2] + acc[fb][3]);
     if (kh == 1) {
 #pragma unroll
         for (int fb = 0; fb < FB; fb++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) red[rb][fb][e][lane] = acc[fb][e];
+            for (int e = 0; e < 4; e++) red[rb][fb][e][lane] = half[fb][e];
     }
     __syncthreads();
     if (kh == 1) return;
     // Output (row 16rb + 4g + e, feature 16fb + i) is element e of lane
     // i + 16g's block fb (the matrix-core output layout).
-    const uint32_t C = a.n_feat / 3, D = a.pool.head_dim;
     const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
 #pragma unroll
     for (int fb = 0; fb < FB; fb++) {
@@ -1049,19 +1095,76 @@ __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanA
         for (int e = 0; e < 4; e++) {
             const uint32_t row = m0 + 16 * rb + 4 * g + e;
             if (row >= a.n_rows) break;
-            const float y = acc[fb][e] + red[rb][fb][e][lane] + b;
-            if (!a.fused || f < C) {
-                a.out[(int64_t)row * a.out_row_stride + f] = y;
-            } else {
-                const AppendEntry en = entries[row];
-                const uint32_t is_v = f >= 2 * C;
-                const uint32_t c = f - C - is_v * C, head = c / D, d = c - head * D;
-                uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)a.layer * a.pool.layer_halves +
-                                (uint64_t)en.page * a.pool.page_halves + (uint64_t)head * a.pool.head_halves +
-                                en.slot * D + d;
-                *dst = (uint16_t)f16_bits(y);
+            qkv_store(a, entries, row, f, (half[fb][e] + red[rb][fb][e][lane]) + b);
+        }
+    }
+}
+
+// Small row counts (single-sequence and small-batch decode): a workgroup of
+// 8 waves owns a 16*RB-row x 16-feature tile, wave p computes part p over
+// all of d_in with its operands loaded straight from memory into the
+// matrix-core layout (up to kQkvBatch slices of x and W in flight per wave,
+// so d_in 768 is one round of loads instead of qkv_kernel's six chunks),
+// and the 8 parts meet in LDS.  The same products in the same order as
+// qkv_kernel, so the bits are the same at every row count.
+constexpr int kQkvBatch = 6;
+
+template <int RB, int INL>
+__global__ __launch_bounds__(64 * kQkvParts) void qkv_small_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __shared__ f4 red[kQkvParts][RB][64];
+    const int lane = threadIdx.x & 63;
+    const uint32_t p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = lane & 15, g = lane >> 4;
+    const uint32_t m0 = blockIdx.x * 16 * RB, n0 = blockIdx.y * 16;
+    const uint32_t n_slices = a.d_in / 16;
+    const float* xr[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)  // rows past n_rows repeat the last row (their results are dropped)
+        xr[rb] = a.x + (int64_t)min(m0 + 16 * rb + i, a.n_rows - 1) * a.x_row_stride + 4 * g;
+    const float* wr = a.w + (uint64_t)(n0 + i) * a.d_in + 4 * g;
+    f4 acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) acc[rb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s0 = p; s0 < n_slices; s0 += kQkvParts * kQkvBatch) {
+        float4 xv[kQkvBatch][RB], wv[kQkvBatch];
+#pragma unroll
+        for (int j = 0; j < kQkvBatch; j++) {
+            const uint32_t sl = s0 + kQkvParts * j;
+            if (sl < n_slices) {
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) xv[j][rb] = *reinterpret_cast<const float4*>(xr[rb] + 16 * sl);
+                wv[j] = *reinterpret_cast<const float4*>(wr + 16 * sl);
             }
         }
+#pragma unroll
+        for (int j = 0; j < kQkvBatch; j++) {
+            if (s0 + kQkvParts * j >= n_slices) break;
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][rb].x, wv[j].x, acc[rb], 0, 0, 0);
+                acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][rb].y, wv[j].y, acc[rb], 0, 0, 0);
+                acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][rb].z, wv[j].z, acc[rb], 0, 0, 0);
+                acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][rb].w, wv[j].w, acc[rb], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) red[p][rb][lane] = acc[rb];
+    __syncthreads();
+    if (p >= (uint32_t)RB) return;
+    // Wave rb finishes row block rb: the same tree as qkv_kernel.
+    const int rb = (int)p;
+    const f4 y = ((red[0][rb][lane] + red[1][rb][lane]) + (red[2][rb][lane] + red[3][rb][lane])) +
+                 ((red[4][rb][lane] + red[5][rb][lane]) + (red[6][rb][lane] + red[7][rb][lane]));
+    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
+    const uint32_t f = n0 + i;
+    const float b = a.bias ? a.bias[f] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t row = m0 + 16 * rb + 4 * g + e;
+        if (row >= a.n_rows) break;
+        qkv_store(a, entries, row, f, y[e] + b);
     }
 }
 
@@ -2278,6 +2381,16 @@ hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hip
 
 hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     if (a.n_rows == 0) return hipSuccess;
+    if (a.n_rows <= NI_QKV_SMALL_ROWS) {
+        constexpr int RB = NI_QKV_SMALL_RB;
+        const dim3 grid((a.n_rows + 16 * RB - 1) / (16 * RB), a.n_feat / 16);
+        return with_plan(a, ip, ib, [&](auto pa) {
+            constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+            hipExtLaunchKernelGGL(qkv_small_kernel<RB, INL>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0, a,
+                                  pa);
+            return hipGetLastError();
+        });
+    }
     // 16-feature tiles at every row count: the most workgroups to stream W
     // with (64-feature tiles measured slower from 64 to 512 rows).
     const dim3 grid((a.n_rows + kQkvTileRows - 1) / kQkvTileRows, a.n_feat / kQkvTileFeat);

@@ -60,10 +60,12 @@ def test_project_matches_f64(gpu, oracle_lib, shape, n):
 @pytest.mark.parametrize("d_in", [64, 400, 768])
 def test_project_batch_invariant(gpu, oracle_lib, shape, d_in):
     """Each output is accumulated in an order that does not depend on the
-    row count (row tiles are independent, d_in is walked in a fixed order),
-    so a row's outputs have the same bits in a batch of any size -- the
-    property the reference's matvec_batch keeps (batch.metal:60-66) and
-    speculative verification relies on."""
+    row count (row tiles are independent, d_in is summed in 8 fixed parts
+    and a fixed tree), so a row's outputs have the same bits in a batch of
+    any size -- the property the reference's matvec_batch keeps
+    (batch.metal:60-66) and speculative verification relies on.  Batches of
+    up to 16 rows run on the small-batch kernel and larger ones on the
+    LDS-staged kernel, so this also checks the two give the same bits."""
     rng = np.random.default_rng(80 + d_in)
     kv = make(shape)
     c = kv.opts.n_embd
@@ -73,13 +75,13 @@ def test_project_batch_invariant(gpu, oracle_lib, shape, d_in):
     big = kv.qkv_project(xd, wd, bd).cpu().numpy()
     want = oracle.matvec_f64(x, w, b)
     assert np.abs(big - want).max() < 2e-5
-    for n in (1, 17, 64):
+    for n in (1, 9, 16, 17, 64):
         small = kv.qkv_project(xd[:n].contiguous(), wd, bd).cpu().numpy()
         assert np.array_equal(small.view(np.uint32), big[:n].view(np.uint32)), f"n={n}"
     # the same rows at an offset inside the big batch, through a strided view
     small = kv.qkv_project(xd[100:130], wd, bd).cpu().numpy()
     assert np.array_equal(small.view(np.uint32), big[100:130].view(np.uint32))
-    say(f"{shape} d_in {d_in}: batches of 1/17/64/30 rows bit-identical to the 512-row batch")
+    say(f"{shape} d_in {d_in}: batches of 1/9/16/17/64/30 rows bit-identical to the 512-row batch")
 
 
 @pytest.mark.parametrize("bias", [True, False])
