@@ -70,7 +70,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", default="config3",
-                    help="config3 (default), config2, config4, config5, configNq8 (the same on the Q8 cache), "
+                    help="config3 (default), config1 (one sequence, prefill 64 + 64 decode steps, with the CPU "
+                         "path beside it), config2, config4, config5, configNq8 (the same on the Q8 cache), "
                          "prefill (16 x 512-row prompts, every row queried), prefillq8 (the same on the Q8 cache), or qkv[ROWS] (the QKV projection with "
                          "the append in its epilogue, ROWS rows per layer, default 64)")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = automatic)")
@@ -627,6 +628,148 @@ def run_prefill(args):
     return res
 
 
+CFG1 = dict(prompt=64, decode=64)  # GPT-2 shape, one sequence: prefill 64 positions, then 64 decode steps
+
+
+def _cfg1_bytes(c, L, P, T):
+    """Algorithmic bytes of config 1 (the step formula summed): the prefill
+    appends and queries P rows over contexts 1..P (each K/V byte once), then
+    decode step t appends and queries one row over P + t + 1 keys."""
+    from nanoinfer_amd.workloads import step_bytes
+
+    total = step_bytes([(0, P, P)], [P], L, c)["total"]
+    for t in range(T):
+        total += step_bytes([(0, 1, 1)], [P + t + 1], L, c)["total"]
+    return total
+
+
+def run_config1(args, reps=REPS):
+    """Benchmark configuration 1, the reference's CPU-runnable case: one GPT-2
+    sequence (12 layers x 12 heads x 64, f16 KV in 16-token pages) prefills
+    64 positions (every row queried, as the CPU forward attends every prompt
+    row) and decodes 64 steps, one K/V row appended and attended per layer
+    and step.  On the device: one ni_kv_step for the prefill, then
+    ni_kv_decode_steps for the 64 decode steps (Batch::decode_resident: all
+    enqueued at once), timed with events around both; `reps` runs, the
+    sequence truncated to 0 between them, median.  Beside it: the contiguous
+    f32 form of the same attention through ni_attention (the CPU engine's
+    Kernels::attention, stage 0/1 caches), and the reference's CPU path (the
+    oracle's restatement of kv16::attention with attend_f16_portable on a
+    thread pool) on the same inputs."""
+    import torch
+
+    import nanoinfer_amd as na
+    from nanoinfer_amd import workloads
+
+    sh = workloads.GPT2
+    L, H, D = sh["n_layer"], sh["n_head"], sh["head_dim"]
+    c, P, T = H * D, CFG1["prompt"], CFG1["decode"]
+    n = P + T
+    kv = na.PagedKv(na.BatchOpts(**sh, kv_blocks=n // 16, max_seqs=1, n_ctx=1024, max_rows=P))
+    s = kv.add_seq()
+    rng = np.random.default_rng(args.seed)
+    q, k, v = (rng.standard_normal((L, n, c), dtype=np.float32) for _ in range(3))
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, k, v))
+    # decode_steps layout [step][layer][row][C]: views of the same rows
+    qs, ks, vs = (x[:, P:, :].permute(1, 0, 2).unsqueeze(2) for x in (qd, kd, vd))
+    out_p = torch.empty((L, P, c), device="cuda")
+    out_d = torch.empty((T, L, 1, c), device="cuda")
+
+    def one():
+        kv.truncate(s, 0)
+        kv.step([(s, P, P)], qd[:, :P], kd[:, :P], vd[:, :P], out=out_p)
+        kv.decode_steps([s], qs, ks, vs, out=out_d)
+
+    one()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        one()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3)
+    t = float(np.median(times))
+    nbytes = _cfg1_bytes(c, L, P, T)
+    res = {"metric": METRIC, "value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": T + 1,
+           "warmup": 1, "ms_per_step": round(t / (T + 1) * 1e3, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "f32", "kv_dtype": "f16",
+           "data": "synthetic (seeded N(0,1) q/k/v resident in HBM)",
+           "config": {"workload": "config1: one GPT-2 sequence (12x12x64), f16 KV in 16-token pages, prefill 64 "
+                                  "positions (every row queried) then 64 decode steps", "n_layer": L, "n_head": H,
+                      "head_dim": D, "prompt": P, "decode_steps": T, "algorithmic_bytes": int(nbytes),
+                      "calls": "ni_kv_step (prefill) + ni_kv_decode_steps (64 steps, one enqueue)"},
+           "pct_of_peak": round(100 * nbytes / t / 1e9 / PEAK_GBS, 3),
+           "seq_tokens_per_s": round(n / t, 1), "seconds_per_run": round(t, 6),
+           "repetitions": {"reps": reps, "seconds": [round(x, 6) for x in times]},
+           "note": "latency-bound: 65 dependent steps of ~0.8 MB each; the figure is tokens/s, not bandwidth"}
+
+    # The contiguous f32 form (Kernels::attention over [pos][C] caches): per
+    # layer the prefill's 64 queries, then one query per decode step.
+    att_out = torch.empty((L, n, c), device="cuda")
+
+    def contiguous():
+        for l in range(L):
+            na.attention(qd[l, :P], kd[l], vd[l], P, 0, H, D, out=att_out[l, :P])
+        for tt in range(T):
+            for l in range(L):
+                na.attention(qd[l, P + tt:P + tt + 1], kd[l], vd[l], 1, P + tt, H, D, out=att_out[l, P + tt:P + tt + 1])
+
+    contiguous()
+    torch.cuda.synchronize()
+    ct = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        contiguous()
+        e1.record()
+        e1.synchronize()
+        ct.append(e0.elapsed_time(e1) / 1e3)
+    res["contiguous_attention"] = {
+        "seconds_per_run": round(float(np.median(ct)), 6), "seq_tokens_per_s": round(n / float(np.median(ct)), 1),
+        "calls": f"ni_attention per layer and step ({L * (T + 1)} calls), f32 K/V rows", "reps": reps}
+
+    if args.cpu_seconds > 0:
+        import oracle
+
+        threads = args.threads or available_parallelism()
+        pools = oracle.PagedPools(L, n // 16, c)
+        table = np.arange(n // 16, dtype=np.uint32).reshape(1, -1)
+        runner = oracle.CpuStep(threads)
+        outc = np.zeros((L, P, c), np.float32)
+        outd = np.zeros((T, L, 1, c), np.float32)
+        # decode step t's inputs: row P + t of each layer, as [L][1][C]
+        qkv_d = [tuple(np.ascontiguousarray(x[:, P + tt:P + tt + 1]) for x in (q, k, v)) for tt in range(T)]
+        qp, kp, vp = (np.ascontiguousarray(x[:, :P]) for x in (q, k, v))
+
+        def cpu_run():
+            rows = np.arange(P, dtype=np.uint32)
+            runner.run(pools, table, n // 16, np.zeros(P, np.uint32), rows, rows, qp, kp, vp, outc, H, D)
+            for tt in range(T):
+                runner.run(pools, table, n // 16, np.zeros(1, np.uint32), np.array([P + tt], np.uint32),
+                           np.zeros(1, np.uint32), *qkv_d[tt], outd[tt], H, D)
+
+        cts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            cpu_run()
+            cts.append(time.perf_counter() - t0)
+        tc = float(np.median(cts))
+        # the device result against the CPU path on the same inputs (a check, not timed)
+        dev = torch.cat([out_p.cpu(), out_d[:, :, 0].permute(1, 0, 2).cpu()], dim=1).numpy()
+        want = np.concatenate([outc, outd[:, :, 0].transpose(1, 0, 2)], axis=1)
+        cp = {"value": round(nbytes / tc / 1e9, 3), "unit": "GB/s", "seq_tokens_per_s": round(n / tc, 1),
+              "seconds_per_run": round(tc, 6), "cores": runner.threads, "kind": "port", "cpu_model": cpu_model(),
+              "repetitions": {"reps": reps, "seconds": [round(x, 6) for x in cts]},
+              "sample": "the whole of config 1 (prefill 64 + 64 decode steps, 12 layers): the oracle's C restatement "
+                        "of the reference x86 CPU path (narrow + attend_f16_portable + fastops::exp, (query, head) "
+                        "units on a thread pool), per step as the device runs it",
+              "max_abs_diff_vs_device": float(np.abs(dev - want).max())}
+        res["cpu_baseline"] = cp
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -644,6 +787,8 @@ def main():
     # The headline line is config 3; the others are secondary measurements.
     if args.workload == "config3":
         res = run_config3(args)
+    elif args.workload == "config1":
+        res = run_config1(args)
     elif args.workload.startswith("qkv"):
         res = run_qkv(args)
     elif args.workload in ("prefill", "prefillq8"):

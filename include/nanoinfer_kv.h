@@ -104,7 +104,7 @@ typedef struct ni_work {
 int ni_kv_create(const ni_kv_opts* opts, ni_kv** out);
 void ni_kv_destroy(ni_kv* kv);
 /* Text of the last failure on this handle; with kv == NULL, of the last
- * failed ni_kv_create on this thread. */
+ * failed ni_kv_create or ni_attention on this thread. */
 const char* ni_kv_last_error(const ni_kv* kv);
 /* Bytes of one page over all layers, K and V (BatchEngine::kv_block_bytes, batch.rs:107-109). */
 size_t ni_kv_page_bytes(const ni_kv* kv);
@@ -243,6 +243,21 @@ int ni_kv_sync(ni_kv* kv, ni_stream stream);
  * *v_pool the first V block.  f16: a block is [16][head_dim] f16.  Q8: a
  * block is [16][head_dim] int8 then 16 f32 scales. */
 int ni_kv_pools(const ni_kv* kv, void** k_pool, void** v_pool, size_t* bytes);
+
+/* Contiguous causal attention over f32 K/V rows, the CPU engine's op
+ * Kernels::attention(out, q: Rows, k: Rows, v: Rows, n_q, q_pos0, n_head,
+ * head_dim, scores) (crates/core/src/kernels/mod.rs:86-98; what it computes:
+ * reference::attention, kernels/reference.rs:109-142): query i at position
+ * q_pos0 + i attends to rows 0 .. q_pos0 + i;
+ * out[i][h*hd + d] = softmax(q_i,h . K_h^T / sqrt(hd)) V_h.  Row j of head h
+ * of K is at k + j*k_stride + h*head_dim (a Rows{data, stride}); q, v and
+ * out alike.  No scores buffer: the device keeps a running softmax.  Keys
+ * past q_pos0 + n_q - 1 are never read.  head_dim 64 or 128; pointers
+ * 16-byte aligned, strides multiples of 4 floats.  Enqueued on `stream`;
+ * failures are reported by ni_kv_last_error(NULL). */
+int ni_attention(float* out, int64_t out_stride, const float* q, int64_t q_stride, const float* k, int64_t k_stride,
+                 const float* v, int64_t v_stride, uint32_t n_q, uint32_t q_pos0, uint32_t n_head, uint32_t head_dim,
+                 ni_stream stream);
 
 /* quant.rs:25-54 on the device, elementwise (the conversion the append uses). */
 int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream);

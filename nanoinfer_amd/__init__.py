@@ -8,6 +8,6 @@ page allocator.  This package holds its sources (``csrc/``), its build recipe
 reference's ``Batch`` API (``batch.py``) and the synthetic workloads of the
 benchmark configurations (``workloads.py``).
 """
-from .batch import ALL_LAYERS, KV_BLOCK, BatchOpts, KvError, PagedKv, f32_to_f16_device
+from .batch import ALL_LAYERS, KV_BLOCK, BatchOpts, KvError, PagedKv, attention, f32_to_f16_device
 
-__all__ = ["ALL_LAYERS", "KV_BLOCK", "BatchOpts", "KvError", "PagedKv", "f32_to_f16_device"]
+__all__ = ["ALL_LAYERS", "KV_BLOCK", "BatchOpts", "KvError", "PagedKv", "attention", "f32_to_f16_device"]

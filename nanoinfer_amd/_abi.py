@@ -126,6 +126,8 @@ def _declare(L):
     L.ni_kv_sync.argtypes = [_vp, _vp]
     L.ni_kv_pools.restype = C.c_int
     L.ni_kv_pools.argtypes = [_vp, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(C.c_size_t)]
+    L.ni_attention.restype = C.c_int
+    L.ni_attention.argtypes = [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _u32, _u32, _u32, _u32, _vp]
     L.ni_f32_to_f16.restype = C.c_int
     L.ni_f32_to_f16.argtypes = [_vp, _vp, C.c_size_t, _vp]
     L.ni_kv_profile.restype = C.c_int

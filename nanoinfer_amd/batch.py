@@ -462,6 +462,48 @@ class PagedKv:
         return float(ms.value), int(n.value)
 
 
+def attention(q, k, v, n_q: int, q_pos0: int, n_head: int, head_dim: int, out=None, stream=None):
+    """``Kernels::attention`` (crates/core/src/kernels/mod.rs:86-98; the math
+    of ``reference::attention``, kernels/reference.rs:109-142) on the GPU
+    through ``ni_attention``: causal multi-head attention of the ``n_q``
+    queries at positions ``q_pos0 ..`` over f32 K/V rows ``0 .. q_pos0+n_q-1``.
+
+    q, k and v are 2-D float32 CUDA tensors whose rows are positions (the
+    reference's ``Rows``: any row stride, e.g. views of a fused ``[n][3C]``
+    buffer); q holds ``n_q`` rows, k and v at least ``q_pos0 + n_q``, each at
+    least ``C = n_head * head_dim`` wide.  Returns ``out`` ([n_q][C] float32,
+    allocated if not given).  No scores buffer is needed."""
+    import torch
+
+    c = n_head * head_dim
+    if n_q < 0 or q_pos0 < 0:
+        raise ValueError("n_q and q_pos0 must be >= 0")
+    args = (("q", q, n_q), ("k", k, q_pos0 + n_q), ("v", v, q_pos0 + n_q))
+    for name, t, rows in args:  # layout first, then the device
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.float32 or t.dim() != 2:
+            raise TypeError(f"{name} must be a 2-D float32 tensor")
+        if t.stride(1) != 1:
+            raise ValueError(f"{name} rows must be contiguous")
+        if t.shape[0] < rows or t.shape[1] < c:
+            raise ValueError(f"{name} is {tuple(t.shape)}; needs at least {rows} rows of {c}")
+    for name, t, _ in args:
+        if not t.is_cuda:
+            raise TypeError(f"{name} must be a CUDA tensor")
+        if t.device != q.device:
+            raise ValueError(f"{name} is on {t.device}, q on {q.device}")
+    if out is None:
+        out = torch.empty((n_q, c), dtype=torch.float32, device=q.device)
+    if (not isinstance(out, torch.Tensor) or out.dtype != torch.float32 or out.dim() != 2 or out.stride(1) != 1
+            or out.shape[0] < n_q or out.shape[1] < c or out.device != q.device):
+        raise ValueError(f"out must be a float32 [{n_q}][{c}] tensor on {q.device} with contiguous rows")
+    L = _abi.lib()
+    rc = L.ni_attention(out.data_ptr(), out.stride(0), q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0),
+                        v.data_ptr(), v.stride(0), n_q, q_pos0, n_head, head_dim, _stream_ptr(stream))
+    if rc != 0:
+        raise KvError(rc, (L.ni_kv_last_error(None) or b"").decode())
+    return out
+
+
 def f32_to_f16_device(x, out=None, stream=None):
     """quant.rs:25-54 on the GPU, elementwise, through the library's device
     conversion (the one the append uses).  Returns int16 bits."""

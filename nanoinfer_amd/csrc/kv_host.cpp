@@ -1384,6 +1384,50 @@ int ni_kv_sync(ni_kv* kv, ni_stream stream) {
     return NI_OK;
 }
 
+int ni_attention(float* out, int64_t out_stride, const float* q, int64_t q_stride, const float* k, int64_t k_stride,
+                 const float* v, int64_t v_stride, uint32_t n_q, uint32_t q_pos0, uint32_t n_head, uint32_t head_dim,
+                 ni_stream stream) {
+    auto fail = [](const std::string& msg) {
+        g_create_error = msg;
+        return NI_ERR_BAD_ARG;
+    };
+    if (n_q == 0) return NI_OK;
+    if (!attention_supported(head_dim)) return fail("head_dim " + std::to_string(head_dim) + " unsupported (64 or 128)");
+    if (n_head == 0) return fail("n_head must be > 0");
+    if ((uint64_t)n_q * n_head >= (1ull << 31)) return fail("n_q * n_head too large");
+    if ((uint64_t)q_pos0 + n_q > (1ull << 31)) return fail("q_pos0 + n_q too large");
+    const struct {
+        const char* name;
+        const void* p;
+        int64_t stride;
+    } args[] = {{"out", out, out_stride}, {"q", q, q_stride}, {"k", k, k_stride}, {"v", v, v_stride}};
+    for (const auto& x : args) {
+        if (!x.p) return fail(std::string(x.name) + " is NULL");
+        if (!aligned16(x.p) || x.stride < 0 || x.stride % 4 != 0)
+            return fail(std::string(x.name) + " must be 16-byte aligned with a non-negative row stride that is a multiple of 4");
+    }
+    RowsLaunch a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.q_stride = q_stride;
+    a.k_stride = k_stride;
+    a.v_stride = v_stride;
+    a.out_stride = out_stride;
+    a.n_q = n_q;
+    a.q_pos0 = q_pos0;
+    a.n_head = n_head;
+    a.head_dim = head_dim;
+    a.qscale = (float)(1.4426950408889634 / std::sqrt((double)head_dim));
+    const hipError_t e = launch_attention_rows(a, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        g_create_error = std::string("attention launch failed: ") + hipGetErrorString(e);
+        return NI_ERR_HIP;
+    }
+    return NI_OK;
+}
+
 int ni_f32_to_f16(const float* in, uint16_t* out, size_t n, ni_stream stream) {
     if (n == 0) return NI_OK;
     if (!in || !out) return NI_ERR_BAD_ARG;

@@ -654,6 +654,128 @@ __global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, 
     }
 }
 
+// --------------------------------------------- contiguous f32 attention
+
+// Kernels::attention (crates/core/src/kernels/mod.rs:86-98; the math of
+// reference::attention, reference.rs:109-142): query i at position q_pos0 + i
+// attends to f32 K/V rows 0 .. q_pos0 + i held contiguously with a row
+// stride.  One workgroup of W waves per (query, head); wave w takes key
+// blocks w, w + W, ... of U * 4 keys.  Lane l reads D/16 floats of key row
+// l / 16 of a load (16 lanes per row, 4 rows per load), keeps its own flash
+// state over the rows it sees, and the lanes' and waves' states are merged
+// once at the end, as in attn_split_kernel.  Rows past the query's last key
+// are never read (their loads repeat the last key and weigh 0).
+template <int D, int W>
+__global__ __launch_bounds__(64 * W) void attn_rows_kernel(const RowsLaunch a) {
+    constexpr int F = D / 16;  // floats per lane
+    constexpr int KPL = 4;     // key rows per load
+    constexpr int U = 4;       // loads per wave iteration
+    constexpr uint32_t KPI = KPL * U;
+    __shared__ float red[W][D + 2];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t i = blockIdx.x / a.n_head, h = blockIdx.x - i * a.n_head;
+    const uint32_t n_kv = a.q_pos0 + i + 1;
+    const int kl = lane >> 4, ds = lane & 15;
+    float q[F];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (int64_t)i * a.q_stride + h * D + F * ds);
+#pragma unroll
+        for (int c = 0; c < F / 4; c++) {
+            const float4 x = qp[c];
+            q[4 * c] = x.x * a.qscale;
+            q[4 * c + 1] = x.y * a.qscale;
+            q[4 * c + 2] = x.z * a.qscale;
+            q[4 * c + 3] = x.w * a.qscale;
+        }
+    }
+    const float* kb = a.k + h * D + F * ds;
+    const float* vb = a.v + h * D + F * ds;
+    float m = kMinScore, l = 0.f, o[F];
+#pragma unroll
+    for (int e = 0; e < F; e++) o[e] = 0.f;
+    for (uint32_t j0 = wave * KPI; j0 < n_kv; j0 += W * KPI) {
+        float4 kr[U][F / 4], vr[U][F / 4];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t j = min(j0 + u * KPL + kl, n_kv - 1);
+            const float4* kp = reinterpret_cast<const float4*>(kb + (int64_t)j * a.k_stride);
+            const float4* vp = reinterpret_cast<const float4*>(vb + (int64_t)j * a.v_stride);
+#pragma unroll
+            for (int c = 0; c < F / 4; c++) {
+                kr[u][c] = kp[c];
+                vr[u][c] = vp[c];
+            }
+        }
+        float s[U];
+        float mb = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < F / 4; c++) {
+                acc = fmaf(q[4 * c], kr[u][c].x, acc);
+                acc = fmaf(q[4 * c + 1], kr[u][c].y, acc);
+                acc = fmaf(q[4 * c + 2], kr[u][c].z, acc);
+                acc = fmaf(q[4 * c + 3], kr[u][c].w, acc);
+            }
+            s[u] = key_sum<16>(acc);
+            if (j0 + u * KPL + kl >= n_kv) s[u] = -INFINITY;
+            mb = fmaxf(mb, s[u]);
+        }
+        const float mn = fmaxf(m, mb);
+        const float alpha = fast_exp2(m - mn);
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int e = 0; e < F; e++) o[e] *= alpha;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float p = fast_exp2(s[u] - mn);
+            l += p;
+#pragma unroll
+            for (int c = 0; c < F / 4; c++) {
+                o[4 * c] = fmaf(p, vr[u][c].x, o[4 * c]);
+                o[4 * c + 1] = fmaf(p, vr[u][c].y, o[4 * c + 1]);
+                o[4 * c + 2] = fmaf(p, vr[u][c].z, o[4 * c + 2]);
+                o[4 * c + 3] = fmaf(p, vr[u][c].w, o[4 * c + 3]);
+            }
+        }
+    }
+    // The wave's 4 key-row groups (lanes ds, ds + 16, ds + 32, ds + 48).
+#pragma unroll
+    for (int off = 16; off < 64; off <<= 1) {
+        const float m2 = __shfl_xor(m, off);
+        const float l2 = __shfl_xor(l, off);
+        float o2[F];
+#pragma unroll
+        for (int e = 0; e < F; e++) o2[e] = __shfl_xor(o[e], off);
+        merge_state(m, l, o, m2, l2, o2);
+    }
+    if (kl == 0) {
+#pragma unroll
+        for (int e = 0; e < F; e++) red[wave][2 + F * ds + e] = o[e];
+        if (ds == 0) {
+            red[wave][0] = m;
+            red[wave][1] = l;
+        }
+    }
+    __syncthreads();
+    for (uint32_t d = threadIdx.x; d < (uint32_t)D; d += 64 * W) {
+        float M = red[0][0];
+#pragma unroll
+        for (int w = 1; w < W; w++) M = fmaxf(M, red[w][0]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            const float wt = fast_exp2(red[w][0] - M);
+            L += red[w][1] * wt;
+            O += red[w][2 + d] * wt;
+        }
+        a.out[(int64_t)i * a.out_stride + h * D + d] = O / L;
+    }
+}
+
 // ------------------------------------------------------- Q8 attention
 
 // Byte j of w as a signed integer, in f32.
@@ -2448,6 +2570,18 @@ hipError_t launch_stream(bool copy, bool span, const void* src, void* dst, size_
     if (copy && !span) hipLaunchKernelGGL((stream_kernel<true, false>), g, t, 0, s, in, out, n16);
     if (!copy && span) hipLaunchKernelGGL((stream_kernel<false, true>), g, t, 0, s, in, out, n16);
     if (!copy && !span) hipLaunchKernelGGL((stream_kernel<false, false>), g, t, 0, s, in, out, n16);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_rows(const RowsLaunch& a, hipStream_t s) {
+    const uint64_t blocks = (uint64_t)a.n_q * a.n_head;
+    if (blocks == 0) return hipSuccess;
+    constexpr int W = 4;
+    switch (a.head_dim) {
+        case 64: hipLaunchKernelGGL((attn_rows_kernel<64, W>), dim3((uint32_t)blocks), dim3(64 * W), 0, s, a); break;
+        case 128: hipLaunchKernelGGL((attn_rows_kernel<128, W>), dim3((uint32_t)blocks), dim3(64 * W), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -236,6 +236,20 @@ hipError_t launch_stream(bool copy, bool span, const void* src, void* dst, size_
                          hipStream_t s);
 hipError_t launch_qkv(const QkvLaunch& a, const void* inline_plan, uint32_t inline_bytes, hipStream_t s,
                       const LaunchTiming& t = {});
+
+// Contiguous f32 attention (Kernels::attention): query i at position
+// q_pos0 + i over K/V rows 0 .. q_pos0 + i, row j of head h at
+// k + j * k_stride + h * head_dim; out row i at out + i * out_stride.
+struct RowsLaunch {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* out;
+    int64_t q_stride, k_stride, v_stride, out_stride;
+    uint32_t n_q, q_pos0, n_head, head_dim;
+    float qscale;  // log2(e) / sqrt(head_dim)
+};
+hipError_t launch_attention_rows(const RowsLaunch& a, hipStream_t s);
 // Blocks a fused launch needs for its orphan rows (n_orphans set).
 uint32_t orphan_blocks(const AttnLaunch& a);
 bool attention_supported(uint32_t head_dim);

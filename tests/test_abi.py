@@ -47,3 +47,19 @@ def test_create_rejects_bad_options():
     with pytest.raises(na.KvError) as e:
         na.PagedKv(na.BatchOpts(kv_blocks=4, page_order=[0, 1, 1, 2], host_only=True))
     assert "permutation" in str(e.value)
+
+
+def test_attention_rejects_bad_arguments_before_any_launch():
+    """ni_attention's checks come before anything touches the device."""
+    L = _abi.lib()
+    buf = (C.c_float * 64)()
+    p = C.addressof(buf)
+    rc = L.ni_attention(p, 768, p, 768, p, 768, p, 768, 1, 0, 12, 96, None)
+    assert rc == _abi.NI_ERR_BAD_ARG and "head_dim 96" in L.ni_kv_last_error(None).decode()
+    rc = L.ni_attention(p + 4, 768, p, 768, p, 768, p, 768, 1, 0, 12, 64, None)
+    assert rc == _abi.NI_ERR_BAD_ARG and "out must be 16-byte aligned" in L.ni_kv_last_error(None).decode()
+    rc = L.ni_attention(p, 768, p, 770, p, 768, p, 768, 1, 0, 12, 64, None)
+    assert rc == _abi.NI_ERR_BAD_ARG and "q must be" in L.ni_kv_last_error(None).decode()
+    rc = L.ni_attention(p, 768, p, 768, None, 768, p, 768, 1, 0, 12, 64, None)
+    assert rc == _abi.NI_ERR_BAD_ARG and "k is NULL" in L.ni_kv_last_error(None).decode()
+    assert L.ni_attention(None, 0, None, 0, None, 0, None, 0, 0, 0, 12, 64, None) == _abi.NI_OK  # nothing to do

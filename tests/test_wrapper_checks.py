@@ -87,3 +87,16 @@ def test_projection_and_decode_steps(kv):
         h.decode_steps([s, s], f(3, L, 1, C), f(3, L, 1, C), f(3, L, 1, C))
     with pytest.raises(ValueError, match="steps"):
         h.decode_steps([s], f(3, L, 1, C), f(3, L, 1, C), f(3, L, 1, C), out=f(2, L, 1, C))
+
+
+def test_contiguous_attention_shapes():
+    """na.attention (Kernels::attention): k/v need q_pos0 + n_q rows of C."""
+    ok_q, ok_kv = f(2, C), f(5, C)
+    with pytest.raises(ValueError, match="needs"):
+        na.attention(ok_q, f(4, C), ok_kv, 2, 3, H, D)  # k one row short
+    with pytest.raises(ValueError, match="needs"):
+        na.attention(ok_q, ok_kv, f(5, C - 4), 2, 3, H, D)  # v too narrow
+    with pytest.raises(ValueError, match="needs"):
+        na.attention(f(1, C), ok_kv, ok_kv, 2, 3, H, D)  # q one row short
+    with pytest.raises(TypeError, match="CUDA"):
+        na.attention(ok_q, ok_kv, ok_kv, 2, 3, H, D)  # the right shape, but not on the GPU
