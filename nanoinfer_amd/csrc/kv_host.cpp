@@ -46,6 +46,15 @@ constexpr uint32_t kRingSlots = 4;
 #ifndef NI_STAGE_ALL_PLANS
 #define NI_STAGE_ALL_PLANS 0
 #endif
+// 1: ni_kv_step_begin uploads the step's plan to device memory once and each
+// layer's launch passes its address.  Off by default: config 3 one launch per
+// layer measured 3535 against 3722 GB/s with the plan inline in each launch's
+// arguments (the stream's wait for the upload costs more than the 16 KB of
+// arguments), and the host time per step did not change (the host runs ahead
+// until the device's queue is full either way).
+#ifndef NI_LAYER_PLAN_STAGED
+#define NI_LAYER_PLAN_STAGED 0
+#endif
 #ifndef NI_PLAN_COPY_STREAM
 #define NI_PLAN_COPY_STREAM 1
 #endif
@@ -526,8 +535,11 @@ Offsets layout(const Plan& P) {
     return o;
 }
 
-// Serialise plan P into `blob` and make it reachable from `s`.
-int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t s, Offsets* off, PlanRef* ref) {
+// Serialise plan P into `blob` and make it reachable from `s`.  stage:
+// always through a staging slot (never inline); with s == nullptr the upload
+// is left for the caller to wait on (the slot's `uploaded` event).
+int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t s, Offsets* off, PlanRef* ref,
+               bool stage = false) {
     *off = layout(P);
     blob.resize(off->total);
     if (!P.app.empty()) memcpy(blob.data() + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
@@ -551,7 +563,7 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
         ref->inl_bytes = (uint32_t)off->total;
         return NI_OK;
     }
-    if (!NI_STAGE_ALL_PLANS && off->total <= kInlinePlanBytes) {
+    if (!NI_STAGE_ALL_PLANS && !stage && off->total <= kInlinePlanBytes) {
         ref->inl = blob.data();
         ref->inl_bytes = (uint32_t)off->total;
         return NI_OK;
@@ -565,9 +577,12 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
     if (e != hipSuccess) return kv->hip_fail(e, "hipMemcpyAsync(plan)");
     e = hipEventRecord(sl->uploaded, kv->copy_stream);
     if (e != hipSuccess) return kv->hip_fail(e, "hipEventRecord(upload)");
-    e = hipStreamWaitEvent(s, sl->uploaded, 0);
-    if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
+    if (s) {
+        e = hipStreamWaitEvent(s, sl->uploaded, 0);
+        if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
+    }
 #else
+    if (!s) return kv->fail(NI_ERR_BAD_ARG, "a staged plan needs a stream to upload on");
     hipError_t e = hipMemcpyAsync(sl->dev, sl->host, off->total, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return kv->hip_fail(e, "hipMemcpyAsync(plan)");
 #endif
@@ -1188,6 +1203,19 @@ int ni_kv_step_begin(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t s
     st.placed = false;
     st.ref = PlanRef{};
     st.stream = nullptr;
+#if NI_LAYER_PLAN_STAGED && NI_PLAN_COPY_STREAM
+    // The step's plan goes to device memory once, here, on the handle's copy
+    // stream (the host is usually ahead of the device, so the upload is done
+    // before the first layer's launch waits for it); every layer's launch then
+    // carries only its arguments and the plan's address.
+    if (!kv->host_only && !(st.plan.items.empty() && st.plan.pitems.empty() && st.plan.app.empty())) {
+        if (int rc = place_plan(kv, st.plan, st.blob, nullptr, &st.off, &st.ref, true)) {
+            st.plan.clear();
+            return rc;
+        }
+        if (st.ref.slot) st.ref.slot->held = true;
+    }
+#endif
     st.open = true;
     return NI_OK;
 }
@@ -1215,10 +1243,15 @@ int ni_kv_step_layer(ni_kv* kv, int32_t layer, const float* q, const float* k, c
     if (st.placed && s != st.stream)
         return kv->fail(NI_ERR_BAD_ARG, "every layer of a step must run on the stream of its first layer");
     if (!st.placed) {
-        if (int rc = place_plan(kv, P, st.blob, s, &st.off, &st.ref)) return rc;
+        if (st.ref.slot) {  // uploaded by ni_kv_step_begin: this stream waits for it once
+            hipError_t e = hipStreamWaitEvent(s, st.ref.slot->uploaded, 0);
+            if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
+        } else {
+            if (int rc = place_plan(kv, P, st.blob, s, &st.off, &st.ref)) return rc;
+            if (st.ref.slot) st.ref.slot->held = true;
+        }
         st.placed = true;
         st.stream = s;
-        if (st.ref.slot) st.ref.slot->held = true;
     }
     return run_placed(kv, P, st.off, st.ref, (uint32_t)layer, 1, k, v, row_stride, 0, q, row_stride, 0, out,
                       out_row_stride, 0, s);
@@ -1230,7 +1263,13 @@ int ni_kv_step_end(ni_kv* kv) {
     if (!st.open) return kv->fail(NI_ERR_BAD_ARG, "no step is open (ni_kv_step_begin)");
     st.open = false;
     int rc = NI_OK;
-    if (st.placed) rc = release_plan(kv, st.ref, st.stream);
+    if (st.placed) {
+        rc = release_plan(kv, st.ref, st.stream);
+    } else if (st.ref.slot) {
+        // Uploaded by ni_kv_step_begin but never launched: the slot is free
+        // once its upload has finished.
+        rc = release_plan(kv, st.ref, kv->copy_stream);
+    }
     if (st.ref.slot) st.ref.slot->held = false;
     st.placed = false;
     st.ref = PlanRef{};
