@@ -80,6 +80,8 @@ def parse():
                     help="CPU baseline threads (0 = available parallelism, as the reference's thread pools)")
     ap.add_argument("--no-profile", action="store_true", help="skip the run timed by per-launch HIP events")
     ap.add_argument("--skip-per-layer", action="store_true", help="config 3: skip the per-layer launch run")
+    ap.add_argument("--skip-secondary", action="store_true",
+                    help="config 3: skip the secondary workloads measured beside the headline")
     ap.add_argument("--seed", type=int, default=7)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only plain 256 MiB device copies (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -479,6 +481,8 @@ def run_config3(args):
                         "ms_per_step": round(rl["seconds"] / rl["steps"] * 1e3, 5),
                         "host_us_per_step": round(rl["host_us_per_step"], 1),
                         "abi_calls_per_step": round(rl["launches"] / rl["steps"], 1), "repetitions": sp}
+    if not args.skip_secondary:
+        res["secondary"] = secondary_lines(args)
     if args.cpu_seconds > 0:
         threads = args.threads or available_parallelism()
         log(f"bench: CPU baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
@@ -499,6 +503,67 @@ def run_config3(args):
 
 
 # ------------------------------------------------- secondary configurations
+
+# Workloads measured beside the headline in the default run, each over a fixed
+# window (their own steps, not the caller's), so that the driver's run records
+# them too: name -> (steps, warmup, kernel(s) the roofline prices).
+SECONDARY_LINES = {
+    "config2": (200, 20, "attn_split_kernel (fused append)"),
+    "config4": (100, 10, "attn_split_kernel + attn_merge_kernel"),
+    "config5": (200, 20, "attn_mfma_kernel (fused append)"),
+    "config3q8": (200, 20, "attn_q8_kernel (fused append), Q8 cache"),
+    "prefill": (50, 5, "attn_prefill_kernel (after its append launch)"),
+    "qkv64": (200, 20, "qkv_kernel (append in the epilogue)"),
+}
+
+
+def secondary_lines(args, reps=3):
+    """Each of SECONDARY_LINES through the C++ driver: the median of `reps`
+    unprofiled runs (algorithmic GB/s, as the headline) and one run timing its
+    kernels with per-launch events.  config3q8 runs the headline's trace after
+    the same append-only ramp."""
+    import argparse as _ap
+
+    out = {}
+    for name, (steps, warmup, kernel) in SECONDARY_LINES.items():
+        a = _ap.Namespace(steps=steps, warmup=warmup, split=0, seed=args.seed)
+        ramp = RAMP_STEPS if name.startswith("config3") else 0
+        runs = [_drive(name, a, ramp=ramp) for _ in range(reps)]
+        gbs = sorted(r["bytes"] / r["seconds"] / 1e9 for r in runs)
+        med = gbs[len(gbs) // 2]
+        r = runs[[round(r["bytes"] / r["seconds"] / 1e9, 6) for r in runs].index(round(med, 6))]
+        line = {"value": round(med, 2), "unit": "GB/s", "pct_of_peak": round(100 * med / PEAK_GBS, 2),
+                "ms_per_step": round(r["seconds"] / r["steps"] * 1e3, 5),
+                "seq_tokens_per_s": round(r["seq_tokens"] / r["seconds"], 1),
+                "algorithmic_bytes_per_step": int(r["bytes"] / r["steps"]), "steps": steps, "warmup": warmup,
+                "ramp_steps": ramp, "reps_gbs": [round(g, 1) for g in gbs]}
+        if name.startswith("qkv"):
+            line["tflops"] = round(r["flops"] / r["seconds"] / 1e12, 2)
+            mask, ids = 1 << 3, (3,)
+        else:
+            mask, ids = (1 << 1) | (1 << 2), (1, 2)
+        rp = _drive(name, a, profile_mask=mask, ramp=ramp)
+        kms = sum(rp["kernel_ms"][i] for i in ids)
+        if name == "prefill":
+            # the attention launch alone: the step's bytes less its append's
+            c, L = 768, 12
+            app = drivers_prefill_append_bytes(c, L)
+            kb = rp["bytes"] / rp["steps"] - app
+            kgbs = kb * rp["steps"] / (kms / 1e3) / 1e9
+        else:
+            kgbs = rp["bytes"] / (kms / 1e3) / 1e9
+        line["kernel"] = {"name": kernel, "us_per_step": round(kms / rp["steps"] * 1e3, 3),
+                          "achieved_gbs": round(kgbs, 1), "frac": round(kgbs / PEAK_GBS, 4)}
+        out[name] = line
+    return out
+
+
+def drivers_prefill_append_bytes(c, L):
+    """Algorithmic bytes of the prefill step's separate append launch (f32
+    K/V read, f16 written), per step."""
+    from nanoinfer_amd import drivers
+
+    return drivers.PREFILL_SEQS * drivers.PREFILL_ROWS * L * (8 * c + 4 * c)
 
 SECONDARY = {
     "config2": ("config2: 16 seqs, ctx U[64,1024], 1024-page pool, seeded page permutation, append 1 + attention, "
