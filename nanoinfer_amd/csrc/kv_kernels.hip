@@ -21,7 +21,10 @@
 //   attn_q8_kernel     single rows on the int8 + scale (Q8) cache (kv8.metal)
 //   attn_merge_kernel  log-sum-exp merge of partitions (b_attn_merge, :403-424)
 //   qkv_kernel         the QKV projection with the append in its epilogue
-//                      (matvec_batch<..., BEPI_QKV>, batch.metal:94-165)
+//                      (matvec_batch<..., BEPI_QKV>, batch.metal:94-165); with
+//                      qkv_small_kernel (up to 16 rows) and qkv_mid_kernel
+//                      (17..64 rows), the same arithmetic at every row count
+//   attn_rows_kernel   contiguous f32 attention (Kernels::attention)
 //
 // Decode is HBM-bound streaming of f16 (or int8) K/V.  Arithmetic is f32 (the
 // matrix-core kernels carry f32 operands as f16 hi + lo parts); softmax runs
@@ -1836,6 +1839,115 @@ __device__ __forceinline__ void wait_tiles(uint32_t ahead) {
         __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
+// QKV projection of mid-size batches (NI_QKV_SMALL_ROWS < n <= NI_QKV_MID_ROWS):
+// a workgroup of 8 waves owns a 16-row x 16-feature tile, as
+// qkv_small_kernel with one row block, but x and W reach the matrix cores
+// through LDS.  Loading operands straight into the matrix-core layout reads
+// 16 rows x 64 bytes per instruction, half of each 128-byte line; x is read
+// by every feature tile, and those half-line reads cost ~4 us per layer more
+// than whole-line ones at 64 rows (measured).  Here every thread issues all
+// its loads of the tile at once, whole lines (wave p: rows 2p and 2p+1 of x
+// and of W, 512 contiguous bytes each per chunk of 128 values of d_in), up to
+// kQkvMidChunks chunks (d_in <= 1024) in registers; then chunk by chunk the tile goes
+// through a double-buffered LDS chunk (one barrier per chunk) into the
+// matrix-core layout.  Row r's 16-byte piece q sits in slot q ^ (r & 15) of
+// its 512-byte LDS row, so the 16 lanes reading piece q of 16 rows hit
+// distinct banks.  Wave p multiplies slice p of every chunk -- part p, in
+// increasing slice order: the same products in the same order as the other
+// two kernels -- and the parts meet in LDS, so the bits are the same at
+// every row count.  (A 3-stage DMA ring of chunks instead, two in flight:
+// 103 us per 12 layers at 64 rows, latency-bound.)
+#ifndef NI_QKV_MID_ROWS
+#define NI_QKV_MID_ROWS 64
+#endif
+constexpr int kQkvMidChunks = 8;  // chunks of d_in held in registers: d_in up to 1024 on this kernel
+
+template <int INL>
+__global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int KC = kQkvChunk;       // d_in values per chunk (8 slices of 16)
+    constexpr uint32_t RB = KC * 4;     // bytes of one row's chunk (512)
+    constexpr uint32_t CB = 16 * RB;    // bytes of 16 rows' chunk (8 KB)
+    constexpr int NC = kQkvMidChunks;
+    static_assert(KC == 128 && kQkvParts == 8, "two rows of 32 pieces per wave and chunk, 8 waves");
+    __shared__ __attribute__((aligned(16))) uint8_t buf[2][2 * CB];  // [x rows | W rows], double-buffered
+    const int lane = threadIdx.x & 63;
+    const uint32_t p = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = lane & 15, g = lane >> 4;
+    // Workgroups go to the 8 XCDs in turn (w % 8), each XCD with its own L2.
+    // The nx row tiles of feature tile f are dealt to one XCD back to back,
+    // so W's tile leaves HBM once and the other row tiles read it from that
+    // L2 (the row tiles of a feature tile on different XCDs made half of all
+    // L2 requests misses at 64 rows).  Needs the feature-tile count to be a
+    // multiple of 8; otherwise the plain order.
+    const uint32_t nx = gridDim.x / (a.n_feat / 16), w = blockIdx.x;
+    uint32_t rt = w % nx, ft = w / nx;
+    if ((a.n_feat / 16) % 8 == 0) {
+        const uint32_t k = w / 8;
+        rt = k % nx;
+        ft = 8 * (k / nx) + w % 8;
+    }
+    const uint32_t m0 = rt * 16, n0 = ft * 16;
+    const uint32_t n_slices = a.d_in / 16;
+    const uint32_t n_chunks = (a.d_in + KC - 1) / KC;
+    // This thread's share of every chunk: piece `pc` of row `dr` (x and W).
+    // Rows past n_rows repeat the last row; pieces past d_in (the last,
+    // partial chunk) load the row's first piece (their slices are skipped).
+    const uint32_t dr = 2 * p + (lane >> 5), pc = lane & 31;
+    const float* xsrc = a.x + (int64_t)min(m0 + dr, a.n_rows - 1) * a.x_row_stride;
+    const float* wsrc = a.w + (uint64_t)(n0 + dr) * a.d_in;
+    const uint32_t wo = dr * RB + 16u * (pc ^ (dr & 15));
+    // Lane (i, g) reads piece 4p + g of x row i and of W row i.
+    const uint32_t rd = (uint32_t)i * RB + 16u * ((4u * p + (uint32_t)g) ^ (uint32_t)i);
+    // Every load at once (d_in <= NC chunks; chunks past the end repeat the
+    // last one, unused): branches or a loop here put xr/wr on the stack.
+    f4 xr[NC], wr[NC];  // native vectors: HIP's float4 struct copied into LDS kept them on the stack
+#pragma clang loop unroll(full)
+    for (int j = 0; j < NC; j++) {
+        uint32_t col = min((uint32_t)j, n_chunks - 1) * KC + 4 * pc;
+        col = col < a.d_in ? col : 0;
+        xr[j] = *reinterpret_cast<const f4*>(xsrc + col);
+        wr[j] = *reinterpret_cast<const f4*>(wsrc + col);
+    }
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma clang loop unroll(full)
+    for (int j = 0; j < NC; j++) {
+        if ((uint32_t)j < n_chunks) {  // uniform
+            uint8_t* b = buf[j & 1];
+            // buf[j & 1] was last read for chunk j - 2, before every wave
+            // passed the barrier of chunk j - 1.
+            *reinterpret_cast<f4*>(b + wo) = xr[j];
+            *reinterpret_cast<f4*>(b + CB + wo) = wr[j];
+            __syncthreads();
+            if (8 * (uint32_t)j + p < n_slices) {
+                const float4 xv = *reinterpret_cast<const float4*>(b + rd);
+                const float4 wv = *reinterpret_cast<const float4*>(b + CB + rd);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, wv.x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, wv.y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, wv.z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, wv.w, acc, 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();  // every wave is done with the buffers: reuse them for the parts
+    f4* red = reinterpret_cast<f4*>(&buf[0][0]);
+    red[p * 64 + lane] = acc;
+    __syncthreads();
+    if (p != 0) return;
+    // The same tree as qkv_kernel and qkv_small_kernel.
+    const f4 y = ((red[0 * 64 + lane] + red[1 * 64 + lane]) + (red[2 * 64 + lane] + red[3 * 64 + lane])) +
+                 ((red[4 * 64 + lane] + red[5 * 64 + lane]) + (red[6 * 64 + lane] + red[7 * 64 + lane]));
+    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
+    const uint32_t f = n0 + i;
+    const float b = a.bias ? a.bias[f] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t row = m0 + 4 * g + e;
+        if (row >= a.n_rows) break;
+        qkv_store(a, entries, row, f, y[e] + b);
+    }
+}
+
 template <int D, int PT, int INL, bool Q8>
 __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_prefill_kernel(const AttnLaunch a,
                                                                                              const PlanArg<INL> pa) {
@@ -2510,6 +2622,14 @@ hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream
             constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
             hipExtLaunchKernelGGL(qkv_small_kernel<RB, INL>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0, a,
                                   pa);
+            return hipGetLastError();
+        });
+    }
+    if (a.n_rows <= NI_QKV_MID_ROWS && a.d_in <= (uint32_t)(kQkvMidChunks * kQkvChunk)) {
+        const dim3 grid((a.n_rows + 15) / 16 * (a.n_feat / 16));  // (row tile, feature tile), dealt by XCD
+        return with_plan(a, ip, ib, [&](auto pa) {
+            constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+            hipExtLaunchKernelGGL(qkv_mid_kernel<INL>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0, a, pa);
             return hipGetLastError();
         });
     }
