@@ -444,8 +444,18 @@ __device__ __forceinline__ void load_pages(PageRegs<PB, LPP>& r, const uint32_t*
 // loads.  Each lane keeps its own flash state (m, l, o[8]) per query over the
 // keys its key-row group sees; the groups are merged once at the end (wave
 // shuffles, then LDS across waves).
+// Waves per SIMD the wide (8-wave, one-layer) workgroups' registers must allow:
+// with one page per iteration (NI_WIDE_PAGES) the fused kernel fits 80 VGPRs
+// without spilling, so a layer's 768 workgroups of config 3 (64 sequences x
+// 12 heads) are all resident at once instead of 512 and then a tail of 256:
+// one launch per layer 3711 -> 4183 GB/s (two pages per iteration, 119
+// VGPRs, 4 waves per SIMD, before).
+#ifndef NI_WIDE_MIN_WAVES
+#define NI_WIDE_MIN_WAVES 6
+#endif
 template <int D, int NQ, int W, int PB, bool FUSED, int INL>
-__global__ __launch_bounds__(64 * W) void attn_split_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+__global__ __launch_bounds__(64 * W, W == 8 ? NI_WIDE_MIN_WAVES : 1) void attn_split_kernel(const AttnLaunch a,
+                                                                                            const PlanArg<INL> pa) {
     constexpr int LPK = D / 8;
     constexpr int KPL = 64 / LPK;
     constexpr int LPP = kPage / KPL;
@@ -2425,6 +2435,13 @@ hipError_t with_plan(const L& a, const void* inline_plan, uint32_t inline_bytes,
     return launch(PlanArg<0>{});
 }
 
+// Pages per wave iteration of the wide (one-layer) single-row launches (see
+// NI_WIDE_MIN_WAVES; separate append + attention calls per layer, whose
+// kernel is not fused, 3501 -> 3780 GB/s).
+#ifndef NI_WIDE_PAGES
+#define NI_WIDE_PAGES 1
+#endif
+
 template <int D, int NQ>
 hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     // Several queries per item hold NQ times the softmax state: one page per
@@ -2438,11 +2455,12 @@ hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
     if constexpr (D == 64 && NQ == 1) {
         if (a.wide) {
             constexpr int WW = kWideWaves;
+            constexpr int WPB = NI_WIDE_PAGES;
             return with_plan(a, ip, ib, [&](auto pa) {
                 constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
                 if (a.napp_total || a.n_orphan_blocks)
-                    return go(attn_split_kernel<D, NQ, WW, PB, true, INL>, blocks, 64 * WW, s, t, a, pa);
-                return go(attn_split_kernel<D, NQ, WW, PB, false, INL>, blocks, 64 * WW, s, t, a, pa);
+                    return go(attn_split_kernel<D, NQ, WW, WPB, true, INL>, blocks, 64 * WW, s, t, a, pa);
+                return go(attn_split_kernel<D, NQ, WW, WPB, false, INL>, blocks, 64 * WW, s, t, a, pa);
             });
         }
     }
