@@ -72,8 +72,9 @@ def parse():
     ap.add_argument("--workload", default="config3",
                     help="config3 (default), config1 (one sequence, prefill 64 + 64 decode steps, with the CPU "
                          "path beside it), config2, config4, config5, configNq8 (the same on the Q8 cache), "
-                         "prefill (16 x 512-row prompts, every row queried), prefillq8 (the same on the Q8 cache), or qkv[ROWS] (the QKV projection with "
-                         "the append in its epilogue, ROWS rows per layer, default 64)")
+                         "prefill (16 x 512-row prompts, every row queried), prefillq8 (the same on the Q8 cache), or qkv[ROWS][f16|q8|q4] (the QKV "
+                         "projection with the append in its epilogue, ROWS rows per layer, default 64, f32 weights or the reference's "
+                         "f16 / q8_0 / q4_0 formats)")
     ap.add_argument("--split", type=int, default=0, help="split_tokens (0 = automatic)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (0 = skip)")
     ap.add_argument("--threads", type=int, default=0,
@@ -617,12 +618,19 @@ def run_qkv(args):
     x, q out and the f16 K/V stores."""
     from nanoinfer_amd import drivers
 
-    rows = int(args.workload[3:] or 64)
+    spec, wname = args.workload[3:], "f32"
+    for suffix, nm in (("f16", "f16"), ("q8", "q8_0"), ("q4", "q4_0")):
+        if spec.endswith(suffix):
+            spec, wname = spec[: -len(suffix)], nm
+    rows = int(spec or 64)
     r = _drive(args.workload, args)
-    ru = _drive(args.workload, args, launch=drivers.NI_DRIVE_PER_LAYER)
-    res = _line(args, r, f"qkv: GPT-2 QKV projection, {rows} rows x 12 layers (768 -> 2304, f32 weights) with K/V "
-                         f"appended as f16 in the epilogue", {"rows": rows, "d_in": 768, "n_feat": 2304},
-                "synthetic (seeded normal x, W ~ N(0, 1/768), bias, resident in HBM)")
+    # the unfused comparison: f32 projection + append (f32 weights)
+    ru = _drive(f"qkv{rows}", args, launch=drivers.NI_DRIVE_PER_LAYER)
+    res = _line(args, r, f"qkv: GPT-2 QKV projection, {rows} rows x 12 layers (768 -> 2304, {wname} weights) with "
+                         f"K/V appended as f16 in the epilogue",
+                {"rows": rows, "d_in": 768, "n_feat": 2304, "weights": wname},
+                "synthetic (seeded normal x, W ~ N(0, 1/768) quantised as the reference uploads it, bias, "
+                "resident in HBM)")
     res["metric"] = "fused QKV projection + KV append, algorithmic GB/s, 1 MI355X"
     res["tflops"] = round(r["flops"] / r["seconds"] / 1e12, 2)
     gu = ru["bytes"] / ru["seconds"] / 1e9

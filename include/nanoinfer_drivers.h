@@ -138,6 +138,8 @@ typedef struct ni_drive_opts {
     uint32_t profile_mask;  /* ni_kv_profile mask over the timed iterations; 0 = none */
     uint32_t qkv_rows;      /* NI_DRIVE_QKV: rows per projection */
     uint32_t fixed_rows;    /* NI_DRIVE_FIXED: rows appended and queried per sequence and iteration (0 = 1) */
+    uint32_t qkv_wformat;   /* NI_DRIVE_QKV: weight format (NI_W_*), quantised on the host as the reference's
+                               upload does (crates/metal/src/weights.rs:12-72) */
 } ni_drive_opts;
 
 typedef struct ni_drive_result {

@@ -152,6 +152,24 @@ int ni_kv_qkv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, c
 int ni_kv_qkv_project(ni_kv* kv, const float* x, int64_t x_row_stride, uint32_t n, uint32_t d_in, const float* w,
                       const float* bias, float* out, int64_t out_row_stride, ni_stream stream);
 
+/* The same two calls with W in one of the reference's weight formats (DType,
+ * crates/metal/src/lib.rs:36-43, laid out as crates/metal/src/weights.rs:12-86
+ * stores the row-major [3C][d_in] matrix; the BEPI_QKV matvec and GEMM
+ * paths load them through BF32/BF16/BQ8/BQ4, batch.metal:45-90).  Each
+ * weight is dequantised exactly into f32 (f16 widened, q * d, (q - 8) * d),
+ * so the result has the bits of the f32 call on the dequantised matrix.
+ * Block formats need d_in a multiple of 32; w 16-byte aligned. */
+#define NI_W_F32 0u  /* [3C][d_in] f32 */
+#define NI_W_F16 1u  /* [3C][d_in] f16 */
+#define NI_W_Q8_0 2u /* [3C*d_in] int8, then [3C*d_in/32] f16 scales (quantize_q8_0) */
+#define NI_W_Q4_0 3u /* [3C*d_in/2] bytes (byte i of a 32-block: element i in the low nibble, i+16 in the high),
+                        then [3C*d_in/32] f16 scales (quantize_q4_0) */
+int ni_kv_qkv_append_w(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* x,
+                       int64_t x_row_stride, uint32_t d_in, const void* w, uint32_t w_format, const float* bias,
+                       float* q_out, int64_t q_row_stride, ni_stream stream);
+int ni_kv_qkv_project_w(ni_kv* kv, const float* x, int64_t x_row_stride, uint32_t n, uint32_t d_in, const void* w,
+                        uint32_t w_format, const float* bias, float* out, int64_t out_row_stride, ni_stream stream);
+
 /* Block-table gather: f16 bits of K and V at (seq, pos) for each row, in the
  * reference's row layout [C] = [head][head_dim] (the reads of b_attn_split,
  * batch.metal:377,392, through kv_slot, :24-26).  Strides in halves. */

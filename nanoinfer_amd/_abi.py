@@ -34,6 +34,8 @@ NI_ERR_NO_DEVICE = 11
 
 NI_K_APPEND, NI_K_ATTN, NI_K_MERGE, NI_K_QKV, NI_K_COUNT = 0, 1, 2, 3, 4
 
+NI_W_F32, NI_W_F16, NI_W_Q8_0, NI_W_Q4_0 = 0, 1, 2, 3
+
 
 class ni_kv_opts(C.Structure):
     _fields_ = [
@@ -100,6 +102,11 @@ def _declare(L):
     L.ni_kv_qkv_append.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _i64, _u32, _vp, _vp, _vp, _i64, _vp]
     L.ni_kv_qkv_project.restype = C.c_int
     L.ni_kv_qkv_project.argtypes = [_vp, _vp, _i64, _u32, _u32, _vp, _vp, _vp, _i64, _vp]
+    L.ni_kv_qkv_append_w.restype = C.c_int
+    L.ni_kv_qkv_append_w.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _i64, _u32, _vp, _u32, _vp, _vp, _i64,
+                                     _vp]
+    L.ni_kv_qkv_project_w.restype = C.c_int
+    L.ni_kv_qkv_project_w.argtypes = [_vp, _vp, _i64, _u32, _u32, _vp, _u32, _vp, _vp, _i64, _vp]
     L.ni_kv_gather_q8.restype = C.c_int
     L.ni_kv_gather_q8.argtypes = [_vp, C.c_int32, C.POINTER(ni_row), _u32, _vp, _vp, _vp, _vp, _vp]
     L.ni_kv_gather.restype = C.c_int

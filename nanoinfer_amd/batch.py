@@ -117,13 +117,34 @@ def _on_device(device, **tensors):
             raise ValueError(f"{name} is on cuda:{t.device.index}, the cache on cuda:{device}")
 
 
-def _weights(w, bias, c, d_in):
-    """Check the layout of W [3C, d_in] (contiguous float32) and bias."""
+# Weight formats of the QKV projection (the reference's DType, crates/metal/src/lib.rs:36-43).
+W_FORMATS = {"f32": _abi.NI_W_F32, "f16": _abi.NI_W_F16, "q8_0": _abi.NI_W_Q8_0, "q4_0": _abi.NI_W_Q4_0}
+
+
+def w_bytes(fmt: str, n: int) -> int:
+    """Bytes of n weights in format fmt (weights.rs:12-86: quants, then one
+    f16 scale per block of 32)."""
+    return {"f32": 4 * n, "f16": 2 * n, "q8_0": n + n // 16, "q4_0": n // 2 + n // 16}[fmt]
+
+
+def _weights(w, bias, c, d_in, fmt="f32"):
+    """Check the layout of W [3C, d_in] in format fmt (f32: a contiguous
+    float32 [3C, d_in] tensor; otherwise a contiguous uint8 tensor of the
+    format's bytes) and bias."""
     import torch
 
-    if not isinstance(w, torch.Tensor) or w.dtype != torch.float32 or not w.is_contiguous() \
-            or tuple(w.shape) != (3 * c, d_in):
-        raise ValueError(f"w must be a contiguous float32 CUDA tensor [{3 * c}, {d_in}]")
+    if fmt not in W_FORMATS:
+        raise ValueError(f"unknown weight format {fmt!r} (one of {sorted(W_FORMATS)})")
+    if fmt == "f32":
+        if not isinstance(w, torch.Tensor) or w.dtype != torch.float32 or not w.is_contiguous() \
+                or tuple(w.shape) != (3 * c, d_in):
+            raise ValueError(f"w must be a contiguous float32 CUDA tensor [{3 * c}, {d_in}]")
+    else:
+        if fmt != "f16" and d_in % 32:
+            raise ValueError(f"d_in {d_in} must be a multiple of 32 for {fmt}")
+        need = w_bytes(fmt, 3 * c * d_in)
+        if not isinstance(w, torch.Tensor) or not w.is_contiguous() or w.numel() * w.element_size() != need:
+            raise ValueError(f"w must be a contiguous tensor of the {need} bytes of a [{3 * c}, {d_in}] {fmt} matrix")
     if bias is not None and (not isinstance(bias, torch.Tensor) or bias.dtype != torch.float32
                              or not bias.is_contiguous() or bias.numel() != 3 * c):
         raise ValueError(f"bias must be a contiguous float32 CUDA tensor of {3 * c} values")
@@ -265,45 +286,47 @@ class PagedKv:
         self._check(self._L.ni_kv_append(self._h, layer, rp, n, k.data_ptr(), v.data_ptr(), rs, ls,
                                          _stream_ptr(stream)))
 
-    def qkv_append(self, rows, x, w, bias=None, q_out=None, layer: int = 0, stream=None):
+    def qkv_append(self, rows, x, w, bias=None, q_out=None, layer: int = 0, stream=None, w_format: str = "f32"):
         """The QKV projection with the append in its epilogue (BEPI_QKV):
         x [n, d_in], w [3C, d_in], bias [3C] float32 CUDA tensors; k/v go to
-        the rows' page slots of `layer` as f16, q is returned [n, C]."""
+        the rows' page slots of `layer` as f16, q is returned [n, C].
+        w_format "f16", "q8_0" or "q4_0": w holds the matrix in the
+        reference's format (weights.rs:12-86), any dtype, contiguous."""
         import torch
 
         arr, rp, n = _rows(rows)
         if not isinstance(x, torch.Tensor) or x.dim() != 2:
             raise ValueError("x must be a [rows, d_in] tensor")
         xs, _ = self._f32(x, "x", False, n, c=x.shape[1])
-        _weights(w, bias, self.opts.n_embd, x.shape[1])
+        _weights(w, bias, self.opts.n_embd, x.shape[1], w_format)
         if q_out is not None:
             self._f32(q_out, "q_out", False, n)
         self._on_device(x=x, w=w, bias=bias, q_out=q_out)
         if q_out is None:
             q_out = torch.zeros((n, self.opts.n_embd), dtype=torch.float32, device=x.device)
         qs, _ = self._f32(q_out, "q_out", False, n)
-        self._check(self._L.ni_kv_qkv_append(self._h, layer, rp, n, x.data_ptr(), xs, x.shape[1], w.data_ptr(),
-                                             None if bias is None else bias.data_ptr(), q_out.data_ptr(), qs,
-                                             _stream_ptr(stream)))
+        self._check(self._L.ni_kv_qkv_append_w(self._h, layer, rp, n, x.data_ptr(), xs, x.shape[1], w.data_ptr(),
+                                               W_FORMATS[w_format], None if bias is None else bias.data_ptr(),
+                                               q_out.data_ptr(), qs, _stream_ptr(stream)))
         return q_out
 
-    def qkv_project(self, x, w, bias=None, out=None, stream=None):
+    def qkv_project(self, x, w, bias=None, out=None, stream=None, w_format: str = "f32"):
         """The same projection, every output column to out [n, 3C] (f32)."""
         import torch
 
         if not isinstance(x, torch.Tensor) or x.dim() != 2:
             raise ValueError("x must be a [rows, d_in] tensor")
         xs, _ = self._f32(x, "x", False, x.shape[0], c=x.shape[1])
-        _weights(w, bias, self.opts.n_embd, x.shape[1])
+        _weights(w, bias, self.opts.n_embd, x.shape[1], w_format)
         if out is not None:
             self._f32(out, "out", False, x.shape[0], c=3 * self.opts.n_embd)
         self._on_device(x=x, w=w, bias=bias, out=out)
         if out is None:
             out = torch.zeros((x.shape[0], 3 * self.opts.n_embd), dtype=torch.float32, device=x.device)
         os_, _ = self._f32(out, "out", False, x.shape[0], c=3 * self.opts.n_embd)
-        self._check(self._L.ni_kv_qkv_project(self._h, x.data_ptr(), xs, x.shape[0], x.shape[1], w.data_ptr(),
-                                              None if bias is None else bias.data_ptr(), out.data_ptr(), os_,
-                                              _stream_ptr(stream)))
+        self._check(self._L.ni_kv_qkv_project_w(self._h, x.data_ptr(), xs, x.shape[0], x.shape[1], w.data_ptr(),
+                                                W_FORMATS[w_format], None if bias is None else bias.data_ptr(),
+                                                out.data_ptr(), os_, _stream_ptr(stream)))
         return out
 
     def gather(self, rows, layer: int = ALL_LAYERS, stream=None):

@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 #include <deque>
 #include <string>
 #include <vector>
@@ -614,6 +615,66 @@ int run_fixed(Runner& r, ni_drive_result* res) {
     return rc;
 }
 
+// The reference's weight upload in the formats it serves with
+// (crates/metal/src/weights.rs:12-27 quantize_q8_0, :54-72 quantize_q4_0,
+// :115-118 f16), over one row-major matrix: quants, then one f16 scale per
+// block of 32.  The f16 conversion is the library's (round to nearest even).
+uint16_t to_f16(float x) {
+    const _Float16 h = static_cast<_Float16>(x);
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+std::vector<uint8_t> upload_weights(const std::vector<float>& w, uint32_t fmt) {
+    const size_t n = w.size();
+    std::vector<uint8_t> out;
+    if (fmt == NI_W_F32) {
+        out.resize(4 * n);
+        std::memcpy(out.data(), w.data(), 4 * n);
+        return out;
+    }
+    if (fmt == NI_W_F16) {
+        out.resize(2 * n);
+        for (size_t i = 0; i < n; i++) {
+            const uint16_t h = to_f16(w[i]);
+            std::memcpy(&out[2 * i], &h, 2);
+        }
+        return out;
+    }
+    const bool q8 = fmt == NI_W_Q8_0;
+    const size_t qb = q8 ? n : n / 2;
+    out.assign(qb + n / 16, 0);
+    for (size_t b = 0; b < n / 32; b++) {
+        const float* blk = &w[32 * b];
+        float d;
+        if (q8) {
+            float amax = 0.f;
+            for (int i = 0; i < 32; i++) amax = std::max(amax, std::fabs(blk[i]));
+            d = amax / 127.f;
+            const float id = d > 0.f ? 1.f / d : 0.f;
+            for (int i = 0; i < 32; i++) {
+                const float r = std::round(blk[i] * id);
+                out[32 * b + i] = (uint8_t)(int8_t)std::max(-128.f, std::min(127.f, r));
+            }
+        } else {
+            float mx = 0.f;
+            for (int i = 0; i < 32; i++)
+                if (std::fabs(blk[i]) > std::fabs(mx)) mx = blk[i];
+            d = mx / -8.f;
+            const float id = d != 0.f ? 1.f / d : 0.f;
+            auto q = [&](float v) { return (uint8_t)std::max(0, std::min(15, (int)(v * id + 8.5f))); };
+            for (int i = 0; i < 16; i++) out[16 * b + i] = (uint8_t)(q(blk[i]) | (q(blk[i + 16]) << 4));
+        }
+        const uint16_t h = to_f16(d);
+        std::memcpy(&out[qb + 2 * b], &h, 2);
+    }
+    return out;
+}
+
+double weight_bytes(uint32_t fmt, double n) {
+    return fmt == NI_W_F32 ? 4 * n : fmt == NI_W_F16 ? 2 * n : fmt == NI_W_Q8_0 ? n + n / 16 : n / 2 + n / 16;
+}
+
 int run_qkv(Runner& r, ni_drive_result* res) {
     const uint32_t n = r.o.qkv_rows, C = r.C, L = r.L, d_in = C, F = 3 * C;
     if (n == 0 || n > r.o.kv.max_rows) return drive_fail(NI_ERR_BAD_ARG, "qkv_rows must be 1..max_rows");
@@ -627,16 +688,22 @@ int run_qkv(Runner& r, ni_drive_result* res) {
     }
     std::vector<ni_row> rows(n);
     for (uint32_t i = 0; i < n; i++) rows[i] = {seqs[i % S], i / S};
-    // W [L][3C][d_in] ~ N(0, 1/d_in), bias [L][3C] ~ N(0, 0.01).
-    float* w = nullptr;
-    float* bias = nullptr;
+    const uint32_t fmt = r.o.qkv_wformat;
+    if (fmt > NI_W_Q4_0) return drive_fail(NI_ERR_BAD_ARG, "qkv_wformat must be one of NI_W_*");
+    if (fmt != NI_W_F32 && r.o.launch != NI_DRIVE_STEP)
+        return drive_fail(NI_ERR_BAD_ARG, "the unfused comparison runs f32 weights only");
+    // W [L][3C][d_in] ~ N(0, 1/d_in) in format fmt (each layer's matrix
+    // quantised on its own), bias [L][3C] ~ N(0, 0.01).
     const size_t wn = (size_t)L * F * d_in;
-    if (hipMalloc(&w, wn * sizeof(float)) != hipSuccess || hipMalloc(&bias, (size_t)L * F * sizeof(float)) != hipSuccess)
+    const size_t wl_bytes = (size_t)weight_bytes(fmt, (double)F * d_in);  // one layer's matrix
+    uint8_t* w = nullptr;
+    float* bias = nullptr;
+    if (hipMalloc(&w, (size_t)L * wl_bytes) != hipSuccess || hipMalloc(&bias, (size_t)L * F * sizeof(float)) != hipSuccess)
         return drive_fail(NI_ERR_HIP, "hipMalloc(weights) failed");
     struct Free {
-        float* p[2];
+        void* p[2];
         ~Free() {
-            for (float* q : p)
+            for (void* q : p)
                 if (q) (void)hipFree(q);
         }
     } guard{{w, bias}};
@@ -645,14 +712,19 @@ int run_qkv(Runner& r, ni_drive_result* res) {
         std::vector<float> host(wn);
         const float sc = 1.f / std::sqrt((float)d_in);
         for (auto& x : host) x = g.normal() * sc;
-        if (hipMemcpy(w, host.data(), wn * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
-            return drive_fail(NI_ERR_HIP, "hipMemcpy(weights) failed");
+        for (uint32_t l = 0; l < L; l++) {
+            std::vector<float> one(host.begin() + (size_t)l * F * d_in, host.begin() + (size_t)(l + 1) * F * d_in);
+            const std::vector<uint8_t> up = upload_weights(one, fmt);
+            if (up.size() != wl_bytes ||
+                hipMemcpy(w + (size_t)l * wl_bytes, up.data(), wl_bytes, hipMemcpyHostToDevice) != hipSuccess)
+                return drive_fail(NI_ERR_HIP, "hipMemcpy(weights) failed");
+        }
         host.resize((size_t)L * F);
         for (auto& x : host) x = g.normal() * 0.1f;
         if (hipMemcpy(bias, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
             return drive_fail(NI_ERR_HIP, "hipMemcpy(bias) failed");
     }
-    const double bytes = (double)L * ((double)F * d_in * 4 + F * 4.0 + (double)n * d_in * 4 + (double)n * C * 4 +
+    const double bytes = (double)L * ((double)wl_bytes + F * 4.0 + (double)n * d_in * 4 + (double)n * C * 4 +
                                       (double)n * 2 * C * 2);
     const double flops = 2.0 * L * n * (double)d_in * F;
     float* x = r.d.q;    // [n][d_in]
@@ -660,16 +732,17 @@ int run_qkv(Runner& r, ni_drive_result* res) {
     // The projection has no append-only form: ramp iterations run whole.
     int rc = timed_run(r, res, [&](Phase ph) -> int {
         for (uint32_t l = 0; l < L; l++) {
-            const float* wl = w + (size_t)l * F * d_in;
+            const void* wl = w + (size_t)l * wl_bytes;
             const float* bl = bias + (size_t)l * F;
             if (r.o.launch == NI_DRIVE_STEP) {
                 r.calls++;
-                if (int e = ni_kv_qkv_append(r.kv, (int32_t)l, rows.data(), n, x, d_in, d_in, wl, bl, r.d.out, C,
-                                             r.stream))
-                    return r.kv_fail(e, "ni_kv_qkv_append");
+                if (int e = ni_kv_qkv_append_w(r.kv, (int32_t)l, rows.data(), n, x, d_in, d_in, wl, fmt, bl,
+                                               r.d.out, C, r.stream))
+                    return r.kv_fail(e, "ni_kv_qkv_append_w");
             } else {
                 r.calls += 2;
-                if (int e = ni_kv_qkv_project(r.kv, x, d_in, n, d_in, wl, bl, y, F, r.stream))
+                if (int e = ni_kv_qkv_project(r.kv, x, d_in, n, d_in, static_cast<const float*>(wl), bl, y, F,
+                                              r.stream))
                     return r.kv_fail(e, "ni_kv_qkv_project");
                 if (int e = ni_kv_append(r.kv, (int32_t)l, rows.data(), n, y + C, y + 2 * C, F, 0, r.stream))
                     return r.kv_fail(e, "ni_kv_append");

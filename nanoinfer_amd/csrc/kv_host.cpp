@@ -1003,7 +1003,7 @@ int ni_kv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const
 
 // Shared checks and launch of the QKV projection; rows == NULL: plain.
 static int qkv_run(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* x, int64_t x_row_stride,
-                   uint32_t d_in, const float* w, const float* bias, float* out, int64_t out_row_stride,
+                   uint32_t d_in, const void* w, uint32_t wfmt, const float* bias, float* out, int64_t out_row_stride,
                    hipStream_t s) {
     if (!kv) return NI_ERR_BAD_ARG;
     if (kv->host_only) return kv->fail(NI_ERR_NO_DEVICE, "host-only handle has no device pools");
@@ -1015,12 +1015,15 @@ static int qkv_run(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, con
         return kv->fail(NI_ERR_BAD_ARG, "layer %d out of range (%u layers)", layer, kv->o.n_layer);
     if (n == 0) return NI_OK;
     if (n > kv->o.max_rows) return kv->fail(NI_ERR_TOO_MANY_ROWS, "%u rows > max_rows %u", n, kv->o.max_rows);
-    if (d_in == 0 || d_in % kQkvK != 0) return kv->fail(NI_ERR_BAD_ARG, "d_in %u must be a positive multiple of %u", d_in, kQkvK);
+    if (wfmt > NI_W_Q4_0) return kv->fail(NI_ERR_BAD_ARG, "unknown weight format %u", wfmt);
+    const uint32_t k_mult = wfmt >= NI_W_Q8_0 ? 32u : kQkvK;  // block formats: whole blocks per row
+    if (d_in == 0 || d_in % k_mult != 0)
+        return kv->fail(NI_ERR_BAD_ARG, "d_in %u must be a positive multiple of %u", d_in, k_mult);
     if (n_feat % kQkvTileFeat != 0)
         return kv->fail(NI_ERR_BAD_ARG, "3 * n_head * head_dim = %u must be a multiple of %u", n_feat, kQkvTileFeat);
     if (int rc = check_f32_operand(kv, "x", x, x_row_stride, 0, false)) return rc;
     if (x_row_stride < (int64_t)d_in) return kv->fail(NI_ERR_BAD_ARG, "x row stride %lld < d_in %u", (long long)x_row_stride, d_in);
-    if (!w || !aligned16(w)) return kv->fail(NI_ERR_BAD_ARG, "w must be a 16-byte aligned [3C][d_in] f32 matrix");
+    if (!w || !aligned16(w)) return kv->fail(NI_ERR_BAD_ARG, "w must be a 16-byte aligned [3C][d_in] weight matrix");
     if (bias && (reinterpret_cast<uintptr_t>(bias) & 3u)) return kv->fail(NI_ERR_BAD_ARG, "bias must be 4-byte aligned");
     if (int rc = check_f32_operand(kv, fused ? "q_out" : "out", out, out_row_stride, 0, false)) return rc;
     if (out_row_stride < (int64_t)(fused ? C : n_feat))
@@ -1040,6 +1043,7 @@ static int qkv_run(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, con
     q.x = x;
     q.x_row_stride = x_row_stride;
     q.w = w;
+    q.wfmt = wfmt;
     q.bias = bias;
     q.out = out;
     q.out_row_stride = out_row_stride;
@@ -1058,18 +1062,31 @@ static int qkv_run(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, con
     return release_plan(kv, ref, s);
 }
 
+int ni_kv_qkv_append_w(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* x,
+                       int64_t x_row_stride, uint32_t d_in, const void* w, uint32_t w_format, const float* bias,
+                       float* q_out, int64_t q_row_stride, ni_stream stream) {
+    if (kv && n && !rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
+    static const ni_row none{0, 0};
+    return qkv_run(kv, layer, rows ? rows : &none, n, x, x_row_stride, d_in, w, w_format, bias, q_out, q_row_stride,
+                   (hipStream_t)stream);
+}
+
+int ni_kv_qkv_project_w(ni_kv* kv, const float* x, int64_t x_row_stride, uint32_t n, uint32_t d_in, const void* w,
+                        uint32_t w_format, const float* bias, float* out, int64_t out_row_stride, ni_stream stream) {
+    return qkv_run(kv, 0, nullptr, n, x, x_row_stride, d_in, w, w_format, bias, out, out_row_stride,
+                   (hipStream_t)stream);
+}
+
 int ni_kv_qkv_append(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, const float* x,
                      int64_t x_row_stride, uint32_t d_in, const float* w, const float* bias, float* q_out,
                      int64_t q_row_stride, ni_stream stream) {
-    if (kv && n && !rows) return kv->fail(NI_ERR_BAD_ARG, "rows is NULL");
-    static const ni_row none{0, 0};
-    return qkv_run(kv, layer, rows ? rows : &none, n, x, x_row_stride, d_in, w, bias, q_out, q_row_stride,
-                   (hipStream_t)stream);
+    return ni_kv_qkv_append_w(kv, layer, rows, n, x, x_row_stride, d_in, w, NI_W_F32, bias, q_out, q_row_stride,
+                              stream);
 }
 
 int ni_kv_qkv_project(ni_kv* kv, const float* x, int64_t x_row_stride, uint32_t n, uint32_t d_in, const float* w,
                       const float* bias, float* out, int64_t out_row_stride, ni_stream stream) {
-    return qkv_run(kv, 0, nullptr, n, x, x_row_stride, d_in, w, bias, out, out_row_stride, (hipStream_t)stream);
+    return ni_kv_qkv_project_w(kv, x, x_row_stride, n, d_in, w, NI_W_F32, bias, out, out_row_stride, stream);
 }
 
 int ni_kv_gather(ni_kv* kv, int32_t layer, const ni_row* rows, uint32_t n, uint16_t* k_out, uint16_t* v_out,

@@ -1115,6 +1115,44 @@ constexpr int kQkvChunk = 128;
 constexpr int kQkvPad = kQkvChunk + 4;  // LDS row stride (floats): conflict-free 16-byte reads
 static_assert(kQkvChunk == 16 * kQkvParts, "one slice per part per chunk");
 
+// W[f][k .. k+3] (k a multiple of 4) as f32, dequantised as the reference's
+// weight loaders do (batch.metal:45-90: BF32, BF16, BQ8, BQ4 over the layouts
+// of crates/metal/src/weights.rs:12-86): f16 widened; Q8_0 q * d and Q4_0
+// (q - 8) * d with d the block's f16 scale -- every value exact in f32, so a
+// projection with quantised weights has the bits of the same projection
+// with the dequantised matrix in f32.  Blocks of 32 follow the row-major
+// element index f * d_in + k (d_in a multiple of 32); Q4_0 byte i of a
+// block holds element i (low nibble) and element i + 16 (high nibble).
+typedef float qkv_f4 __attribute__((ext_vector_type(4)));
+template <int WF>
+__device__ __forceinline__ qkv_f4 qkv_w4(const QkvLaunch& a, uint32_t f, uint32_t k) {
+    const uint64_t i = (uint64_t)f * a.d_in + k;
+    if constexpr (WF == kWF32) {
+        return *reinterpret_cast<const qkv_f4*>(static_cast<const float*>(a.w) + i);
+    } else if constexpr (WF == kWF16) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 h = *reinterpret_cast<const h4*>(static_cast<const uint16_t*>(a.w) + i);
+        return qkv_f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+    } else {
+        const uint8_t* wb = static_cast<const uint8_t*>(a.w);
+        const uint64_t n = (uint64_t)a.n_feat * a.d_in;
+        const uint16_t* scales = reinterpret_cast<const uint16_t*>(wb + (WF == kWQ8 ? n : n / 2));
+        const float d = (float)__builtin_bit_cast(_Float16, scales[i / 32]);
+        if constexpr (WF == kWQ8) {
+            const uint32_t q = *reinterpret_cast<const uint32_t*>(wb + i);
+            return qkv_f4{(float)(int8_t)(q & 0xffu) * d, (float)(int8_t)((q >> 8) & 0xffu) * d,
+                          (float)(int8_t)((q >> 16) & 0xffu) * d, (float)(int8_t)(q >> 24) * d};
+        } else {
+            const uint32_t j = (uint32_t)(i % 32);
+            const uint32_t q = *reinterpret_cast<const uint32_t*>(wb + (i / 32) * 16 + (j % 16));
+            const uint32_t sh = j < 16 ? 0u : 4u;
+            return qkv_f4{(float)((int)((q >> sh) & 15u) - 8) * d, (float)((int)((q >> (8 + sh)) & 15u) - 8) * d,
+                          (float)((int)((q >> (16 + sh)) & 15u) - 8) * d,
+                          (float)((int)((q >> (24 + sh)) & 15u) - 8) * d};
+        }
+    }
+}
+
 // Output y of (row, feature f): q columns (or every column when not fused)
 // to `out`, k/v as f16 (the append's rounding) into the row's page slot.
 __device__ __forceinline__ void qkv_store(const QkvLaunch& a, const AppendEntry* entries, uint32_t row, uint32_t f,
@@ -1132,7 +1170,7 @@ __device__ __forceinline__ void qkv_store(const QkvLaunch& a, const AppendEntry*
     }
 }
 
-template <int FB, int INL>
+template <int FB, int INL, int WF>
 __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int TM = kQkvTileRows, TF = 16 * FB, KC = kQkvChunk, KP = kQkvPad;
@@ -1161,8 +1199,12 @@ __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanA
 #pragma unroll
         for (int j = 0; j < WV; j++) {
             const uint32_t u = threadIdx.x + 256 * j, row = u / (KC / 4), col = 4 * (u % (KC / 4));
-            wr[j] = k0 + col < a.d_in ? *reinterpret_cast<const float4*>(a.w + (uint64_t)(n0 + row) * a.d_in + k0 + col)
-                                      : float4{0.f, 0.f, 0.f, 0.f};
+            if (k0 + col < a.d_in) {
+                const qkv_f4 v = qkv_w4<WF>(a, n0 + row, k0 + col);
+                wr[j] = float4{v[0], v[1], v[2], v[3]};
+            } else {
+                wr[j] = float4{0.f, 0.f, 0.f, 0.f};
+            }
         }
     };
     f4 acc[FB][4];  // the wave's 4 parts
@@ -1244,7 +1286,7 @@ __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanA
 // qkv_kernel, so the bits are the same at every row count.
 constexpr int kQkvBatch = 6;
 
-template <int RB, int INL>
+template <int RB, int INL, int WF>
 __global__ __launch_bounds__(64 * kQkvParts) void qkv_small_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     __shared__ f4 red[kQkvParts][RB][64];
@@ -1257,7 +1299,7 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_small_kernel(const QkvLaun
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)  // rows past n_rows repeat the last row (their results are dropped)
         xr[rb] = a.x + (int64_t)min(m0 + 16 * rb + i, a.n_rows - 1) * a.x_row_stride + 4 * g;
-    const float* wr = a.w + (uint64_t)(n0 + i) * a.d_in + 4 * g;
+
     f4 acc[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) acc[rb] = f4{0.f, 0.f, 0.f, 0.f};
@@ -1269,7 +1311,8 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_small_kernel(const QkvLaun
             if (sl < n_slices) {
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++) xv[j][rb] = *reinterpret_cast<const float4*>(xr[rb] + 16 * sl);
-                wv[j] = *reinterpret_cast<const float4*>(wr + 16 * sl);
+                const qkv_f4 w = qkv_w4<WF>(a, n0 + i, 16 * sl + 4 * g);
+                wv[j] = float4{w[0], w[1], w[2], w[3]};
             }
         }
 #pragma unroll
@@ -1872,7 +1915,7 @@ __device__ __forceinline__ void wait_tiles(uint32_t ahead) {
 #endif
 constexpr int kQkvMidChunks = 8;  // chunks of d_in held in registers: d_in up to 1024 on this kernel
 
-template <int INL>
+template <int INL, int WF>
 __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int KC = kQkvChunk;       // d_in values per chunk (8 slices of 16)
@@ -1905,7 +1948,7 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch
     // partial chunk) load the row's first piece (their slices are skipped).
     const uint32_t dr = 2 * p + (lane >> 5), pc = lane & 31;
     const float* xsrc = a.x + (int64_t)min(m0 + dr, a.n_rows - 1) * a.x_row_stride;
-    const float* wsrc = a.w + (uint64_t)(n0 + dr) * a.d_in;
+
     const uint32_t wo = dr * RB + 16u * (pc ^ (dr & 15));
     // Lane (i, g) reads piece 4p + g of x row i and of W row i.
     const uint32_t rd = (uint32_t)i * RB + 16u * ((4u * p + (uint32_t)g) ^ (uint32_t)i);
@@ -1917,7 +1960,7 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch
         uint32_t col = min((uint32_t)j, n_chunks - 1) * KC + 4 * pc;
         col = col < a.d_in ? col : 0;
         xr[j] = *reinterpret_cast<const f4*>(xsrc + col);
-        wr[j] = *reinterpret_cast<const f4*>(wsrc + col);
+        wr[j] = qkv_w4<WF>(a, n0 + dr, col);
     }
     f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma clang loop unroll(full)
@@ -2631,15 +2674,15 @@ hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hip
     });
 }
 
-hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
-    if (a.n_rows == 0) return hipSuccess;
+template <int WF>
+hipError_t launch_qkv_t(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     if (a.n_rows <= NI_QKV_SMALL_ROWS) {
         constexpr int RB = NI_QKV_SMALL_RB;
         const dim3 grid((a.n_rows + 16 * RB - 1) / (16 * RB), a.n_feat / 16);
         return with_plan(a, ip, ib, [&](auto pa) {
             constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-            hipExtLaunchKernelGGL(qkv_small_kernel<RB, INL>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0, a,
-                                  pa);
+            hipExtLaunchKernelGGL(qkv_small_kernel<RB, INL, WF>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0,
+                                  a, pa);
             return hipGetLastError();
         });
     }
@@ -2647,7 +2690,8 @@ hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream
         const dim3 grid((a.n_rows + 15) / 16 * (a.n_feat / 16));  // (row tile, feature tile), dealt by XCD
         return with_plan(a, ip, ib, [&](auto pa) {
             constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-            hipExtLaunchKernelGGL(qkv_mid_kernel<INL>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0, a, pa);
+            hipExtLaunchKernelGGL(qkv_mid_kernel<INL, WF>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0, a,
+                                  pa);
             return hipGetLastError();
         });
     }
@@ -2656,9 +2700,21 @@ hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream
     const dim3 grid((a.n_rows + kQkvTileRows - 1) / kQkvTileRows, a.n_feat / kQkvTileFeat);
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-        hipExtLaunchKernelGGL(qkv_kernel<kQkvTileFeat / 16, INL>, grid, dim3(256), 0, s, t.start, t.stop, 0, a, pa);
+        hipExtLaunchKernelGGL(qkv_kernel<kQkvTileFeat / 16, INL, WF>, grid, dim3(256), 0, s, t.start, t.stop, 0, a,
+                              pa);
         return hipGetLastError();
     });
+}
+
+hipError_t launch_qkv(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
+    if (a.n_rows == 0) return hipSuccess;
+    switch (a.wfmt) {
+        case kWF32: return launch_qkv_t<kWF32>(a, ip, ib, s, t);
+        case kWF16: return launch_qkv_t<kWF16>(a, ip, ib, s, t);
+        case kWQ8: return launch_qkv_t<kWQ8>(a, ip, ib, s, t);
+        case kWQ4: return launch_qkv_t<kWQ4>(a, ip, ib, s, t);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gather_q8(const GatherQ8Launch& a, const void* ip, uint32_t ib, hipStream_t s) {

@@ -121,15 +121,20 @@ struct GatherLaunch {
     uint32_t n_lay;
 };
 
+// Weight formats of the projection (the values of NI_W_* in nanoinfer_kv.h).
+enum : uint32_t { kWF32 = 0, kWF16 = 1, kWQ8 = 2, kWQ4 = 3 };
+
 // The QKV projection y = x W^T + b of n rows (W [n_feat][d_in] row-major, the
-// reference's weight layout, n_feat = 3C).  Fused: q columns to `out`
-// ([n][C]), k/v columns as f16 to each row's page slot of `layer` (entries
-// in the plan, src_row = x row).  Plain: every column to `out` ([n][3C]).
+// reference's weight layout, n_feat = 3C, in one of its formats).  Fused: q
+// columns to `out` ([n][C]), k/v columns as f16 to each row's page slot of
+// `layer` (entries in the plan, src_row = x row).  Plain: every column to
+// `out` ([n][3C]).
 struct QkvLaunch {
     PoolGeom pool;
     const float* x;
     int64_t x_row_stride;
-    const float* w;
+    const void* w;      // [n_feat][d_in] in format `wfmt`
+    uint32_t wfmt;
     const float* bias;  // [n_feat] or null
     float* out;
     int64_t out_row_stride;

@@ -5,6 +5,7 @@
 //
 //   ni_drive [serve|spec|qkv|prefill] [--per-layer|--step-layers] [--steps K] [--warmup W]
 //            [--ramp R] [--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]
+//            [--wfmt f32|f16|q8_0|q4_0]
 //
 // --ramp: R append-only iterations (no attention) before the warmup.
 //
@@ -16,7 +17,8 @@
 // empty, every row queried, rolled back each iteration.
 //
 // qkv: the QKV projection of N rows per layer with K/V appended in its
-// epilogue; --per-layer runs the unfused path (f32 projection + append).
+// epilogue, weights in --wfmt; --per-layer runs the unfused path (f32
+// projection + append).
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -48,6 +50,11 @@ int main(int argc, char** argv) {
         if (!strcmp(a, "serve") || !strcmp(a, "spec") || !strcmp(a, "qkv") || !strcmp(a, "prefill")) workload = a;
         else if (!strcmp(a, "--rows")) o.qkv_rows = (uint32_t)atoi(val(a));
         else if (!strcmp(a, "--q8")) q8 = true;
+        else if (!strcmp(a, "--wfmt")) {  // qkv: f32 (default), f16, q8_0, q4_0
+            const char* f = val(a);
+            o.qkv_wformat = !strcmp(f, "f16") ? NI_W_F16 : !strcmp(f, "q8_0") ? NI_W_Q8_0
+                          : !strcmp(f, "q4_0") ? NI_W_Q4_0 : NI_W_F32;
+        }
         else if (!strcmp(a, "--per-layer")) o.launch = NI_DRIVE_PER_LAYER;
         else if (!strcmp(a, "--step-layers")) o.launch = NI_DRIVE_STEP_LAYERS;
         else if (!strcmp(a, "--all-prompt-rows")) o.serve.query_all_prompt_rows = 1;
@@ -58,7 +65,7 @@ int main(int argc, char** argv) {
         else if (!strcmp(a, "--seed")) o.data_seed = o.serve.seed = strtoull(val(a), nullptr, 10);
         else {
             fprintf(stderr, "usage: ni_drive [serve|spec|qkv|prefill] [--per-layer|--step-layers] [--steps K] [--warmup W] "
-                            "[--ramp R] [--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8]\n");
+                            "[--ramp R] [--split T] [--all-prompt-rows] [--seed S] [--rows N] [--q8] [--wfmt F]\n");
             return 2;
         }
     }

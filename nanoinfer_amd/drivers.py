@@ -39,7 +39,7 @@ class ni_drive_opts(C.Structure):
                 ("spec_seed", C.c_uint64), ("spec_window", _u32), ("ramp", _u32), ("warmup", _u32), ("steps", _u32),
                 ("split_tokens", _u32), ("data_seed", C.c_uint64), ("fixed_ctx", C.POINTER(_u32)),
                 ("fixed_n", _u32), ("kv_std", C.c_float), ("profile_mask", _u32), ("qkv_rows", _u32),
-                ("fixed_rows", _u32)]
+                ("fixed_rows", _u32), ("qkv_wformat", _u32)]
 
 
 class ni_drive_result(C.Structure):
@@ -247,9 +247,17 @@ def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, spli
         o.fixed_ctx, o.fixed_n, o.fixed_rows = arr.ctypes.data_as(C.POINTER(_u32)), B, P
         _kv(o, workloads.GPT2, B * workloads.pages(P) + 8, B, 1024, B * P)
     elif name.startswith("qkv"):
-        # qkv<rows>: the projection of <rows> rows per layer, GPT-2 shape
+        # qkv<rows>[f16|q8|q4]: the projection of <rows> rows per layer, GPT-2
+        # shape, with f32 weights or in one of the reference's weight formats
         o.workload = NI_DRIVE_QKV
-        o.qkv_rows = int(name[3:] or 64)
+        spec = name[3:]
+        fmt = 0
+        for suffix, f in (("f16", 1), ("q8", 2), ("q4", 3)):
+            if spec.endswith(suffix):
+                spec, fmt = spec[: -len(suffix)], f
+                break
+        o.qkv_rows = int(spec or 64)
+        o.qkv_wformat = fmt
         _kv(o, workloads.GPT2, 64 * 64, 64, 1024, 512)
     else:
         raise ValueError(name)

@@ -83,6 +83,12 @@ def lib():
                                      _sz, _sz, _f32p]
     L.or_split_attention_f64.argtypes = [_f64p, _f32p, _f32p, _f32p, _sz, _sz, _sz]
     L.or_matvec_f64.argtypes = [_f64p, _f32p, _sz, _f32p, C.c_void_p, _sz, _sz, _sz]
+    _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+    L.or_quantize_q8_0.restype = _sz
+    L.or_quantize_q8_0.argtypes = [_f32p, _sz, _u8p]
+    L.or_quantize_q4_0.restype = _sz
+    L.or_quantize_q4_0.argtypes = [_f32p, _sz, _u8p]
+    L.or_dequantize.argtypes = [_u8p, _sz, C.c_int, _f32p]
     _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
     L.or_q8_quantize.restype = C.c_float
     L.or_q8_quantize.argtypes = [_f32p, _sz, _i8p]
@@ -241,6 +247,40 @@ def matvec_f64(x, w, bias=None):
     out = np.zeros((n, d_out), np.float64)
     b = None if bias is None else _f32(bias)
     lib().or_matvec_f64(out, x.reshape(-1), d_in, w.reshape(-1), None if b is None else b.ctypes.data, n, d_in, d_out)
+    return out
+
+
+# ------------------------------------------------------------ weight formats
+
+W_FORMAT_IDS = {"f32": 0, "f16": 1, "q8_0": 2, "q4_0": 3}
+
+
+def quantize(w, fmt: str) -> np.ndarray:
+    """The reference's weight upload (weights.rs:12-27, 54-72, 115-118) of a
+    row-major matrix w in format fmt, as bytes (uint8)."""
+    w = _f32(w).reshape(-1)
+    n = w.size
+    if fmt == "f32":
+        return w.view(np.uint8).copy()
+    if fmt == "f16":
+        return f32_to_f16(w).view(np.uint8).copy()
+    assert n % 32 == 0, "block formats need whole blocks of 32"
+    if fmt == "q8_0":
+        out = np.zeros(n + n // 16, np.uint8)
+        assert lib().or_quantize_q8_0(w, n, out) == out.size
+        return out
+    if fmt == "q4_0":
+        out = np.zeros(n // 2 + n // 16, np.uint8)
+        assert lib().or_quantize_q4_0(w, n, out) == out.size
+        return out
+    raise ValueError(fmt)
+
+
+def dequantize(q, n: int, fmt: str) -> np.ndarray:
+    """weights.rs:29-52 (and the f16/f32 formats): n weights from bytes q."""
+    q = np.ascontiguousarray(q, dtype=np.uint8).reshape(-1)
+    out = np.zeros(n, np.float32)
+    lib().or_dequantize(q, n, W_FORMAT_IDS[fmt], out)
     return out
 
 

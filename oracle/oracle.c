@@ -734,6 +734,97 @@ void or_matvec_f64(double* out, const float* x, size_t x_stride, const float* w,
 }
 
 /* ------------------------------------------------------------------------- */
+/* Weight formats of the projection (crates/metal/src/weights.rs)             */
+/* ------------------------------------------------------------------------- */
+
+/* quantize_q8_0, weights.rs:12-27, over n weights (n a multiple of 32), into
+ * out: [n] int8 quants, then [n / 32] little-endian f16 scales.  Per block:
+ * amax = max |w| (f32 max fold), d = amax / 127, id = d > 0 ? 1 / d : 0,
+ * q = (w * id).round() as i8 -- Rust's round is half away from zero, `as`
+ * saturates (and takes NaN to 0); the scale is f16::from_f32(d) (round to
+ * nearest even, or_f32_to_f16).  Returns the bytes written, n + n / 16. */
+size_t or_quantize_q8_0(const float* w, size_t n, uint8_t* out) {
+    uint8_t* sc = out + n;
+    for (size_t b = 0; b < n / 32; b++) {
+        const float* blk = w + 32 * b;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(blk[i]));
+        volatile float d = amax / 127.0f;
+        volatile float id = d > 0.0f ? 1.0f / d : 0.0f;
+        for (int i = 0; i < 32; i++) {
+            volatile float t = blk[i] * id;
+            float r = roundf(t);
+            int32_t q = r != r ? 0 : r >= 127.0f ? 127 : r <= -128.0f ? -128 : (int32_t)r;
+            out[32 * b + i] = (uint8_t)(int8_t)q;
+        }
+        uint16_t h = or_f32_to_f16(d);
+        sc[2 * b] = (uint8_t)(h & 0xff);
+        sc[2 * b + 1] = (uint8_t)(h >> 8);
+    }
+    return n + n / 16;
+}
+
+/* quantize_q4_0, weights.rs:54-72 (GGML's rounding): per block of 32, max =
+ * the value of largest magnitude (the first one on ties: replaced only when
+ * |v| > |max|), d = max / -8, id = d != 0 ? 1 / d : 0, q(v) = ((v * id + 8.5)
+ * as i32).clamp(0, 15) (`as` truncates toward zero, saturating, NaN to 0);
+ * byte i of the block = q(w[i]) | q(w[i + 16]) << 4.  Then the [n / 32] f16
+ * scales.  Returns the bytes written, n / 2 + n / 16. */
+size_t or_quantize_q4_0(const float* w, size_t n, uint8_t* out) {
+    uint8_t* sc = out + n / 2;
+    for (size_t b = 0; b < n / 32; b++) {
+        const float* blk = w + 32 * b;
+        float mx = 0.0f;
+        for (int i = 0; i < 32; i++)
+            if (fabsf(blk[i]) > fabsf(mx)) mx = blk[i];
+        volatile float d = mx / -8.0f;
+        volatile float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t q[32];
+        for (int i = 0; i < 32; i++) {
+            volatile float t = blk[i] * id;
+            volatile float u = t + 8.5f;
+            float tr = truncf(u);
+            int32_t v = u != u ? 0 : tr >= 2147483647.0f ? 2147483647 : tr <= -2147483648.0f ? (-2147483647 - 1) : (int32_t)tr;
+            q[i] = (uint8_t)(v < 0 ? 0 : v > 15 ? 15 : v);
+        }
+        for (int i = 0; i < 16; i++) out[16 * b + i] = (uint8_t)(q[i] | (q[i + 16] << 4));
+        uint16_t h = or_f32_to_f16(d);
+        sc[2 * b] = (uint8_t)(h & 0xff);
+        sc[2 * b + 1] = (uint8_t)(h >> 8);
+    }
+    return n / 2 + n / 16;
+}
+
+/* dequantize, weights.rs:29-52, for fmt 2 (Q8_0: q * d) and 3 (Q4_0:
+ * (nibble - 8) * d, element j of a block in byte j % 16, low nibble for
+ * j < 16), each product in f32; fmt 1 (F16) widens f16 bits; fmt 0 copies. */
+void or_dequantize(const uint8_t* q, size_t n, int fmt, float* out) {
+    if (fmt == 0) {
+        memcpy(out, q, n * sizeof(float));
+        return;
+    }
+    if (fmt == 1) {
+        for (size_t i = 0; i < n; i++) out[i] = or_f16_to_f32((uint16_t)(q[2 * i] | (q[2 * i + 1] << 8)));
+        return;
+    }
+    const size_t qbytes = fmt == 2 ? n : n / 2;
+    for (size_t i = 0; i < n; i++) {
+        const size_t b = i / 32, j = i % 32;
+        const uint16_t h = (uint16_t)(q[qbytes + 2 * b] | (q[qbytes + 2 * b + 1] << 8));
+        const float d = or_f16_to_f32(h);
+        float v;
+        if (fmt == 2) {
+            v = (float)(int8_t)q[i];
+        } else {
+            const uint8_t byte = q[b * 16 + j % 16];
+            v = (float)(j < 16 ? (byte & 15) : (byte >> 4)) - 8.0f;
+        }
+        volatile float r = v * d;
+        out[i] = r;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
 /* Q8 KV cache (crates/metal/src/shaders/kv8.metal)                           */
 /* ------------------------------------------------------------------------- */
 

@@ -164,3 +164,72 @@ def test_qkv_errors(gpu):
         kv.qkv_project(torch.zeros((2, 40), device="cuda"), w40)
     with pytest.raises(na.KvError, match="max_rows"):
         kv.qkv_project(torch.zeros((17, 64), device="cuda"), w)
+
+
+@pytest.mark.parametrize("fmt", ["f16", "q8_0", "q4_0"])
+def test_weight_formats_equal_the_dequantised_projection(gpu, oracle_lib, fmt):
+    """The reference's weight formats (DType, weights.rs:12-86, loaded by
+    batch.metal:45-90's BF16/BQ8/BQ4): each weight is dequantised exactly into
+    f32 on load, so the projection with the quantised bytes has the bits of
+    the f32 projection with the dequantised matrix, at every row count (all
+    three kernels), and is within f32 rounding of the f64 product."""
+    shape = workloads.GPT2
+    rng = np.random.default_rng(90)
+    kv = make(shape)
+    c, d_in = kv.opts.n_embd, 768
+    w, b = weights(rng, c, d_in)
+    wq = oracle.quantize(w, fmt)
+    wdq = oracle.dequantize(wq, w.size, fmt).reshape(w.shape)
+    x = rng.standard_normal((512, d_in)).astype(np.float32)
+    xd, wqd, wdd, bd = (torch.from_numpy(t).cuda() for t in (x, wq, wdq, b))
+    for n in (1, 9, 16, 17, 40, 64, 100, 512):
+        got = kv.qkv_project(xd[:n].contiguous(), wqd, bd, w_format=fmt).cpu().numpy()
+        ref = kv.qkv_project(xd[:n].contiguous(), wdd, bd).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"{fmt} n={n}"
+    err = np.abs(got.astype(np.float64) - oracle.matvec_f64(x, wdq, b)).max()
+    assert err < 2e-5, err
+    say(f"{fmt}: bit-identical to the dequantised f32 projection at 1..512 rows; max err vs f64 {err:.2e}")
+
+
+@pytest.mark.parametrize("fmt", ["f16", "q4_0"])
+def test_weight_formats_fused_append(gpu, oracle_lib, fmt):
+    """ni_kv_qkv_append_w stores f32_to_f16 of ni_kv_qkv_project_w's k/v
+    columns and returns its q columns, bit for bit."""
+    rng = np.random.default_rng(91)
+    kv = make(workloads.GPT2)
+    c, d_in = kv.opts.n_embd, 768
+    s = kv.add_seq()
+    kv.reserve(s, 100)
+    rows = [(s, p) for p in range(3, 100, 3)]
+    w, b = weights(rng, c, d_in)
+    wq = torch.from_numpy(oracle.quantize(w, fmt)).cuda()
+    x = torch.from_numpy(rng.standard_normal((len(rows), d_in)).astype(np.float32)).cuda()
+    bd = torch.from_numpy(b).cuda()
+    y = kv.qkv_project(x, wq, bd, w_format=fmt).cpu().numpy()
+    q = kv.qkv_append(rows, x, wq, bd, layer=5, w_format=fmt).cpu().numpy()
+    assert np.array_equal(q, y[:, :c])
+    kg, vg = kv.gather(rows, layer=5)
+    assert np.array_equal(kg.cpu().numpy().view(np.uint16), oracle.f32_to_f16(y[:, c:2 * c]))
+    assert np.array_equal(vg.cpu().numpy().view(np.uint16), oracle.f32_to_f16(y[:, 2 * c:]))
+
+
+def test_weight_format_errors(gpu):
+    kv = make(dict(n_layer=2, n_head=2, head_dim=64), kv_blocks=8, n_ctx=64, max_rows=16)
+    c = 128
+    x = torch.zeros((2, 48), device="cuda")
+    with pytest.raises(ValueError, match="multiple of 32"):
+        kv.qkv_project(x, torch.zeros(3 * c * 48 // 2 + 3 * c * 48 // 16, dtype=torch.uint8, device="cuda"),
+                       w_format="q4_0")
+    with pytest.raises(ValueError, match="bytes"):
+        kv.qkv_project(torch.zeros((2, 64), device="cuda"), torch.zeros(100, dtype=torch.uint8, device="cuda"),
+                       w_format="q8_0")
+    with pytest.raises(ValueError, match="unknown weight format"):
+        kv.qkv_project(torch.zeros((2, 64), device="cuda"), torch.zeros(1, device="cuda"), w_format="bf16")
+    L = kv._L
+    w = torch.zeros(3 * c * 48, dtype=torch.uint8, device="cuda")  # the library's own check, past the wrapper
+    rc = L.ni_kv_qkv_project_w(kv.handle, x.data_ptr(), 48, 2, 48, w.data_ptr(), 2, None,
+                               torch.zeros((2, 3 * c), device="cuda").data_ptr(), 3 * c, None)
+    assert rc == na._abi.NI_ERR_BAD_ARG and "multiple of 32" in L.ni_kv_last_error(kv.handle).decode()
+    rc = L.ni_kv_qkv_project_w(kv.handle, x.data_ptr(), 48, 2, 48, w.data_ptr(), 7, None,
+                               torch.zeros((2, 3 * c), device="cuda").data_ptr(), 3 * c, None)
+    assert rc == na._abi.NI_ERR_BAD_ARG and "unknown weight format" in L.ni_kv_last_error(kv.handle).decode()
