@@ -513,7 +513,7 @@ SECONDARY_LINES = {
     "config4": (100, 10, "attn_split_kernel + attn_merge_kernel"),
     "config5": (200, 20, "attn_mfma_kernel (fused append)"),
     "config3q8": (200, 20, "attn_q8_kernel (fused append), Q8 cache"),
-    "prefill": (50, 5, "attn_prefill_kernel (after its append launch)"),
+    "prefill": (50, 5, "attn_prefill_kernel (appending the prompt rows itself)"),
     "qkv64": (200, 20, "qkv_kernel (append in the epilogue)"),
 }
 
@@ -542,11 +542,11 @@ def secondary_lines(args, reps=3):
             line["tflops"] = round(r["flops"] / r["seconds"] / 1e12, 2)
             mask, ids = 1 << 3, (3,)
         else:
-            mask, ids = (1 << 1) | (1 << 2), (1, 2)
+            mask, ids = (1 << 0) | (1 << 1) | (1 << 2), (1, 2)
         rp = _drive(name, a, profile_mask=mask, ramp=ramp)
         kms = sum(rp["kernel_ms"][i] for i in ids)
-        if name == "prefill":
-            # the attention launch alone: the step's bytes less its append's
+        if name == "prefill" and rp["kernel_launches"][0]:
+            # the attention launch alone: the step's bytes less its append launch's
             c, L = 768, 12
             app = drivers_prefill_append_bytes(c, L)
             kb = rp["bytes"] / rp["steps"] - app
@@ -560,8 +560,8 @@ def secondary_lines(args, reps=3):
 
 
 def drivers_prefill_append_bytes(c, L):
-    """Algorithmic bytes of the prefill step's separate append launch (f32
-    K/V read, f16 written), per step."""
+    """Algorithmic bytes of the prefill step's append (f32 K/V read, f16
+    written), per step."""
     from nanoinfer_amd import drivers
 
     return drivers.PREFILL_SEQS * drivers.PREFILL_ROWS * L * (8 * c + 4 * c)
@@ -660,9 +660,11 @@ PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16 matrix throughput, AMD's published 
 def run_prefill(args):
     """Prefill: 16 sequences each append a 512-row prompt from empty and
     attend every row causally (groups of up to 64 rows on the prefill
-    kernel, after a separate append launch), rolled back each step.  The
-    roofline prices the attention launch alone: its algorithmic bytes (q
-    read, out written, each sequence's K/V read once) against HBM, with its
+    kernel, whose workgroups append each sequence's rows before its groups
+    read them), rolled back each step.  The roofline prices the prefill
+    launch: its algorithmic bytes (the rows' f32 K/V read and stored, q
+    read, out written, each sequence's K/V read once; without the rows'
+    bytes when a separate append launch stored them) against HBM, with its
     useful flops (4 per query, visible key and element of C) against the f16
     matrix peak beside them."""
     from nanoinfer_amd import drivers, workloads
@@ -686,7 +688,8 @@ def run_prefill(args):
         steps = rp["steps"]
         attn_ms = rp["kernel_ms"][1] + rp["kernel_ms"][2]
         append_bytes = B * P * L * (8 * c + 2 * kvb)
-        attn_bytes = rp["bytes"] / steps - append_bytes
+        fused = rp["kernel_launches"][0] == 0  # the prefill launch appends the rows
+        attn_bytes = rp["bytes"] / steps - (0 if fused else append_bytes)
         t = attn_ms / 1e3 / steps
         gbs = attn_bytes / t / 1e9
         tfl = rp["flops"] / steps / t / 1e12
@@ -697,7 +700,8 @@ def run_prefill(args):
                            "algorithmic_bytes_per_launch": int(attn_bytes),
                            "flops_per_launch": int(rp["flops"] / steps), "achieved_tflops": round(tfl, 2),
                            "frac_of_f16_matrix_peak": round(tfl / PEAK_F16_TFLOPS, 4),
-                           "append_us": round(rp["kernel_ms"][0] / steps * 1e3, 3)}
+                           "append": "in the prefill launch" if fused else
+                           f"its own launch, {rp['kernel_ms'][0] / steps * 1e3:.3f} us per step"}
     return res
 
 

@@ -58,6 +58,13 @@ constexpr uint32_t kRingSlots = 4;
 #ifndef NI_PREFILL_SEQ_ORDER
 #define NI_PREFILL_SEQ_ORDER 1
 #endif
+// A step of prompt chunks (every sequence queried as prefill groups, no
+// partitions): the prefill launch appends each sequence's rows (one workgroup
+// per sequence, layer and head, its groups in turn) instead of an append
+// launch before it.
+#ifndef NI_PREFILL_SEQ_APPEND
+#define NI_PREFILL_SEQ_APPEND 1
+#endif
 #ifndef NI_LAYER_PLAN_STAGED
 #define NI_LAYER_PLAN_STAGED 0
 #endif
@@ -91,15 +98,19 @@ struct Plan {
     std::vector<AttnItem> pitems;    // prefill groups (attn_prefill_kernel), their merges
     std::vector<MergeItem> pmerges;  //   and partial slots (a region after the others')
     std::vector<uint32_t> table;
+    std::vector<PrefillSeq> pseqs;  // prompt-chunk step: the prefill launch appends, a workgroup per sequence
     uint32_t n_slots = 0;
     uint32_t n_pslots = 0;
     uint32_t nq_tile = 1;
     uint32_t napp_total = 0;  // fused: rows the attention items append
     bool fused = false;
     bool wide = false;        // kWideWaves waves per attention workgroup
+    bool seq_prefill = false; // every row belongs to a sequence queried as prefill groups (see pseqs)
     void clear() {
         app.clear();
         orphans.clear();
+        pseqs.clear();
+        seq_prefill = false;
         items.clear();
         merges.clear();
         pitems.clear();
@@ -116,7 +127,7 @@ struct Plan {
 
 // Byte offsets of each part of a serialised plan.
 struct Offsets {
-    size_t app, orphans, items, merges, pitems, pmerges, table, total;
+    size_t app, orphans, items, merges, pitems, pmerges, pseqs, table, total;
 };
 
 // Where the kernels find a plan: in the launch arguments (small plans) or in
@@ -134,7 +145,7 @@ struct PlanRef {
 struct QRow {
     uint32_t row, seq, pos;
     uint32_t new_begin, new_end, app_first;
-    uint32_t pre = 0;  // fused step: a prompt chunk queried at more rows than one matrix tile (prefill launch)
+    uint32_t pre = 0;  // fused or prompt-chunk step: a chunk queried at more rows than one matrix tile (prefill launch)
 };
 
 }  // namespace
@@ -414,8 +425,19 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         }
         (g.pre || g.nq > kMfmaTile ? P.pitems : P.items).push_back(it);
     };
+    // Per sequence (page-list offset): its appended rows, for prefill
+    // workgroups that append them (P.seq_prefill).
+    struct SeqRows {
+        uint32_t app_first, new_begin, new_end;
+    };
+    std::vector<SeqRows> app_of;  // by table offset
     for (const Group& g : groups) {
         const bool pre = g.pre || g.nq > kMfmaTile;
+        if (P.seq_prefill) {
+            const uint32_t tab = (uint32_t)kv->seq_tab[g.seq];
+            if (app_of.size() <= tab) app_of.resize(tab + 1, {0u, 0u, 0u});
+            app_of[tab] = {g.app_first, g.new_begin, g.new_end};
+        }
         if (!pre) max_nq = std::max(max_nq, g.nq);
         const uint32_t L = g.pos0 + g.nq;
         const uint32_t n_parts = (L + part - 1) / part;
@@ -460,6 +482,36 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
 #else
     std::stable_sort(P.pitems.begin(), P.pitems.end(), longest_first);
 #endif
+    // Prompt-chunk step without partitions: one prefill workgroup per
+    // (sequence, layer, head) runs the sequence's groups shortest first, each
+    // after appending the new rows up to its last key (the last group: all
+    // that are left), so the append's loads interleave with attention.
+    if (P.seq_prefill && NI_PREFILL_SEQ_ORDER && P.items.empty() && P.n_pslots == 0 && !P.pitems.empty()) {
+        uint64_t rows = 0;
+        for (uint32_t i = 0; i < P.pitems.size();) {
+            const uint32_t tab = P.pitems[i].tab;
+            uint32_t e = i + 1;
+            while (e < P.pitems.size() && P.pitems[e].tab == tab) e++;
+            std::reverse(P.pitems.begin() + i, P.pitems.begin() + e);  // longest first -> shortest first
+            const SeqRows& sr = app_of[tab];
+            uint32_t lo = sr.new_begin;
+            for (uint32_t j = i; j < e; j++) {
+                AttnItem& it = P.pitems[j];
+                const uint32_t hi = j + 1 == e ? sr.new_end : std::max(lo, std::min(it.kv_end, sr.new_end));
+                it.app0 = sr.app_first + (lo - sr.new_begin);
+                it.napp = hi - lo;
+                lo = hi;
+            }
+            P.pseqs.push_back({i, e - i});
+            rows += sr.new_end - sr.new_begin;
+            i = e;
+        }
+        if (rows != P.app.size()) {  // some rows belong to no prefill sequence: append launch
+            P.pseqs.clear();
+            for (AttnItem& it : P.pitems) it.app0 = it.napp = 0;
+        }
+    }
+    P.seq_prefill = !P.pseqs.empty();
     // Single queries stream on the vector kernel; groups go to matrix cores.
     P.nq_tile = (NI_ATTN_MFMA && max_nq > 1) ? kMfmaTile : max_nq;
     return NI_OK;
@@ -555,7 +607,8 @@ Offsets layout(const Plan& P) {
     o.merges = align_up(o.items + P.items.size() * sizeof(AttnItem), kAlign);
     o.pitems = align_up(o.merges + P.merges.size() * sizeof(MergeItem), kAlign);
     o.pmerges = align_up(o.pitems + P.pitems.size() * sizeof(AttnItem), kAlign);
-    o.table = align_up(o.pmerges + P.pmerges.size() * sizeof(MergeItem), kAlign);
+    o.pseqs = align_up(o.pmerges + P.pmerges.size() * sizeof(MergeItem), kAlign);
+    o.table = align_up(o.pseqs + P.pseqs.size() * sizeof(PrefillSeq), kAlign);
     o.total = align_up(o.table + P.table.size() * sizeof(uint32_t), kAlign);
     return o;
 }
@@ -575,6 +628,7 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
     if (!P.pitems.empty()) memcpy(blob.data() + off->pitems, P.pitems.data(), P.pitems.size() * sizeof(AttnItem));
     if (!P.pmerges.empty())
         memcpy(blob.data() + off->pmerges, P.pmerges.data(), P.pmerges.size() * sizeof(MergeItem));
+    if (!P.pseqs.empty()) memcpy(blob.data() + off->pseqs, P.pseqs.data(), P.pseqs.size() * sizeof(PrefillSeq));
     if (!P.table.empty()) memcpy(blob.data() + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
     *ref = PlanRef{};
     if (kv->no_alloc) {
@@ -640,7 +694,7 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
         int rc = ensure_partials(kv, (main_floats + pre_floats) * sizeof(float), &partials);
         if (rc) return rc;
     }
-    if (!P.app.empty() && !P.fused) {
+    if (!P.app.empty() && !P.fused && !P.seq_prefill) {
         AppendLaunch a;
         a.pool = kv->geom();
         a.k = k;
@@ -719,6 +773,15 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
         a.n_lay = n_lay;
         a.nq_tile = kPrefillRows;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
+        if (P.seq_prefill) {  // the launch appends the rows too
+            a.k = k;
+            a.v = v;
+            a.kv_row_stride = kv_row_stride;
+            a.kv_layer_stride = kv_layer_stride;
+            a.off_app = (uint32_t)off.app;
+            a.off_pseqs = (uint32_t)off.pseqs;
+            a.n_pseqs = (uint32_t)P.pseqs.size();
+        }
         {
             ProfileScope ps(kv, NI_K_ATTN);
             hipError_t e = launch_attention(a, ref.inl, ref.inl_bytes, s, ps.t);
@@ -1425,6 +1488,12 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
     }
     if (big) fused = prefill && small;
     kv->plan.fused = fused;
+    // A step of prompt chunks whose every sequence is queried as prefill
+    // groups: the prefill launch appends each sequence's rows itself (one
+    // workgroup per sequence, layer and head), no append launch.
+    bool every_big = n_work > 0;
+    for (uint32_t w = 0; w < n_work; w++) every_big &= work[w].n_query > max_group_rows(kv);
+    kv->plan.seq_prefill = NI_PREFILL_SEQ_APPEND && prefill && !fused && every_big;
     uint32_t row = 0;
     for (uint32_t w = 0; w < n_work; w++) {
         const ni_work& it = work[w];
@@ -1435,7 +1504,10 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
             const uint32_t pos = len + i;
             const AppendEntry e{row, pg[pos / kPage], pos % kPage, 0};
             kv->plan.app.push_back(e);
-            const bool pre = fused && it.n_query > max_group_rows(kv);
+            // (a prompt chunk's short last group too: in a fused step its rows
+            // are appended by the extra blocks, in a prompt-chunk step by its
+            // sequence's prefill workgroup)
+            const bool pre = (fused || kv->plan.seq_prefill) && it.n_query > max_group_rows(kv);
             if (fused && (it.n_query == 0 || pre)) kv->plan.orphans.push_back(e);
             if (i >= it.n_new - it.n_query) kv->qrows.push_back({row, it.seq, pos, len, len + it.n_new, first, pre});
         }

@@ -17,7 +17,9 @@
 //   attn_mfma_kernel   the same for groups of 2..16 causal query rows of one
 //                      sequence, on the matrix cores
 //   attn_prefill_kernel  groups of 17..64 rows (prompt chunks), K/V tiles DMA'd
-//                      into an LDS ring shared by four waves (attn.metal:100-222)
+//                      into an LDS ring shared by four waves (attn.metal:100-222);
+//                      in a step of prompt chunks only, a workgroup runs one
+//                      sequence's groups, appending the rows each needs first
 //   attn_q8_kernel     single rows on the int8 + scale (Q8) cache (kv8.metal)
 //   attn_merge_kernel  log-sum-exp merge of partitions (b_attn_merge, :403-424)
 //   qkv_kernel         the QKV projection with the append in its epilogue
@@ -2001,6 +2003,57 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch
     }
 }
 
+// The new rows app0 .. app0+napp-1 of one (layer, head) appended by a whole
+// workgroup: item_append's enumeration with U chunks per thread loaded
+// before any is stored, so a prompt's hundreds of rows stream instead of
+// paying a load latency per chunk.  Loads past the end read the last chunk
+// again (in bounds) and are not stored; Q8's D/8-lane groups stay whole.
+#ifndef NI_SEQ_APPEND_UNROLL
+#define NI_SEQ_APPEND_UNROLL 4
+#endif
+template <int D, bool Q8, int U>
+__device__ __forceinline__ void seq_append(const AttnLaunch& a, const uint8_t* plan, uint32_t app0, uint32_t napp,
+                                           uint32_t lay, uint32_t head, uint64_t layer_off, uint32_t nthreads) {
+    constexpr uint32_t CH = D / 8;
+    const uint32_t n = napp * 2 * CH;
+    const AppendEntry* ent = reinterpret_cast<const AppendEntry*>(plan + a.off_app) + app0;
+    for (uint32_t t0 = threadIdx.x; t0 < n; t0 += nthreads * U) {
+        qkv_f4 x[U][2];
+        AppendEntry e[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t t = min(t0 + u * nthreads, n - 1);
+            const uint32_t row = t / (2 * CH);
+            const uint32_t rem2 = t - row * (2 * CH);
+            const uint32_t is_v = rem2 >= CH;
+            const uint32_t c = (rem2 - is_v * CH) * 8;
+            e[u] = ent[row];
+            const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride +
+                               (int64_t)e[u].src_row * a.kv_row_stride + head * D + c;
+            x[u][0] = reinterpret_cast<const qkv_f4*>(src)[0];
+            x[u][1] = reinterpret_cast<const qkv_f4*>(src)[1];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t t = t0 + u * nthreads;
+            if (t >= n) break;
+            const uint32_t row = t / (2 * CH);
+            const uint32_t rem2 = t - row * (2 * CH);
+            const uint32_t is_v = rem2 >= CH;
+            const uint32_t c = (rem2 - is_v * CH) * 8;
+            const float4 x0 = make_float4(x[u][0].x, x[u][0].y, x[u][0].z, x[u][0].w);
+            const float4 x1 = make_float4(x[u][1].x, x[u][1].y, x[u][1].z, x[u][1].w);
+            const uint64_t pg = layer_off + (uint64_t)e[u].page * a.pool.page_halves;
+            if constexpr (Q8) {
+                q8_store8(q8_block(a.pool, is_v, pg), D, e[u].slot, c, x0, x1);
+            } else {
+                uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + pg + e[u].slot * D + c;
+                *reinterpret_cast<uint4*>(dst) = pack8(x0, x1);
+            }
+        }
+    }
+}
+
 template <int D, int PT, int INL, bool Q8>
 __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_prefill_kernel(const AttnLaunch a,
                                                                                              const PlanArg<INL> pa) {
@@ -2023,11 +2076,28 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     const uint32_t H = a.pool.n_head;
     const uint32_t lh = a.n_lay * H;
     const uint8_t* plan = plan_base(pa, a.plan);
-    const uint32_t item_i = blockIdx.x / lh;
-    const uint32_t rem = blockIdx.x - item_i * lh;
+    const uint32_t unit = blockIdx.x / lh;
+    const uint32_t rem = blockIdx.x - unit * lh;
     const uint32_t lay = rem / H;
     const uint32_t head = rem - lay * H;
+    // One item per workgroup, or (a.n_pseqs) the items of one sequence of a
+    // prompt-chunk step in turn, each appending its new rows for this (layer,
+    // head) first -- no other workgroup reads or writes those blocks, and the
+    // vector L1 starts the kernel clean, so after the barrier the tiles'
+    // loads see the stores.
+    uint32_t item0 = unit, n_items = 1;
+    if (a.n_pseqs) {
+        const PrefillSeq ps = reinterpret_cast<const PrefillSeq*>(plan + a.off_pseqs)[unit];
+        item0 = ps.item0;
+        n_items = ps.n_items;
+    }
+    for (uint32_t item_i = item0; item_i < item0 + n_items; item_i++) {
     const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
+    if (a.n_pseqs && it.napp) {  // rows past the previous item's keys: no wave still reads them
+        const uint64_t loff = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
+        seq_append<D, Q8, NI_SEQ_APPEND_UNROLL>(a, plan, it.app0, it.napp, lay, head, loff, 256);
+    }
+    if (item_i != item0 || (a.n_pseqs && it.napp)) __syncthreads();  // ring free again; the rows stored
     const int col = lane & 15;  // query slot of S^T / O^T columns
     const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
 
@@ -2349,7 +2419,7 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     }
     // Lanes q, q+16, q+32, q+48 hold partial sums of query q's softmax.
     lsum = rows4_sum(lsum);
-    if (!qok) return;
+    if (qok) {
     const uint32_t row = it.row0 + r0 + col;
     if (it.part_slot == kNoSlot) {
         float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)row * a.out_row_stride + head * D;
@@ -2374,6 +2444,8 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
 #pragma unroll
             for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j]) * (kPUnscalePre * vref);
     }
+    }  // qok
+    }  // items
 }
 
 // One workgroup per (merge item, layer, head).  Thread t owns output unit
@@ -2552,7 +2624,7 @@ hipError_t mfma_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
 
 template <int D>
 hipError_t prefill_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
-    const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head;
+    const uint64_t blocks = (uint64_t)(a.n_pseqs ? a.n_pseqs : a.n_items) * a.n_lay * a.pool.n_head;
     if (blocks == 0) return hipSuccess;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;

@@ -71,6 +71,15 @@ struct AttnItem {
     uint32_t pad;
 };
 
+// A sequence of a prompt-chunk step run by one prefill workgroup per (layer,
+// head): its prefill items item0 .. item0 + n_items - 1 in turn, each first
+// appending, for the workgroup's head, the item's new rows (append entries
+// app0 .. app0 + napp - 1 of the item).
+struct PrefillSeq {
+    uint32_t item0;
+    uint32_t n_items;
+};
+
 // A group split into n_parts partitions, merged by log-sum-exp.
 struct MergeItem {
     uint32_t row0;
@@ -194,6 +203,8 @@ struct AttnLaunch {
     uint32_t nq_tile;         // query tile: 1..8 (vector kernel), kMfmaTile (matrix cores) or kPrefillRows
     float qscale;             // log2(e) / sqrt(head_dim)
     uint32_t wide;            // 1: kWideWaves waves per workgroup (single-row items, head_dim 64)
+    uint32_t off_pseqs;       // prefill launch: PrefillSeq[n_pseqs]; 0 sequences: one workgroup per item
+    uint32_t n_pseqs;
 };
 
 // A plan travels to the device either inside the kernel arguments (up to

@@ -284,3 +284,26 @@ def test_q8_refusals(gpu):
     with pytest.raises(na.KvError, match="not a Q8 cache"):
         f16.gather_q8([(t, 0)])
     assert kv.kv_block_bytes() * 2 < f16.kv_block_bytes() * 1.1
+
+
+def test_q8_prompt_chunk_steps(gpu, oracle_lib):
+    """A Q8 step of prompt chunks only, every sequence queried at more than
+    16 rows: the prefill launch quantises and appends each sequence's rows
+    before its groups read them; int8 values and scales bit for bit."""
+    rng = np.random.default_rng(95)
+    m = MirrorQ8(opts(workloads.GPT2, n_layer=2, max_rows=1100))
+    a, b, c = (m.kv.add_seq() for _ in range(3))
+    m.fill(b, 90, rng)
+    work = [(a, 512, 512), (b, 200, 100), (c, 50, 20)]
+    rows, qrows = step_rows(m.kv, work)
+    q, k, v = (rng.standard_normal((2, len(rows), m.c)).astype(np.float32) for _ in range(3))
+    m.kv.profile([0])
+    got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v)), split_tokens=1024).cpu().numpy()
+    _, n_app = m.kv.profile_read(0)
+    m.kv.profile([])
+    assert n_app == 0
+    m.append_oracle(rows, k, v)
+    want = m.attention_oracle(rows[qrows], q[:, qrows])
+    err = assert_close(got[:, qrows], want, "q8 prompt chunks")
+    m.check_bytes(rows)
+    say(f"q8 prompt chunks: max abs err {err:.2e}")
