@@ -446,6 +446,7 @@ def run_config3(args):
                      algorithmic_bytes_per_step=int(r["bytes"] / r["steps"])),
                 "synthetic (seeded N(0,1) q/k/v resident in HBM, seeded Poisson request trace)")
     res["repetitions"] = spread
+    res["host_idle_us"] = {"ni_kv_step": round(r["idle_us_plan_call"], 2)}  # per call, device idle
     res["copy_ceiling"] = copy_ceiling()
     res["stream_ceiling"] = stream_ceiling()
     try:
@@ -482,6 +483,11 @@ def run_config3(args):
                         "ms_per_step": round(rl["seconds"] / rl["steps"] * 1e3, 5),
                         "host_us_per_step": round(rl["host_us_per_step"], 1),
                         "abi_calls_per_step": round(rl["launches"] / rl["steps"], 1), "repetitions": sp}
+            if mode == drivers.NI_DRIVE_STEP_LAYERS:
+                # host_us_per_step above is paced by the device's queue; the
+                # calls' own cost with the device idle:
+                res[key]["host_idle_us"] = {"ni_kv_step_begin": round(rl["idle_us_plan_call"], 2),
+                                            "ni_kv_step_layer": round(rl["idle_us_layer_call"], 2)}
     if not args.skip_secondary:
         res["secondary"] = secondary_lines(args)
     if args.cpu_seconds > 0:

@@ -344,6 +344,10 @@ struct Runner {
     int64_t ls;  // layer stride of the q/k/v/out buffers (floats)
     std::vector<ni_row> rows, qrows;
     uint64_t calls = 0;
+    // Host seconds inside the planning calls (ni_kv_step, ni_kv_step_begin)
+    // and the per-layer calls (ni_kv_step_layer), and their counts.
+    double plan_s = 0, layer_s = 0;
+    uint64_t plan_n = 0, layer_n = 0;
 
     double kvb;  // stored bytes of one position's K (or V) in one layer
 
@@ -413,23 +417,34 @@ struct Runner {
     // a ramp iteration).
     int launch(const ni_work* w, uint32_t n, bool ramp = false) {
         if (ramp) return append_only(w, n);
+        using clk = std::chrono::steady_clock;
+        auto since = [](clk::time_point t) { return std::chrono::duration<double>(clk::now() - t).count(); };
         if (o.launch == NI_DRIVE_STEP) {
             calls++;
+            const auto t0 = clk::now();
             if (int rc = ni_kv_step(kv, w, n, d.q, d.k, d.v, C, ls, d.out, C, ls, o.split_tokens, stream))
                 return kv_fail(rc, "ni_kv_step");
+            plan_s += since(t0);
+            plan_n++;
             return NI_OK;
         }
         if (o.launch == NI_DRIVE_STEP_LAYERS) {
             // The step planned once, then one append + attention launch per
             // layer, as a model's forward would call it between layers.
+            const auto t0 = clk::now();
             if (int rc = ni_kv_step_begin(kv, w, n, o.split_tokens)) return kv_fail(rc, "ni_kv_step_begin");
+            plan_s += since(t0);
+            plan_n++;
             for (uint32_t l = 0; l < L; l++) {
                 calls++;
+                const auto t1 = clk::now();
                 if (int rc = ni_kv_step_layer(kv, (int32_t)l, d.q + l * ls, d.k + l * ls, d.v + l * ls, C,
                                               d.out + l * ls, C, stream)) {
                     (void)ni_kv_step_end(kv);
                     return kv_fail(rc, "ni_kv_step_layer");
                 }
+                layer_s += since(t1);
+                layer_n++;
             }
             if (int rc = ni_kv_step_end(kv)) return kv_fail(rc, "ni_kv_step_end");
             return NI_OK;
@@ -512,6 +527,19 @@ int timed_run(Runner& r, ni_drive_result* res, Fn&& iterate) {
                 return r.kv_fail(rc, "ni_kv_profile_read");
         ni_kv_profile(r.kv, 0);
     }
+    // The host cost of the calls themselves: a few more iterations, each
+    // after the stream has drained, so no call waits for room in the
+    // device's queue (in the timed loop the host runs ahead until it does).
+    r.plan_s = r.layer_s = 0;
+    r.plan_n = r.layer_n = 0;
+    const uint32_t n_idle = std::min<uint32_t>(r.o.steps, 20);
+    for (uint32_t i = 0; i < n_idle; i++) {
+        if (hipStreamSynchronize(r.stream) != hipSuccess) return drive_fail(NI_ERR_HIP, "hipStreamSynchronize failed");
+        if (int rc = iterate(WARMUP)) return rc;
+    }
+    if (hipStreamSynchronize(r.stream) != hipSuccess) return drive_fail(NI_ERR_HIP, "hipStreamSynchronize failed");
+    res->idle_us_plan_call = r.plan_n ? r.plan_s / r.plan_n * 1e6 : 0;
+    res->idle_us_layer_call = r.layer_n ? r.layer_s / r.layer_n * 1e6 : 0;
     return NI_OK;
 }
 

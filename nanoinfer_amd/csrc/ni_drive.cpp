@@ -129,9 +129,10 @@ int main(int argc, char** argv) {
            "\"value\": %.2f, \"unit\": \"GB/s\", \"pct_of_peak\": %.2f, \"ms_per_step\": %.5f, "
            "\"gpu_ms_per_step\": %.5f, \"host_us_per_step\": %.1f, \"abi_calls_per_step\": %.1f, "
            "\"seq_tokens_per_s\": %.1f, \"algorithmic_bytes_per_step\": %.0f, \"mean_live\": %.2f, "
-           "\"mean_context\": %.1f, \"kv\": \"%s\"}\n",
+           "\"mean_context\": %.1f, \"kv\": \"%s\", \"idle_us_plan_call\": %.2f, \"idle_us_layer_call\": %.2f}\n",
            workload.c_str(), o.launch == NI_DRIVE_STEP ? "step" : o.launch == NI_DRIVE_PER_LAYER ? "per-layer" : "step-layers", r.steps, o.ramp, o.warmup, gbs,
            100.0 * gbs / 8000.0, r.seconds / r.steps * 1e3, r.gpu_seconds / r.steps * 1e3, r.host_us_per_step,
-           (double)r.launches / r.steps, r.seq_tokens / r.seconds, r.bytes / r.steps, r.mean_live, r.mean_context, q8 ? "q8" : "f16");
+           (double)r.launches / r.steps, r.seq_tokens / r.seconds, r.bytes / r.steps, r.mean_live, r.mean_context, q8 ? "q8" : "f16",
+           r.idle_us_plan_call, r.idle_us_layer_call);
     return 0;
 }

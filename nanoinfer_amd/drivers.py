@@ -47,7 +47,8 @@ class ni_drive_result(C.Structure):
                 ("seq_tokens", C.c_double), ("host_us_per_step", C.c_double), ("steps", _u32),
                 ("launches", C.c_uint64), ("mean_live", C.c_double), ("mean_context", C.c_double),
                 ("flops", C.c_double),
-                ("kernel_ms", C.c_double * _abi.NI_K_COUNT), ("kernel_launches", C.c_uint64 * _abi.NI_K_COUNT)]
+                ("kernel_ms", C.c_double * _abi.NI_K_COUNT), ("kernel_launches", C.c_uint64 * _abi.NI_K_COUNT),
+                ("idle_us_plan_call", C.c_double), ("idle_us_layer_call", C.c_double)]
 
 
 NI_DRIVE_SERVE, NI_DRIVE_SPEC, NI_DRIVE_FIXED, NI_DRIVE_QKV = 0, 1, 2, 3
