@@ -1172,6 +1172,21 @@ __device__ __forceinline__ void qkv_store(const QkvLaunch& a, const AppendEntry*
     }
 }
 
+// qkv_store with the row's append entry already in hand.
+__device__ __forceinline__ void qkv_store_en(const QkvLaunch& a, const AppendEntry& en, uint32_t row, uint32_t f,
+                                             float y) {
+    const uint32_t C = a.n_feat / 3, D = a.pool.head_dim;
+    if (!a.fused || f < C) {
+        a.out[(int64_t)row * a.out_row_stride + f] = y;
+    } else {
+        const uint32_t is_v = f >= 2 * C;
+        const uint32_t c = f - C - is_v * C, head = c / D, d = c - head * D;
+        uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + (uint64_t)a.layer * a.pool.layer_halves +
+                        (uint64_t)en.page * a.pool.page_halves + (uint64_t)head * a.pool.head_halves + en.slot * D + d;
+        *dst = (uint16_t)f16_bits(y);
+    }
+}
+
 template <int FB, int INL, int WF>
 __global__ __launch_bounds__(256) void qkv_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
     typedef float f4 __attribute__((ext_vector_type(4)));
@@ -1302,6 +1317,24 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_small_kernel(const QkvLaun
     for (int rb = 0; rb < RB; rb++)  // rows past n_rows repeat the last row (their results are dropped)
         xr[rb] = a.x + (int64_t)min(m0 + 16 * rb + i, a.n_rows - 1) * a.x_row_stride + 4 * g;
 
+    // What wave p < RB stores at the end (rows m0 + 16p + 4g .. +3, feature
+    // n0 + i): the rows' pages and slots and the bias, loaded with the
+    // operands instead of after the sum.
+    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
+    AppendEntry en[4] = {};
+    float bias = 0.f;
+    if (p < (uint32_t)RB) {
+        if (a.fused && n0 >= a.n_feat / 3) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const AppendEntry& r = entries[min(m0 + 16 * p + 4 * g + e, a.n_rows - 1)];
+                en[e].page = r.page;
+                en[e].slot = r.slot;
+            }
+        }
+        if (a.bias) bias = a.bias[n0 + i];
+    }
+
     f4 acc[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) acc[rb] = f4{0.f, 0.f, 0.f, 0.f};
@@ -1337,14 +1370,12 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_small_kernel(const QkvLaun
     const int rb = (int)p;
     const f4 y = ((red[0][rb][lane] + red[1][rb][lane]) + (red[2][rb][lane] + red[3][rb][lane])) +
                  ((red[4][rb][lane] + red[5][rb][lane]) + (red[6][rb][lane] + red[7][rb][lane]));
-    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
     const uint32_t f = n0 + i;
-    const float b = a.bias ? a.bias[f] : 0.f;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const uint32_t row = m0 + 16 * rb + 4 * g + e;
         if (row >= a.n_rows) break;
-        qkv_store(a, entries, row, f, y[e] + b);
+        qkv_store_en(a, en[e], row, f, y[e] + bias);
     }
 }
 
@@ -1902,8 +1933,8 @@ __device__ __forceinline__ void wait_tiles(uint32_t ahead) {
 // by every feature tile, and those half-line reads cost ~4 us per layer more
 // than whole-line ones at 64 rows (measured).  Here every thread issues all
 // its loads of the tile at once, whole lines (wave p: rows 2p and 2p+1 of x
-// and of W, 512 contiguous bytes each per chunk of 128 values of d_in), up to
-// kQkvMidChunks chunks (d_in <= 1024) in registers; then chunk by chunk the tile goes
+// and of W, 512 contiguous bytes each per chunk of 128 values of d_in), NC
+// chunks in registers (6 up to d_in 768, else 8: d_in <= 1024); then chunk by chunk the tile goes
 // through a double-buffered LDS chunk (one barrier per chunk) into the
 // matrix-core layout.  Row r's 16-byte piece q sits in slot q ^ (r & 15) of
 // its 512-byte LDS row, so the 16 lanes reading piece q of 16 rows hit
@@ -1917,13 +1948,13 @@ __device__ __forceinline__ void wait_tiles(uint32_t ahead) {
 #endif
 constexpr int kQkvMidChunks = 8;  // chunks of d_in held in registers: d_in up to 1024 on this kernel
 
-template <int INL, int WF>
+template <int INL, int WF, int NC>
 __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch a, const PlanArg<INL> pa) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int KC = kQkvChunk;       // d_in values per chunk (8 slices of 16)
     constexpr uint32_t RB = KC * 4;     // bytes of one row's chunk (512)
     constexpr uint32_t CB = 16 * RB;    // bytes of 16 rows' chunk (8 KB)
-    constexpr int NC = kQkvMidChunks;
+    static_assert(NC <= kQkvMidChunks, "chunks held in registers");
     static_assert(KC == 128 && kQkvParts == 8, "two rows of 32 pieces per wave and chunk, 8 waves");
     __shared__ __attribute__((aligned(16))) uint8_t buf[2][2 * CB];  // [x rows | W rows], double-buffered
     const int lane = threadIdx.x & 63;
@@ -1964,6 +1995,23 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch
         xr[j] = *reinterpret_cast<const f4*>(xsrc + col);
         wr[j] = qkv_w4<WF>(a, n0 + dr, col);
     }
+    // What the store at the end needs (wave 0: rows m0 + 4g .. +3, feature
+    // n0 + i): the rows' append entries and the bias, loaded with the
+    // operands instead of after the sum.
+    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
+    AppendEntry en[4] = {};
+    float bias = 0.f;
+    if (p == 0) {
+        if (a.fused && n0 >= a.n_feat / 3) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const AppendEntry& r = entries[min(m0 + 4 * g + e, a.n_rows - 1)];
+                en[e].page = r.page;  // (the store needs page and slot only)
+                en[e].slot = r.slot;
+            }
+        }
+        if (a.bias) bias = a.bias[n0 + i];
+    }
     f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma clang loop unroll(full)
     for (int j = 0; j < NC; j++) {
@@ -1992,14 +2040,12 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch
     // The same tree as qkv_kernel and qkv_small_kernel.
     const f4 y = ((red[0 * 64 + lane] + red[1 * 64 + lane]) + (red[2 * 64 + lane] + red[3 * 64 + lane])) +
                  ((red[4 * 64 + lane] + red[5 * 64 + lane]) + (red[6 * 64 + lane] + red[7 * 64 + lane]));
-    const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
     const uint32_t f = n0 + i;
-    const float b = a.bias ? a.bias[f] : 0.f;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const uint32_t row = m0 + 4 * g + e;
         if (row >= a.n_rows) break;
-        qkv_store(a, entries, row, f, y[e] + b);
+        qkv_store_en(a, en[e], row, f, y[e] + bias);
     }
 }
 
@@ -2762,8 +2808,13 @@ hipError_t launch_qkv_t(const QkvLaunch& a, const void* ip, uint32_t ib, hipStre
         const dim3 grid((a.n_rows + 15) / 16 * (a.n_feat / 16));  // (row tile, feature tile), dealt by XCD
         return with_plan(a, ip, ib, [&](auto pa) {
             constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-            hipExtLaunchKernelGGL(qkv_mid_kernel<INL, WF>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop, 0, a,
-                                  pa);
+            // Registers for as many chunks as d_in has: 6 up to 768 (GPT-2), else 8.
+            if (a.d_in <= 6u * kQkvChunk)
+                hipExtLaunchKernelGGL(qkv_mid_kernel<INL, WF, 6>, grid, dim3(64 * kQkvParts), 0, s, t.start, t.stop,
+                                      0, a, pa);
+            else
+                hipExtLaunchKernelGGL(qkv_mid_kernel<INL, WF, kQkvMidChunks>, grid, dim3(64 * kQkvParts), 0, s,
+                                      t.start, t.stop, 0, a, pa);
             return hipGetLastError();
         });
     }

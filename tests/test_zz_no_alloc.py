@@ -74,7 +74,10 @@ def test_noalloc_equals_step_on_two_calls(gpu):
     work1 = [(0, 1, 1), (1, 1, 1), (2, 5, 5), (3, 40, 1), (4, 24, 24), (5, 1, 1), (6, 1, 1), (7, 3, 0)]
     # Call 2: fewer, smaller rows, another partition size.
     work2 = [(1, 1, 1), (6, 2, 2), (4, 1, 1)]
-    for i, (work, split) in enumerate(((work1, 64), (work2, 128))):
+    # Call 3: prompt chunks only, every sequence queried at more than 16 rows
+    # and no partitions: the prefill launch appends the rows itself.
+    work3 = [(4, 40, 40), (7, 30, 20)]
+    for i, (work, split) in enumerate(((work1, 64), (work2, 128), (work3, 1024))):
         n = sum(w[1] for w in work)
         q, k, v = (torch.randn((L, n, C_), device="cuda", generator=g) for _ in range(3))
         out_a = torch.full((L, n, C_), float("nan"), device="cuda")
