@@ -120,6 +120,7 @@ __device__ __forceinline__ const uint8_t* plan_base(const PlanArg<N>& pa, const 
 // One thread's share of an append: 8 elements (two float4 loads, one 16-byte
 // store) of K or V of one row of one layer.  `gid` enumerates
 // [layer][row][K then V][C/8] over the n_rows entries.
+template <bool IDX_SRC = false>
 __device__ __forceinline__ void append_chunk(const PoolGeom& pool, const float* k, const float* v, int64_t row_stride,
                                              int64_t layer_stride, const AppendEntry* entries, uint32_t n_rows,
                                              uint32_t layer0, uint32_t n_lay, uint32_t gid) {
@@ -135,7 +136,10 @@ __device__ __forceinline__ void append_chunk(const PoolGeom& pool, const float* 
     const uint32_t is_v = r >= chunks;
     const uint32_t c8 = (r - is_v * chunks) * 8;
     const AppendEntry e = entries[row];
-    const float* src = (is_v ? v : k) + (int64_t)lay * layer_stride + (int64_t)e.src_row * row_stride + c8;
+    // IDX_SRC: entry i reads input row i (a step's own append list), so the
+    // input load need not wait for the entry's.
+    const float* src =
+        (is_v ? v : k) + (int64_t)lay * layer_stride + (int64_t)(IDX_SRC ? row : e.src_row) * row_stride + c8;
     const float4 x0 = reinterpret_cast<const float4*>(src)[0];
     const float4 x1 = reinterpret_cast<const float4*>(src)[1];
     const uint32_t head = c8 / D, d0 = c8 - head * D;
@@ -181,6 +185,7 @@ __device__ __forceinline__ void q8_store8(uint8_t* blk, uint32_t D, uint32_t slo
 // append_chunk for a Q8 pool: the same enumeration; the D/8 lanes of one
 // (layer, row, K|V, head) are consecutive and aligned, and whole groups
 // leave together at the end of the grid.
+template <bool IDX_SRC = false>
 __device__ __forceinline__ void append_chunk_q8(const PoolGeom& pool, const float* k, const float* v, int64_t row_stride,
                                                 int64_t layer_stride, const AppendEntry* entries, uint32_t n_rows,
                                                 uint32_t layer0, uint32_t n_lay, uint32_t gid) {
@@ -196,7 +201,10 @@ __device__ __forceinline__ void append_chunk_q8(const PoolGeom& pool, const floa
     const uint32_t is_v = r >= chunks;
     const uint32_t c8 = (r - is_v * chunks) * 8;
     const AppendEntry e = entries[row];
-    const float* src = (is_v ? v : k) + (int64_t)lay * layer_stride + (int64_t)e.src_row * row_stride + c8;
+    // IDX_SRC: entry i reads input row i (a step's own append list), so the
+    // input load need not wait for the entry's.
+    const float* src =
+        (is_v ? v : k) + (int64_t)lay * layer_stride + (int64_t)(IDX_SRC ? row : e.src_row) * row_stride + c8;
     const float4 x0 = reinterpret_cast<const float4*>(src)[0];
     const float4 x1 = reinterpret_cast<const float4*>(src)[1];
     const uint32_t head = c8 / D, d0 = c8 - head * D;
@@ -209,10 +217,10 @@ template <int INL>
 __global__ __launch_bounds__(256) void kv_append_kernel(const AppendLaunch a, const PlanArg<INL> pa) {
     const AppendEntry* entries = reinterpret_cast<const AppendEntry*>(plan_base(pa, a.plan) + a.off_entries);
     if (a.pool.q8)
-        append_chunk_q8(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
-                        blockIdx.x * 256u + threadIdx.x);
+        append_chunk_q8<true>(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
+                              blockIdx.x * 256u + threadIdx.x);
     else
-        append_chunk(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
+        append_chunk<true>(a.pool, a.k, a.v, a.row_stride, a.layer_stride, entries, a.n_rows, a.layer0, a.n_lay,
                      blockIdx.x * 256u + threadIdx.x);
 }
 

@@ -47,7 +47,7 @@ constexpr uint32_t kMaxGroupRows = NI_ATTN_MFMA ? kMfmaTile : 8;  // most query 
 
 // Where one appended row goes: pool page `page`, position `slot` (0..15) in it.
 struct AppendEntry {
-    uint32_t src_row;  // row index in the k/v input
+    uint32_t src_row;  // row index in the k/v input (in a call's own append list, the entry's index)
     uint32_t page;
     uint32_t slot;
     uint32_t pad;
