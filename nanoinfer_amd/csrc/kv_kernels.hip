@@ -371,8 +371,9 @@ __device__ __forceinline__ void item_append(const AttnLaunch& a, const uint8_t* 
         const uint32_t is_v = rem2 >= CH;
         const uint32_t c = (rem2 - is_v * CH) * 8;
         const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan + a.off_app)[it.app0 + row];
-        const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride + (int64_t)e.src_row * a.kv_row_stride +
-                           head * D + c;
+        // (append entry i reads input row i: the load need not wait for e)
+        const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride +
+                           (int64_t)(it.app0 + row) * a.kv_row_stride + head * D + c;
         const float4 x0 = reinterpret_cast<const float4*>(src)[0];
         const float4 x1 = reinterpret_cast<const float4*>(src)[1];
         uint16_t* dst = (is_v ? a.pool.v : a.pool.k) + layer_off + (uint64_t)e.page * page_stride + e.slot * D + c;
@@ -823,8 +824,9 @@ __device__ __forceinline__ void item_append_q8(const AttnLaunch& a, const uint8_
         const uint32_t is_v = rem2 >= CH;
         const uint32_t c = (rem2 - is_v * CH) * 8;
         const AppendEntry e = reinterpret_cast<const AppendEntry*>(plan + a.off_app)[it.app0 + row];
-        const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride + (int64_t)e.src_row * a.kv_row_stride +
-                           head * D + c;
+        // (append entry i reads input row i: the load need not wait for e)
+        const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride +
+                           (int64_t)(it.app0 + row) * a.kv_row_stride + head * D + c;
         const float4 x0 = reinterpret_cast<const float4*>(src)[0];
         const float4 x1 = reinterpret_cast<const float4*>(src)[1];
         q8_store8(q8_block(a.pool, is_v, layer_off + (uint64_t)e.page * page_stride), D, e.slot, c, x0, x1);
@@ -2083,7 +2085,7 @@ __device__ __forceinline__ void seq_append(const AttnLaunch& a, const uint8_t* p
             const uint32_t c = (rem2 - is_v * CH) * 8;
             e[u] = ent[row];
             const float* src = (is_v ? a.v : a.k) + (int64_t)lay * a.kv_layer_stride +
-                               (int64_t)e[u].src_row * a.kv_row_stride + head * D + c;
+                               (int64_t)(app0 + row) * a.kv_row_stride + head * D + c;  // entry i: input row i
             x[u][0] = reinterpret_cast<const qkv_f4*>(src)[0];
             x[u][1] = reinterpret_cast<const qkv_f4*>(src)[1];
         }
