@@ -520,7 +520,7 @@ SECONDARY_LINES = {
     "config5": (200, 20, "attn_mfma_kernel (fused append)"),
     "config3q8": (200, 20, "attn_q8_kernel (fused append), Q8 cache"),
     "prefill": (100, 10, "attn_prefill_kernel (appending the prompt rows itself)"),
-    "qkv64": (200, 20, "qkv_kernel (append in the epilogue)"),
+    "qkv64": (200, 20, "qkv_mid_kernel (append in the epilogue)"),
 }
 
 
