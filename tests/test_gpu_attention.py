@@ -250,41 +250,53 @@ def test_wide_workgroups(gpu, oracle_lib):
     say("wide workgroups: per-layer, all-layer and fused launches within bounds, no merge launches")
 
 
+SEQ_PREFILL_MIN_UNITS = 1536  # kSeqPrefillMinUnits: (sequence, layer, head) units for the appending prefill launch
+
+
 @pytest.mark.parametrize("shape", [dict(n_layer=3, n_head=12, head_dim=64), dict(n_layer=2, n_head=4, head_dim=128)],
                          ids=["hd64", "hd128"])
 @pytest.mark.parametrize("per_layer", [False, True], ids=["all_layers", "per_layer"])
 def test_prompt_chunk_steps(gpu, oracle_lib, shape, per_layer):
     """Steps whose every sequence is queried at more than 16 rows (prompt
-    chunks, the reference's all_logits): the prefill launch appends each
-    sequence's rows itself, a workgroup per (sequence, layer, head) running
-    its groups shortest first, each after the new rows up to its last key.
-    Chunks from empty and after existing context, queried at every row or at
-    the last rows only (the rows before the first query appended by the
-    first group), 17..512 queried rows; no append launch runs; every row
-    gathered bit for bit; then a step with a decode row mixed in and
-    automatic partitions (append launch again)."""
+    chunks, the reference's all_logits).  With at least 1536 (sequence,
+    layer, head) units the prefill launch appends each sequence's rows
+    itself, a workgroup per unit running the sequence's groups shortest
+    first, each after the new rows up to its last key, and no append launch
+    runs; with fewer (one layer per launch, or head_dim 128's 8 heads x
+    layers) an append launch runs first and every group has its own
+    workgroup.  Chunks from empty and after existing context, queried at
+    every row or at the last rows only (the rows before the first query
+    appended by the first group), 17..512 queried rows, plus 39 short
+    prompts of 17..24 rows; every row gathered bit for bit; then a step with
+    a decode row mixed in and automatic partitions."""
     rng = np.random.default_rng(33)
-    m = Mirror(opts(shape, kv_blocks=400, n_ctx=1024, max_rows=1100))
+    n_fill = 39
+    m = Mirror(opts(shape, kv_blocks=600, n_ctx=1024, max_rows=2048, max_seqs=4 + n_fill))
     a, b, c, d = (m.kv.add_seq() for _ in range(4))
+    fill = [m.kv.add_seq() for _ in range(n_fill)]
     m.fill(b, 100, rng)
     m.fill(d, 40, rng)
     L = shape["n_layer"]
     m.kv.profile([0, 1])
-    for work in ([(a, 512, 512), (b, 300, 150), (c, 70, 17), (d, 64, 64)],
-                 [(a, 33, 33), (c, 100, 80)]):
+    for work in ([(a, 512, 512), (b, 300, 150), (c, 70, 17), (d, 64, 64)] +
+                 [(s, 17 + i % 8, 17 + i % 8) for i, s in enumerate(fill)],
+                 [(a, 33, 33), (b, 20, 17), (c, 100, 80), (d, 20, 17)] + [(s, 20, 17) for s in fill]):
         srows, _ = step_rows(m.kv, work)
         q, k, v = (rng.standard_normal((L, len(srows), m.c)).astype(np.float32) for _ in range(3))
         # 1024-token partitions: no group is split (a small step's automatic
         # choice would split them to fill the GPU, and split groups keep the
         # append launch)
         got, want, qr = mirror_step(m, work, q, k, v, split_tokens=1024, per_layer=per_layer)
-        err = assert_close(got[:, qr], want[:, qr], f"{work}")
+        err = assert_close(got[:, qr], want[:, qr], f"{len(work)} sequences")
         (kg, vg), (kw, vw) = m.gather(srows)
         assert np.array_equal(kg, kw) and np.array_equal(vg, vw)
         _, n_app = m.kv.profile_read(0)
         _, n_attn = m.kv.profile_read(1)
-        assert n_app == 0 and n_attn == (L if per_layer else 1), (n_app, n_attn)
-        say(f"{shape} per_layer {per_layer} {work}: max abs err {err:.2e}")
+        launches = L if per_layer else 1
+        fused = len(work) * (1 if per_layer else L) * shape["n_head"] >= SEQ_PREFILL_MIN_UNITS
+        assert n_attn == launches and n_app == (0 if fused else launches), (n_app, n_attn, fused)
+        say(f"{shape} per_layer {per_layer} {len(work)} sequences (append in the prefill launch: {fused}): "
+            f"max abs err {err:.2e}")
     work = [(a, 1, 1), (c, 40, 40)]
     srows, _ = step_rows(m.kv, work)
     q, k, v = (rng.standard_normal((L, len(srows), m.c)).astype(np.float32) for _ in range(3))

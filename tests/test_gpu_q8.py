@@ -288,13 +288,17 @@ def test_q8_refusals(gpu):
 
 def test_q8_prompt_chunk_steps(gpu, oracle_lib):
     """A Q8 step of prompt chunks only, every sequence queried at more than
-    16 rows: the prefill launch quantises and appends each sequence's rows
-    before its groups read them; int8 values and scales bit for bit."""
+    16 rows, over at least 1536 (sequence, layer, head) units: the prefill
+    launch quantises and appends each sequence's rows before its groups read
+    them (no append launch); int8 values and scales bit for bit."""
     rng = np.random.default_rng(95)
-    m = MirrorQ8(opts(workloads.GPT2, n_layer=2, max_rows=1100))
+    n_fill = 61
+    m = MirrorQ8(opts(workloads.GPT2, n_layer=2, max_rows=2100, kv_blocks=600, max_seqs=3 + n_fill))
     a, b, c = (m.kv.add_seq() for _ in range(3))
+    fill = [m.kv.add_seq() for _ in range(n_fill)]
     m.fill(b, 90, rng)
-    work = [(a, 512, 512), (b, 200, 100), (c, 50, 20)]
+    work = [(a, 512, 512), (b, 200, 100), (c, 50, 20)] + [(s, 17 + i % 9, 17 + i % 9) for i, s in enumerate(fill)]
+    assert len(work) * 2 * 12 >= 1536
     rows, qrows = step_rows(m.kv, work)
     q, k, v = (rng.standard_normal((2, len(rows), m.c)).astype(np.float32) for _ in range(3))
     m.kv.profile([0])
