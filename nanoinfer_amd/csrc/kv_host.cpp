@@ -1505,7 +1505,8 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
     // workgroup per sequence, layer and head), no append launch.
     bool every_big = n_work > 0;
     for (uint32_t w = 0; w < n_work; w++) every_big &= work[w].n_query > max_group_rows(kv);
-    kv->plan.seq_prefill = NI_PREFILL_SEQ_APPEND && prefill && !fused && every_big;
+    kv->plan.seq_prefill =
+        NI_PREFILL_SEQ_APPEND && prefill && !fused && every_big && (is_q8(kv->o) || NI_PREFILL_SEQ_F16);
     uint32_t row = 0;
     for (uint32_t w = 0; w < n_work; w++) {
         const ni_work& it = work[w];

@@ -2110,7 +2110,7 @@ __device__ __forceinline__ void seq_append(const AttnLaunch& a, const uint8_t* p
     }
 }
 
-template <int D, int PT, int INL, bool Q8>
+template <int D, int PT, int INL, bool Q8, bool SEQ>
 __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_prefill_kernel(const AttnLaunch a,
                                                                                              const PlanArg<INL> pa) {
     constexpr int QC = D / 32;              // 32-dim chunks of the QK product
@@ -2141,19 +2141,23 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
     // head) first -- no other workgroup reads or writes those blocks, and the
     // vector L1 starts the kernel clean, so after the barrier the tiles'
     // loads see the stores.
+    // (SEQ: the launch has a.n_pseqs sequences; otherwise one item per unit.)
     uint32_t item0 = unit, n_items = 1;
-    if (a.n_pseqs) {
+    if constexpr (SEQ) {
         const PrefillSeq ps = reinterpret_cast<const PrefillSeq*>(plan + a.off_pseqs)[unit];
         item0 = ps.item0;
         n_items = ps.n_items;
     }
     for (uint32_t item_i = item0; item_i < item0 + n_items; item_i++) {
     const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
-    if (a.n_pseqs && it.napp) {  // rows past the previous item's keys: no wave still reads them
-        const uint64_t loff = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
-        seq_append<D, Q8, NI_SEQ_APPEND_UNROLL>(a, plan, it.app0, it.napp, lay, head, loff, 256);
+    if constexpr (SEQ) {
+        if (it.napp) {  // rows past the previous item's keys: no wave still reads them
+            const uint64_t loff =
+                (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
+            seq_append<D, Q8, NI_SEQ_APPEND_UNROLL>(a, plan, it.app0, it.napp, lay, head, loff, 256);
+        }
+        if (item_i != item0 || it.napp) __syncthreads();  // ring free again; the rows stored
     }
-    if (item_i != item0 || (a.n_pseqs && it.napp)) __syncthreads();  // ring free again; the rows stored
     const int col = lane & 15;  // query slot of S^T / O^T columns
     const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
 
@@ -2686,10 +2690,19 @@ hipError_t prefill_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hi
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         // head_dim 128 stages one page per tile (two spill registers).
         constexpr int PT = D == 128 ? 1 : kPrefillPages;
-        if constexpr (D == 64 && PT == 2)
-            if (a.pool.q8) return go(attn_prefill_kernel<D, PT, INL, true>, blocks, 256, s, t, a, pa);
+        const bool seq = a.n_pseqs != 0;
+        if constexpr (D == 64 && PT == 2) {
+            if (a.pool.q8)
+                return seq ? go(attn_prefill_kernel<D, PT, INL, true, true>, blocks, 256, s, t, a, pa)
+                           : go(attn_prefill_kernel<D, PT, INL, true, false>, blocks, 256, s, t, a, pa);
+        }
         if (a.pool.q8) return hipErrorInvalidValue;
-        return go(attn_prefill_kernel<D, PT, INL, false>, blocks, 256, s, t, a, pa);
+#if NI_PREFILL_SEQ_F16
+        if (seq) return go(attn_prefill_kernel<D, PT, INL, false, true>, blocks, 256, s, t, a, pa);
+#else
+        if (seq) return hipErrorInvalidValue;  // the host plans sequences on Q8 pools only
+#endif
+        return go(attn_prefill_kernel<D, PT, INL, false, false>, blocks, 256, s, t, a, pa);
     });
 }
 

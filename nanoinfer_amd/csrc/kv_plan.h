@@ -71,6 +71,13 @@ struct AttnItem {
     uint32_t pad;
 };
 
+// Sequences of prompt-chunk steps (PrefillSeq) on f16 pools too, not only
+// Q8 (measured 1% slower on f16: 16 x 512 prompts 470 against 465 us; Q8
+// 511 against 533).
+#ifndef NI_PREFILL_SEQ_F16
+#define NI_PREFILL_SEQ_F16 0
+#endif
+
 // A sequence of a prompt-chunk step run by one prefill workgroup per (layer,
 // head): its prefill items item0 .. item0 + n_items - 1 in turn, each first
 // appending, for the workgroup's head, the item's new rows (append entries

@@ -311,3 +311,15 @@ def test_q8_prompt_chunk_steps(gpu, oracle_lib):
     err = assert_close(got[:, qrows], want, "q8 prompt chunks")
     m.check_bytes(rows)
     say(f"q8 prompt chunks: max abs err {err:.2e}")
+    # Three sequences (72 units): an append launch, then the groups.
+    work = [(a, 40, 40), (b, 30, 20), (c, 18, 18)]
+    rows, qrows = step_rows(m.kv, work)
+    q, k, v = (rng.standard_normal((2, len(rows), m.c)).astype(np.float32) for _ in range(3))
+    m.kv.profile([0])
+    got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v)), split_tokens=1024).cpu().numpy()
+    _, n_app = m.kv.profile_read(0)
+    m.kv.profile([])
+    assert n_app == 1
+    m.append_oracle(rows, k, v)
+    assert_close(got[:, qrows], m.attention_oracle(rows[qrows], q[:, qrows]), "q8 prompt chunks, 3 sequences")
+    m.check_bytes(rows)
