@@ -59,9 +59,9 @@ constexpr uint32_t kRingSlots = 4;
 #define NI_PREFILL_SEQ_ORDER 1
 #endif
 // A step of prompt chunks (every sequence queried as prefill groups, no
-// partitions): the prefill launch appends each sequence's rows (one workgroup
-// per sequence, layer and head, its groups in turn) instead of an append
-// launch before it.
+// partitions) on a Q8 pool (NI_PREFILL_SEQ_F16: f16 too): the prefill launch
+// appends each sequence's rows (one workgroup per sequence, layer and head,
+// its groups in turn) instead of an append launch before it.
 #ifndef NI_PREFILL_SEQ_APPEND
 #define NI_PREFILL_SEQ_APPEND 1
 #endif
@@ -1501,8 +1501,8 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
     if (big) fused = prefill && small;
     kv->plan.fused = fused;
     // A step of prompt chunks whose every sequence is queried as prefill
-    // groups: the prefill launch appends each sequence's rows itself (one
-    // workgroup per sequence, layer and head), no append launch.
+    // groups, on a Q8 pool: the prefill launch appends each sequence's rows
+    // itself (one workgroup per sequence, layer and head), no append launch.
     bool every_big = n_work > 0;
     for (uint32_t w = 0; w < n_work; w++) every_big &= work[w].n_query > max_group_rows(kv);
     kv->plan.seq_prefill =

@@ -18,7 +18,7 @@
 //                      sequence, on the matrix cores
 //   attn_prefill_kernel  groups of 17..64 rows (prompt chunks), K/V tiles DMA'd
 //                      into an LDS ring shared by four waves (attn.metal:100-222);
-//                      in a step of prompt chunks only, a workgroup runs one
+//                      in a Q8 step of prompt chunks only, a workgroup runs one
 //                      sequence's groups, appending the rows each needs first
 //   attn_q8_kernel     single rows on the int8 + scale (Q8) cache (kv8.metal)
 //   attn_merge_kernel  log-sum-exp merge of partitions (b_attn_merge, :403-424)
