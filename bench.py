@@ -519,7 +519,7 @@ SECONDARY_LINES = {
     "config4": (100, 10, "attn_split_kernel + attn_merge_kernel"),
     "config5": (200, 20, "attn_mfma_kernel (fused append)"),
     "config3q8": (200, 20, "attn_q8_kernel (fused append), Q8 cache"),
-    "prefill": (100, 10, "attn_prefill_kernel (appending the prompt rows itself)"),
+    "prefill": (100, 10, "attn_prefill_kernel (after its append launch)"),
     "qkv64": (200, 20, "qkv_mid_kernel (append in the epilogue)"),
 }
 
