@@ -9,6 +9,7 @@ bit-identical -- on two calls in a row, the second smaller (the array keeps
 the first call's contents).  The no-allocation call must not lower the
 device's free memory, and steps beyond its limits (a plan over 32 KB, split
 partials over 32 MiB) are refused with a clear error, launching nothing.
+Captured in a HIP graph, the call replays bit-identically.
 """
 import ctypes as C
 import sys
@@ -144,3 +145,46 @@ def test_noalloc_limits(gpu):
     assert rc == 0, lib.ni_kv_last_error(kv.handle).decode()
     torch.cuda.synchronize()
     assert torch.isfinite(out2).all()
+
+
+def test_noalloc_step_replayed_from_a_graph(gpu):
+    """The callers it is for: ni_kv_step_noalloc captured in a HIP graph
+    (through torch.cuda.graph) and replayed three times, with eager work and
+    gathers between the replays; every replay's outputs and stored K/V equal
+    the eager ni_kv_step of a twin handle."""
+    L, H, D = 12, 12, 64
+    C_ = H * D
+    opts = na.BatchOpts(n_layer=L, n_head=H, head_dim=D, kv_blocks=512, max_seqs=16, n_ctx=1024, max_rows=512)
+    a, b = na.PagedKv(opts), na.PagedKv(opts)
+    g = torch.Generator(device="cuda").manual_seed(73)
+    seqs = list(range(6))
+    fill([a, b], seqs, [1, 17, 100, 300, 511, 64], g, C_)
+    lib = _abi.lib()
+    # decode rows, a 5-row verify group, a chunk without a query (orphan
+    # rows), 64-token partitions (split partials in the library's array)
+    work = [(0, 1, 1), (1, 1, 1), (2, 5, 5), (3, 1, 1), (4, 1, 1), (5, 7, 0)]
+    n = sum(w[1] for w in work)
+    q, k, v = (torch.randn((L, n, C_), device="cuda", generator=g) for _ in range(3))
+    out_a = torch.full((L, n, C_), float("nan"), device="cuda")
+    out_b = torch.full((L, n, C_), float("nan"), device="cuda")
+    rc = call(a, lib.ni_kv_step, work, q, k, v, out_a, 64)
+    assert rc == 0, lib.ni_kv_last_error(a.handle).decode()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    say("graph: capturing ni_kv_step_noalloc")
+    with torch.cuda.graph(graph):
+        rc = call(b, lib.ni_kv_step_noalloc, work, q, k, v, out_b, 64)
+    assert rc == 0, lib.ni_kv_last_error(b.handle).decode()
+    queried = [r for w, r0 in zip(work, np.cumsum([0] + [w[1] for w in work])) for r in
+               range(r0 + w[1] - w[2], r0 + w[1])]
+    qi = torch.tensor(queried, device="cuda")
+    for rep in range(3):
+        say(f"graph: replay {rep + 1}")
+        out_b.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_a[:, qi], out_b[:, qi]), f"replay {rep + 1}"
+        same_state(a, b, seqs)  # eager gathers between the replays
+        x = torch.randn((1024, 1024), device="cuda", generator=g)
+        (x @ x).sum().item()  # unrelated eager work
