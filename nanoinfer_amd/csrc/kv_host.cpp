@@ -586,6 +586,14 @@ int acquire_slot(ni_kv* kv, size_t bytes, StagingSlot** out) {
     return NI_OK;
 }
 
+// The merge launch's workgroups per (merge item, layer, head): the largest
+// merge_split_of over its items (the others' extra workgroups return at once).
+uint32_t merge_split(const std::vector<MergeItem>& merges, uint32_t D) {
+    uint32_t split = 1;
+    for (const MergeItem& m : merges) split = std::max(split, merge_split_of(m.n_parts, m.nq, D));
+    return split;
+}
+
 int ensure_partials(ni_kv* kv, size_t bytes, float** out) {
     if (kv->no_alloc) {
         if (bytes > kScratchBytes)
@@ -758,6 +766,7 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
             if (e != hipSuccess) return kv->hip_fail(e, "attention kernel");
         }
         if (!P.merges.empty()) {
+            a.merge_split = merge_split(P.merges, D);
             ProfileScope ps(kv, NI_K_MERGE);
             hipError_t e = launch_merge(a, ref.inl, ref.inl_bytes, s, ps.t);
             if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
@@ -800,6 +809,7 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
             if (e != hipSuccess) return kv->hip_fail(e, "prefill attention kernel");
         }
         if (!P.pmerges.empty()) {
+            a.merge_split = merge_split(P.pmerges, D);
             ProfileScope ps(kv, NI_K_MERGE);
             hipError_t e = launch_merge(a, ref.inl, ref.inl_bytes, s, ps.t);
             if (e != hipSuccess) return kv->hip_fail(e, "prefill merge kernel");

@@ -2515,8 +2515,7 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
 // loads do not depend on earlier arithmetic, so they stream back to back
 // (batch.metal:403-424 merges the same (m, l, o) partials).  The G states of
 // a unit are combined through LDS.  A partition where a row has no key holds
-// m = kMinScore, l = 0, o = 0 and weighs nothing.
-constexpr int kMergeThreads = 512;
+// m = kMinScore, l = 0, o = 0 and weighs nothing.  (kMergeThreads: kv_plan.h.)
 
 template <int D, int NQ, int INL>
 __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
@@ -2524,20 +2523,28 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnLau
     __shared__ float sm[T], sl[T], so[T];
     const uint32_t H = a.pool.n_head;
     const uint32_t lh = a.n_lay * H;
-    const uint32_t mi = blockIdx.x / lh;
-    const uint32_t rem = blockIdx.x - mi * lh;
+    // merge_split_of(item) workgroups share a (merge item, layer, head) (the
+    // launch has a.merge_split, the largest, per unit; the rest return):
+    // workgroup ms takes units ms*U .. ms*U+U-1 of its nq * D (U = nq * D /
+    // split), so more groups of threads split the partitions.
+    const uint32_t stride = a.merge_split ? a.merge_split : 1;
+    const uint32_t bid = blockIdx.x / stride, ms = blockIdx.x - bid * stride;
+    const uint32_t mi = bid / lh;
+    const uint32_t rem = bid - mi * lh;
     const uint32_t lay = rem / H;
     const uint32_t head = rem - lay * H;
     const MergeItem g = reinterpret_cast<const MergeItem*>(plan_base(pa, a.plan) + a.off_merges)[mi];
+    const uint32_t split = merge_split_of(g.n_parts, g.nq, D);
+    if (ms >= split) return;
     const uint64_t slot_stride = (uint64_t)a.n_lay * H * NQ * (D + 2);
     const float* base = a.partials + (((uint64_t)g.slot0 * a.n_lay + lay) * H + head) * NQ * (D + 2);
-    const uint32_t units = g.nq * D;
+    const uint32_t units = g.nq * D / split, ub = ms * units;
     const uint32_t G = units >= T ? 1u : T / units;
     const uint32_t t = threadIdx.x;
     for (uint32_t u0 = 0; u0 < units; u0 += T) {  // several passes only when G == 1
         const uint32_t j = G > 1 ? t / units : 0u;
-        const uint32_t u = G > 1 ? t - j * units : u0 + t;
-        const bool active = j < G && u < units;
+        const uint32_t u = ub + (G > 1 ? t - j * units : u0 + t);
+        const bool active = j < G && u < ub + units;
         const uint32_t r = u / D, d = u - r * D;
         float m = kMinScore, l = 0.f, o = 0.f;
         if (active) {
@@ -2562,7 +2569,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnLau
         sl[t] = l;
         so[t] = o;
         __syncthreads();
-        if (t < units) {
+        if (t < units) {  // (j = 0: dst is unit ub + t's)
             float M = sm[t];
             for (uint32_t k = 1; k < G; k++) M = fmaxf(M, sm[k * units + t]);
             float L = 0.f, O = 0.f;
@@ -2650,7 +2657,7 @@ hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipSt
 
 template <int D, int NQ>
 hipError_t merge_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
-    const uint64_t blocks = (uint64_t)a.n_merges * a.n_lay * a.pool.n_head;
+    const uint64_t blocks = (uint64_t)a.n_merges * a.n_lay * a.pool.n_head * (a.merge_split ? a.merge_split : 1);
     if (blocks == 0) return hipSuccess;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;

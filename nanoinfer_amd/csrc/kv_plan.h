@@ -88,6 +88,23 @@ struct PrefillSeq {
 };
 
 // A group split into n_parts partitions, merged by log-sum-exp.
+// Threads per merge workgroup.
+constexpr int kMergeThreads = 512;
+#ifndef NI_MERGE_SPLIT_MAX
+#define NI_MERGE_SPLIT_MAX 8
+#endif
+// Workgroups that merge one (merge item, layer, head) of nq rows and n_parts
+// partitions: enough that each thread merges at most 4 partitions (the loads
+// of one unrolled batch).  A function of the item alone, so a row's merge
+// (and its bits) does not depend on the rest of the call.
+__host__ __device__ inline uint32_t merge_split_of(uint32_t n_parts, uint32_t nq, uint32_t D) {
+    const uint32_t per = nq * D;
+    const uint32_t G = per >= (uint32_t)kMergeThreads ? 1u : (uint32_t)kMergeThreads / per;
+    uint32_t split = 1;
+    while (split < NI_MERGE_SPLIT_MAX && n_parts > 4 * G * split) split *= 2;
+    return split;
+}
+
 struct MergeItem {
     uint32_t row0;
     uint32_t nq;
@@ -212,6 +229,7 @@ struct AttnLaunch {
     uint32_t wide;            // 1: kWideWaves waves per workgroup (single-row items, head_dim 64)
     uint32_t off_pseqs;       // prefill launch: PrefillSeq[n_pseqs]; 0 sequences: one workgroup per item
     uint32_t n_pseqs;
+    uint32_t merge_split;     // merge launch: the largest merge_split_of over its items (0 = 1)
 };
 
 // A plan travels to the device either inside the kernel arguments (up to
