@@ -1,5 +1,5 @@
-"""Configs 3 and 5 at the sizes the benchmark measures, every step against the
-oracle.
+"""Configs 3 (f16 and Q8) and 5 at the sizes the benchmark measures, every step
+against the oracle.
 
 Config 3 is the continuous-batching trace of metal_serve.rs:255-363 with 64
 slots and the reference's 3080-page pool (metal_serve.rs:485); config 5 is the
@@ -86,6 +86,49 @@ def test_config3_full_size_trace(gpu, oracle_lib):
     assert np.array_equal(kg, kw) and np.array_equal(vg, vw)
     say(f"config 3: {len(live)} live after {retired} retirements and {readmitted} later admissions, "
         f"{len(rows)} rows gathered bit for bit, {queried} rows queried, max abs err {worst:.2e}")
+
+
+def test_config3_q8_full_size_steady_state(gpu, oracle_lib):
+    """Config 3 on a Q8 cache (kv8.metal:15-95), the same trace from an empty
+    3080-page pool: every step's appends mirrored into the Q8 oracle
+    (quantised by the oracle from the same f32 inputs), the attention of
+    every queried row checked on steps 300..309 with all 64 slots live after
+    retirements and page reuse, then every live row's int8 values and
+    scales compared bit for bit."""
+    from test_gpu_q8 import MirrorQ8
+
+    rng = np.random.default_rng(43)
+    m = MirrorQ8(na.BatchOpts(**workloads.GPT2, kv_blocks=3080, max_seqs=64, n_ctx=1024, max_rows=512, q8=True))
+    trace = workloads.ContinuousBatching(m.kv)
+    R = 2048
+    qa, ka, va = (rng.standard_normal((12, R, m.c), dtype=np.float32) for _ in range(3))
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (qa, ka, va))
+    worst, queried, retired = 0.0, 0, 0
+    for step in range(310):
+        st = trace.plan()
+        retired += len(st.retire)
+        n = int(st.work[:, 1].sum())
+        off = (step * 389) % (R - 512)
+        rows, qrows = step_rows(m.kv, st.work)
+        out = m.kv.step(st.work, qd[:, off:off + n], kd[:, off:off + n], vd[:, off:off + n])
+        m.append_oracle(rows, ka[:, off:off + n], va[:, off:off + n])
+        if step >= 300:
+            assert sum(m.kv.is_live(s) for s in range(64)) == 64
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            want = m.attention_oracle(rows[qrows], qa[:, off:off + n][:, qrows])
+            worst = max(worst, assert_close(got[:, qrows], want, f"Q8 config 3 step {step}"))
+            queried += len(qrows)
+        trace.commit()
+        if step % 40 == 39:
+            say(f"Q8 config 3 step {step}: {retired} retired, max abs err {worst:.2e}")
+    assert retired > 0 and queried >= 10 * 56  # (a sequence mid-prompt has no query that step)
+    live = [s for s in range(64) if m.kv.is_live(s)]
+    rows = [(s, p) for s in live for p in range(m.kv.seq_len(s))]
+    for i in range(0, len(rows), 512):  # one gather holds at most max_rows rows
+        m.check_bytes(rows[i:i + 512])
+    say(f"Q8 config 3: {retired} retirements, {len(rows)} rows' int8 values and scales bit for bit, "
+        f"{queried} rows queried, max abs err {worst:.2e}")
 
 
 @pytest.mark.parametrize("per_layer", [False, True], ids=["all_layers", "per_layer"])
