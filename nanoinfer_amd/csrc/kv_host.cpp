@@ -499,8 +499,11 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     for (uint32_t i = 0; i < P.pitems.size(); i++) n_seqs += i == 0 || P.pitems[i].tab != P.pitems[i - 1].tab;
     if (P.seq_prefill && (uint64_t)n_seqs * n_lay * kv->o.n_head < kSeqPrefillMinUnits) P.seq_prefill = false;
     if (P.seq_prefill && NI_PREFILL_SEQ_ORDER && P.items.empty() && P.n_pslots == 0 && !P.pitems.empty()) {
-        uint64_t rows = 0;
-        for (uint32_t i = 0; i < P.pitems.size();) {
+        uint64_t rows = 0;  // the sequences' new rows: all of the step's, or an append launch
+        for (uint32_t i = 0; i < P.pitems.size(); i++)
+            if (i == 0 || P.pitems[i].tab != P.pitems[i - 1].tab)
+                rows += app_of[P.pitems[i].tab].new_end - app_of[P.pitems[i].tab].new_begin;
+        for (uint32_t i = 0; rows == P.app.size() && i < P.pitems.size();) {
             const uint32_t tab = P.pitems[i].tab;
             uint32_t e = i + 1;
             while (e < P.pitems.size() && P.pitems[e].tab == tab) e++;
@@ -515,12 +518,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
                 lo = hi;
             }
             P.pseqs.push_back({i, e - i});
-            rows += sr.new_end - sr.new_begin;
             i = e;
-        }
-        if (rows != P.app.size()) {  // some rows belong to no prefill sequence: append launch
-            P.pseqs.clear();
-            for (AttnItem& it : P.pitems) it.app0 = it.napp = 0;
         }
     }
     P.seq_prefill = !P.pseqs.empty();
