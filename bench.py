@@ -297,18 +297,22 @@ def _line(args, r, workload, cfg, data):
     }
 
 
-def _roofline(rp, kernel, with_merge):
-    """Algorithmic bytes of the profiled run / the attention (+ merge)
-    launches' event time."""
+def _roofline(rp, kernel, with_merge, with_append=False):
+    """Algorithmic bytes of the profiled run / the attention (+ merge, + an
+    append launch before it when the step has one) launches' event time."""
     ms, n = rp["kernel_ms"][1], rp["kernel_launches"][1]
     mm, mn = rp["kernel_ms"][2], rp["kernel_launches"][2]
-    kernel_ms = ms + (mm if with_merge else 0.0)
+    am, an = rp["kernel_ms"][0], rp["kernel_launches"][0]
+    kernel_ms = ms + (mm if with_merge else 0.0) + (am if with_append else 0.0)
     ach = rp["bytes"] / (kernel_ms / 1e3) / 1e9
     out = {"bound": "hbm", "achieved": round(ach, 2), "peak": PEAK_GBS, "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4),
            "traffic": None, "kernel": kernel, "avg_launch_us": round(ms / n * 1e3, 3), "launches": n,
            "algorithmic_bytes_per_launch": int(rp["bytes"] / n)}
     if with_merge:
         out["avg_merge_us"] = round(mm / mn * 1e3, 3) if mn else 0.0
+    if with_append and an:
+        out["avg_append_us"] = round(am / an * 1e3, 3)
+        out["append_launches"] = an
     return out
 
 
@@ -517,7 +521,7 @@ def run_config3(args):
 SECONDARY_LINES = {
     "config2": (200, 20, "attn_split_kernel (fused append)"),
     "config4": (100, 10, "attn_split_kernel + attn_merge_kernel"),
-    "config5": (200, 20, "attn_mfma_kernel (fused append)"),
+    "config5": (200, 20, "kv_append_kernel + attn_mfma_kernel"),
     "config3q8": (200, 20, "attn_q8_kernel (fused append), Q8 cache"),
     "prefill": (100, 10, "attn_prefill_kernel (after its append launch)"),
     "qkv64": (200, 20, "qkv_mid_kernel (append in the epilogue)"),
@@ -548,7 +552,10 @@ def secondary_lines(args, reps=3):
             line["tflops"] = round(r["flops"] / r["seconds"] / 1e12, 2)
             mask, ids = 1 << 3, (3,)
         else:
-            mask, ids = (1 << 0) | (1 << 1) | (1 << 2), (1, 2)
+            # every launch of the step (config 5's append launch too); the
+            # prefill line below takes its attention launch alone
+            mask = (1 << 0) | (1 << 1) | (1 << 2)
+            ids = (1, 2) if name == "prefill" else (0, 1, 2)
         rp = _drive(name, a, profile_mask=mask, ramp=ramp)
         kms = sum(rp["kernel_ms"][i] for i in ids)
         if name == "prefill" and rp["kernel_launches"][0]:
@@ -597,10 +604,11 @@ def run_secondary(args):
                 "synthetic (seeded normal q/k/v resident in HBM)")
     res["repetitions"] = spread
     if not args.no_profile:
-        rp = _drive(args.workload, args, profile_mask=(1 << 1) | (1 << 2))
+        rp = _drive(args.workload, args, profile_mask=(1 << 0) | (1 << 1) | (1 << 2))
         res["roofline"] = _roofline(rp, "attn_q8_kernel (+ attn_merge_kernel when split)" if args.workload.endswith("q8")
-                                    else "attn_split_kernel / attn_mfma_kernel (+ attn_merge_kernel when split)",
-                                    with_merge=True)
+                                    else "attn_split_kernel / attn_mfma_kernel (+ attn_merge_kernel when split, "
+                                         "+ kv_append_kernel before a step of query groups)",
+                                    with_merge=True, with_append=True)
         tr = measured_traffic(args.workload, args, 0)
         if tr:
             res["roofline"]["traffic"] = tr["traffic_bytes_per_launch"]

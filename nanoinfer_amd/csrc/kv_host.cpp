@@ -69,6 +69,11 @@ constexpr uint32_t kRingSlots = 4;
 #define NI_SEQ_PREFILL_MIN_UNITS 1536
 #endif
 constexpr uint64_t kSeqPrefillMinUnits = NI_SEQ_PREFILL_MIN_UNITS;
+// 1: all-layer f16 steps of query groups only append in a launch of their own
+// (build_step_plan).
+#ifndef NI_SPLIT_GROUP_APPEND
+#define NI_SPLIT_GROUP_APPEND 1
+#endif
 #ifndef NI_LAYER_PLAN_STAGED
 #define NI_LAYER_PLAN_STAGED 0
 #endif
@@ -1507,6 +1512,24 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
         big |= work[w].n_query > max_group_rows(kv);
     }
     if (big) fused = prefill && small;
+    // An all-layer f16 step whose queried sequences are all verify-style
+    // groups (2 .. max_group_rows rows) takes an append launch first: in the
+    // group kernel the workgroup's own append (f32 loads, f16 stores, then a
+    // barrier) sits before its first page loads, and config 5 measured
+    // 5584 -> 5716 GB/s without it, the append launch included.  One layer per
+    // launch keeps the fused form (a second launch per layer: 3808 -> 3411),
+    // and so do Q8 pools (4140 -> 4081).
+    if (NI_SPLIT_GROUP_APPEND && fused && n_lay > 1 && !is_q8(kv->o)) {
+        bool groups_only = false;
+        for (uint32_t w = 0; w < n_work; w++) {
+            if (work[w].n_query == 1) {
+                groups_only = false;
+                break;
+            }
+            groups_only |= work[w].n_query > 1;
+        }
+        if (groups_only) fused = false;
+    }
     kv->plan.fused = fused;
     // A step of prompt chunks whose every sequence is queried as prefill
     // groups, on a Q8 pool: the prefill launch appends each sequence's rows
