@@ -69,10 +69,10 @@ constexpr uint32_t kRingSlots = 4;
 #define NI_SEQ_PREFILL_MIN_UNITS 1536
 #endif
 constexpr uint64_t kSeqPrefillMinUnits = NI_SEQ_PREFILL_MIN_UNITS;
-// 1: all-layer f16 steps of query groups only append in a launch of their own
-// (build_step_plan).
-#ifndef NI_SPLIT_GROUP_APPEND
-#define NI_SPLIT_GROUP_APPEND 1
+// 1: all-layer steps whose fused form would append in workgroup prologues take
+// an append launch of their own first (build_step_plan).
+#ifndef NI_SPLIT_PROLOGUE_APPEND
+#define NI_SPLIT_PROLOGUE_APPEND 1
 #endif
 #ifndef NI_LAYER_PLAN_STAGED
 #define NI_LAYER_PLAN_STAGED 0
@@ -1512,23 +1512,33 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
         big |= work[w].n_query > max_group_rows(kv);
     }
     if (big) fused = prefill && small;
-    // An all-layer f16 step whose queried sequences are all verify-style
-    // groups (2 .. max_group_rows rows) takes an append launch first: in the
-    // group kernel the workgroup's own append (f32 loads, f16 stores, then a
-    // barrier) sits before its first page loads, and config 5 measured
-    // 5584 -> 5716 GB/s without it, the append launch included.  One layer per
-    // launch keeps the fused form (a second launch per layer: 3808 -> 3411),
-    // and so do Q8 pools (4140 -> 4081).
-    if (NI_SPLIT_GROUP_APPEND && fused && n_lay > 1 && !is_q8(kv->o)) {
-        bool groups_only = false;
+    // All layers per launch, an append launch goes first where the fused
+    // form would put the append in workgroup prologues (the rows' input
+    // loads and stores, then a barrier, before the first page loads):
+    // * f16, every queried sequence a verify-style group (2 .. max_group_rows
+    //   rows; the group kernel appends in its prologue): config 5 5584 ->
+    //   5716 GB/s, the append launch included;
+    // * Q8 (the all-layer Q8 kernel appends in its prologue), a queried
+    //   sequence appending more than max_group_rows rows (a prompt chunk whose
+    //   last row is queried) or at least kQ8SplitUnits queried (sequence,
+    //   layer, head) units: Q8 config 3 (9216 units, prompt chunks) 4815 ->
+    //   4944, while config 2 (2304 units, one row each) measured 4786 fused
+    //   against 4741, config 4 and 5 the same either way.
+    // f16 single rows take their rows as their pages stream (no prologue),
+    // and stay fused (config 3: 6146 fused against 6118); so does one layer
+    // per launch (a second launch per layer: f16 config 5 3808 -> 3411).
+    if (NI_SPLIT_PROLOGUE_APPEND && fused && n_lay > 1) {
+        constexpr uint64_t kQ8SplitUnits = 8192;
+        bool any_group = false, any_single = false, long_rows = false;
+        uint64_t units = 0;
         for (uint32_t w = 0; w < n_work; w++) {
-            if (work[w].n_query == 1) {
-                groups_only = false;
-                break;
-            }
-            groups_only |= work[w].n_query > 1;
+            if (work[w].n_query == 0) continue;  // (rows appended by extra blocks, not prologues)
+            any_group |= work[w].n_query > 1;
+            any_single |= work[w].n_query == 1;
+            long_rows |= work[w].n_new > max_group_rows(kv);
+            units += (uint64_t)n_lay * kv->o.n_head;
         }
-        if (groups_only) fused = false;
+        if (is_q8(kv->o) ? long_rows || units >= kQ8SplitUnits : any_group && !any_single) fused = false;
     }
     kv->plan.fused = fused;
     // A step of prompt chunks whose every sequence is queried as prefill

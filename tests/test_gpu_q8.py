@@ -172,9 +172,10 @@ def test_q8_large_values(gpu, oracle_lib, nq):
 @pytest.mark.parametrize("per_layer", [False, True], ids=["all_layers", "per_layer"])
 def test_q8_step_fused_rollback_and_reuse(gpu, oracle_lib, per_layer):
     """ni_kv_step on a Q8 cache: decode rows, a prompt chunk queried at its
-    last row, a 5-row verify group and a mid-prompt chunk (no query), all in
-    one fused launch (per_layer: one per layer over one plan); then
-    truncate, free and reuse pages."""
+    last row, a 5-row verify group and a mid-prompt chunk (no query) in one
+    step -- one fused launch, or, all layers with the 37-row chunk queried,
+    an append launch and then the attention launch (per_layer: one fused
+    launch per layer over one plan); then truncate, free and reuse pages."""
     rng = np.random.default_rng(92)
     m = MirrorQ8(opts(workloads.GPT2, n_layer=3))
     a, b, c, d = (m.kv.add_seq() for _ in range(4))
