@@ -522,7 +522,7 @@ SECONDARY_LINES = {
     "config2": (200, 20, "attn_split_kernel (fused append)"),
     "config4": (100, 10, "attn_split_kernel + attn_merge_kernel"),
     "config5": (200, 20, "kv_append_kernel + attn_mfma_kernel"),
-    "config3q8": (200, 20, "attn_q8_kernel (fused append), Q8 cache"),
+    "config3q8": (200, 20, "kv_append_kernel + attn_q8_kernel, Q8 cache"),
     "prefill": (100, 10, "attn_prefill_kernel (after its append launch)"),
     "qkv64": (200, 20, "qkv_mid_kernel (append in the epilogue)"),
 }
