@@ -227,7 +227,9 @@ int ni_kv_step_noalloc(ni_kv* kv, const ni_work* work, uint32_t n_work, const fl
  * ni_kv_step_begin checks the work items and reserves pages exactly as
  * ni_kv_step (same errors; nothing is open after an error) and plans the step
  * once; ni_kv_step_layer(layer) then appends that layer's new rows and runs
- * its attention in one launch over that plan (q/k/v/out hold the layer's rows
+ * its attention over that plan, in one launch (a step of prompt chunks that
+ * are queried at every row: an append launch, then the prefill launch)
+ * (q/k/v/out hold the layer's rows
  * only, row r at base + r*row_stride); ni_kv_step_end commits seq_len +=
  * n_new.  Layers may come in any order, each once, all on the stream of
  * the first layer's call (the layers share the step's plan and split
