@@ -156,10 +156,10 @@ typedef struct ni_drive_result {
                              * query, key and element of C: q.k and p.v), of the timed iterations */
     double kernel_ms[NI_K_COUNT]; /* per ni_kernel_id over the timed iterations, when profiled */
     uint64_t kernel_launches[NI_K_COUNT];
-    /* Host microseconds per call with the device idle (up to 20 more
-     * iterations after the timed ones, each after the stream drains): the
-     * planning call (ni_kv_step, or ni_kv_step_begin) and ni_kv_step_layer;
-     * 0 where the launch path makes no such call. */
+    /* Host microseconds per call with the device idle, the median over up to
+     * 20 more iterations after the timed ones, each after the stream drains:
+     * the planning call (ni_kv_step, or ni_kv_step_begin) and
+     * ni_kv_step_layer; 0 where the launch path makes no such call. */
     double idle_us_plan_call;
     double idle_us_layer_call;
 } ni_drive_result;

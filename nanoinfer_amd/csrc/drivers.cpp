@@ -344,10 +344,10 @@ struct Runner {
     int64_t ls;  // layer stride of the q/k/v/out buffers (floats)
     std::vector<ni_row> rows, qrows;
     uint64_t calls = 0;
-    // Host seconds inside the planning calls (ni_kv_step, ni_kv_step_begin)
-    // and the per-layer calls (ni_kv_step_layer), and their counts.
-    double plan_s = 0, layer_s = 0;
-    uint64_t plan_n = 0, layer_n = 0;
+    // With time_calls set: host seconds of each planning call (ni_kv_step,
+    // ni_kv_step_begin) and each per-layer call (ni_kv_step_layer).
+    bool time_calls = false;
+    std::vector<double> plan_t, layer_t;
 
     double kvb;  // stored bytes of one position's K (or V) in one layer
 
@@ -424,8 +424,7 @@ struct Runner {
             const auto t0 = clk::now();
             if (int rc = ni_kv_step(kv, w, n, d.q, d.k, d.v, C, ls, d.out, C, ls, o.split_tokens, stream))
                 return kv_fail(rc, "ni_kv_step");
-            plan_s += since(t0);
-            plan_n++;
+            if (time_calls) plan_t.push_back(since(t0));
             return NI_OK;
         }
         if (o.launch == NI_DRIVE_STEP_LAYERS) {
@@ -433,8 +432,7 @@ struct Runner {
             // layer, as a model's forward would call it between layers.
             const auto t0 = clk::now();
             if (int rc = ni_kv_step_begin(kv, w, n, o.split_tokens)) return kv_fail(rc, "ni_kv_step_begin");
-            plan_s += since(t0);
-            plan_n++;
+            if (time_calls) plan_t.push_back(since(t0));
             for (uint32_t l = 0; l < L; l++) {
                 calls++;
                 const auto t1 = clk::now();
@@ -443,8 +441,7 @@ struct Runner {
                     (void)ni_kv_step_end(kv);
                     return kv_fail(rc, "ni_kv_step_layer");
                 }
-                layer_s += since(t1);
-                layer_n++;
+                if (time_calls) layer_t.push_back(since(t1));
             }
             if (int rc = ni_kv_step_end(kv)) return kv_fail(rc, "ni_kv_step_end");
             return NI_OK;
@@ -530,16 +527,24 @@ int timed_run(Runner& r, ni_drive_result* res, Fn&& iterate) {
     // The host cost of the calls themselves: a few more iterations, each
     // after the stream has drained, so no call waits for room in the
     // device's queue (in the timed loop the host runs ahead until it does).
-    r.plan_s = r.layer_s = 0;
-    r.plan_n = r.layer_n = 0;
+    // The median of the calls, so that one stall of the host does not move it.
+    r.plan_t.clear();
+    r.layer_t.clear();
+    r.time_calls = true;
     const uint32_t n_idle = std::min<uint32_t>(r.o.steps, 20);
     for (uint32_t i = 0; i < n_idle; i++) {
         if (hipStreamSynchronize(r.stream) != hipSuccess) return drive_fail(NI_ERR_HIP, "hipStreamSynchronize failed");
         if (int rc = iterate(WARMUP)) return rc;
     }
+    r.time_calls = false;
     if (hipStreamSynchronize(r.stream) != hipSuccess) return drive_fail(NI_ERR_HIP, "hipStreamSynchronize failed");
-    res->idle_us_plan_call = r.plan_n ? r.plan_s / r.plan_n * 1e6 : 0;
-    res->idle_us_layer_call = r.layer_n ? r.layer_s / r.layer_n * 1e6 : 0;
+    auto median_us = [](std::vector<double>& t) {
+        if (t.empty()) return 0.0;
+        std::nth_element(t.begin(), t.begin() + t.size() / 2, t.end());
+        return t[t.size() / 2] * 1e6;
+    };
+    res->idle_us_plan_call = median_us(r.plan_t);
+    res->idle_us_layer_call = median_us(r.layer_t);
     return NI_OK;
 }
 
