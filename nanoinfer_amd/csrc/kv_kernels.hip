@@ -2822,6 +2822,23 @@ hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hip
     });
 }
 
+// Compute units of the current device (a round of the QKV grid), looked up
+// once per device; 256 (MI355X) if the query fails.
+uint32_t qkv_cus() {
+    static std::mutex mu;
+    static std::vector<uint32_t> per_device;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    if ((size_t)dev >= per_device.size()) per_device.resize((size_t)dev + 1, 0);
+    if (!per_device[dev]) {
+        int n = 0;
+        per_device[dev] =
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return per_device[dev];
+}
+
 template <int WF>
 hipError_t launch_qkv_t(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
     if (a.n_rows <= NI_QKV_SMALL_ROWS) {
@@ -2848,9 +2865,26 @@ hipError_t launch_qkv_t(const QkvLaunch& a, const void* ip, uint32_t ib, hipStre
             return hipGetLastError();
         });
     }
-    // 16-feature tiles at every row count: the most workgroups to stream W
-    // with (64-feature tiles measured slower from 64 to 512 rows).
-    const dim3 grid((a.n_rows + kQkvTileRows - 1) / kQkvTileRows, a.n_feat / kQkvTileFeat);
+    // 16-feature tiles: the most workgroups to stream W with (64-feature tiles
+    // measured slower from 64 to 512 rows).  Large batches take 48-feature
+    // tiles (x read by a third as many workgroups; 48 KB of LDS, 3 per CU)
+    // when that grid fills whole rounds of the GPU or spans two or more:
+    // 12 layers of GPT-2, 512 rows 327 -> 281 us, 1024 556 -> 502, 2048
+    // 1053 -> 955, while partial rounds lose (384 rows 284 against 293, 640
+    // 376 against 387).  Both issue the same products in the same order.
+    const uint32_t row_tiles = (a.n_rows + kQkvTileRows - 1) / kQkvTileRows;
+    if (a.n_feat % 48 == 0) {
+        const uint64_t wg = (uint64_t)row_tiles * (a.n_feat / 48), round = 3ull * qkv_cus();
+        if (wg >= 2 * round || (wg >= round && wg % round == 0)) {
+            return with_plan(a, ip, ib, [&](auto pa) {
+                constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
+                hipExtLaunchKernelGGL(qkv_kernel<3, INL, WF>, dim3(row_tiles, a.n_feat / 48), dim3(256), 0, s,
+                                      t.start, t.stop, 0, a, pa);
+                return hipGetLastError();
+            });
+        }
+    }
+    const dim3 grid(row_tiles, a.n_feat / kQkvTileFeat);
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
         hipExtLaunchKernelGGL(qkv_kernel<kQkvTileFeat / 16, INL, WF>, grid, dim3(256), 0, s, t.start, t.stop, 0, a,
