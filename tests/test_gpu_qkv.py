@@ -64,8 +64,11 @@ def test_project_batch_invariant(gpu, oracle_lib, shape, d_in):
     and a fixed tree), so a row's outputs have the same bits in a batch of
     any size -- the property the reference's matvec_batch keeps
     (batch.metal:60-66) and speculative verification relies on.  Batches of
-    up to 16 rows run on the small-batch kernel and larger ones on the
-    LDS-staged kernel, so this also checks the two give the same bits."""
+    up to 16 rows run on the small-batch kernel, 17..64 on the mid-size
+    kernel and larger ones on the LDS-staged kernel -- 16-feature tiles at 100
+    and 384 rows, 48-feature tiles for the 512-row batch of head_dim 64 (its
+    768 workgroups fill a round of the GPU) -- so this also checks that they
+    all give the same bits."""
     rng = np.random.default_rng(80 + d_in)
     kv = make(shape)
     c = kv.opts.n_embd
@@ -75,13 +78,13 @@ def test_project_batch_invariant(gpu, oracle_lib, shape, d_in):
     big = kv.qkv_project(xd, wd, bd).cpu().numpy()
     want = oracle.matvec_f64(x, w, b)
     assert np.abs(big - want).max() < 2e-5
-    for n in (1, 9, 16, 17, 64):
+    for n in (1, 9, 16, 17, 64, 100, 384):
         small = kv.qkv_project(xd[:n].contiguous(), wd, bd).cpu().numpy()
         assert np.array_equal(small.view(np.uint32), big[:n].view(np.uint32)), f"n={n}"
     # the same rows at an offset inside the big batch, through a strided view
     small = kv.qkv_project(xd[100:130], wd, bd).cpu().numpy()
     assert np.array_equal(small.view(np.uint32), big[100:130].view(np.uint32))
-    say(f"{shape} d_in {d_in}: batches of 1/9/16/17/64/30 rows bit-identical to the 512-row batch")
+    say(f"{shape} d_in {d_in}: batches of 1/9/16/17/64/100/384/30 rows bit-identical to the 512-row batch")
 
 
 @pytest.mark.parametrize("bias", [True, False])
