@@ -364,13 +364,22 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     // of kWideWaves waves share each item's pages instead of splitting it:
     // no partials, no merge launch.  Query groups of up to one matrix tile
     // (a verify step's rows) do the same from kWideMinGroupUnits units.
-    uint32_t part = split_tokens;
+    // Prefill groups (more rows than one matrix tile, in a launch of their
+    // own) are split automatically only past kLongItem keys: each of their
+    // workgroups already carries 64 queries, and splitting them to fill the
+    // GPU cost more than it gained (prompt steps, every row queried, no split
+    // against the fill choice: one launch per layer 16 x 512 rows 611 against
+    // 753 us, 4 x 512 286 against 436, 1 x 512 254 against 305; all layers 1 x
+    // 512 45 against 67 us, 4 x 512 146 against 167, 2 x 512 and 8 x 256 the
+    // same).
+    constexpr uint32_t kLongItem = 4096;
+    uint32_t part = split_tokens, pre_part = split_tokens;
     if (part == 0) {
         constexpr uint64_t kFillWorkgroups = 2048;
         constexpr uint64_t kWideMinUnits = 512;
         constexpr uint64_t kWideMinGroupUnits = NI_WIDE_MIN_GROUP_UNITS;
-        constexpr uint32_t kLongItem = 4096;
         static const uint32_t kChoices[] = {1024, 512, 256, 128};
+        pre_part = kLongItem;
         const uint64_t per_unit = (uint64_t)n_lay * kv->o.n_head;
         const uint64_t units = (uint64_t)groups.size() * per_unit;
         bool single = true, tiles = true;  // every group one row; every group within one matrix tile
@@ -449,7 +458,8 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         }
         if (!pre) max_nq = std::max(max_nq, g.nq);
         const uint32_t L = g.pos0 + g.nq;
-        const uint32_t n_parts = (L + part - 1) / part;
+        const uint32_t gpart = pre ? pre_part : part;
+        const uint32_t n_parts = (L + gpart - 1) / gpart;
         const uint32_t tab = (uint32_t)kv->seq_tab[g.seq];
         if (n_parts <= 1) {
             item(g, tab, 0, L, kNoSlot);
@@ -457,7 +467,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         }
         uint32_t& n_slots = pre ? P.n_pslots : P.n_slots;
         const uint32_t slot0 = n_slots;
-        for (uint32_t p = 0; p < n_parts; p++) item(g, tab, p * part, std::min((p + 1) * part, L), slot0 + p);
+        for (uint32_t p = 0; p < n_parts; p++) item(g, tab, p * gpart, std::min((p + 1) * gpart, L), slot0 + p);
         (pre ? P.pmerges : P.merges).push_back({g.row0, g.nq, slot0, n_parts});
         n_slots += n_parts;
     }

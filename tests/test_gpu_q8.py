@@ -303,7 +303,7 @@ def test_q8_prompt_chunk_steps(gpu, oracle_lib):
     rows, qrows = step_rows(m.kv, work)
     q, k, v = (rng.standard_normal((2, len(rows), m.c)).astype(np.float32) for _ in range(3))
     m.kv.profile([0])
-    got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v)), split_tokens=1024).cpu().numpy()
+    got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v))).cpu().numpy()
     _, n_app = m.kv.profile_read(0)
     m.kv.profile([])
     assert n_app == 0
@@ -317,7 +317,7 @@ def test_q8_prompt_chunk_steps(gpu, oracle_lib):
     rows, qrows = step_rows(m.kv, work)
     q, k, v = (rng.standard_normal((2, len(rows), m.c)).astype(np.float32) for _ in range(3))
     m.kv.profile([0])
-    got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v)), split_tokens=1024).cpu().numpy()
+    got = m.kv.step(work, *(torch.from_numpy(x).cuda() for x in (q, k, v))).cpu().numpy()
     _, n_app = m.kv.profile_read(0)
     m.kv.profile([])
     assert n_app == 1
