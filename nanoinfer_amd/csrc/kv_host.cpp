@@ -382,16 +382,28 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         pre_part = kLongItem;
         const uint64_t per_unit = (uint64_t)n_lay * kv->o.n_head;
         const uint64_t units = (uint64_t)groups.size() * per_unit;
+        constexpr uint32_t kShortItem = 1280;  // keys (a 1024-token context and its new rows)
         bool single = true, tiles = true;  // every group one row; every group within one matrix tile
+        uint32_t max_keys = 0;
         for (const Group& g : groups) {
             single &= g.nq == 1;
             tiles &= g.nq <= kMfmaTile && !g.pre;
+            max_keys = std::max(max_keys, g.pos0 + g.nq);
         }
         if (units >= kFillWorkgroups) {
             part = kLongItem;
         } else if (tiles && units >= (single ? kWideMinUnits : kWideMinGroupUnits) && kv->o.head_dim == 64) {
             part = kLongItem;
             P.wide = true;
+        } else if (n_lay == 1 && max_keys <= kShortItem) {
+            // One layer per launch and no item past kShortItem keys: the
+            // merge launch a split needs costs more than the fill it buys
+            // (decode rows of 4..32 sequences with contexts U[64,1024]: 213-240
+            // against 251-284 us per step of 12 such launches; 8 x 1024 keys
+            // 208 against 246; from 2048 keys the split wins, 4 x 2048 242
+            // against 285, 4 x 4096 246 against 524, and 16 x U[1024,2048]
+            // 262 against 273).
+            part = kLongItem;
         } else {
             part = kChoices[3];
             for (uint32_t c : kChoices) {
