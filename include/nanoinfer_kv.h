@@ -38,7 +38,7 @@ typedef void* ni_stream; /* hipStream_t */
 
 /* Positions per page (crates/metal/src/batch.rs:33, KV_BLOCK). */
 #define NI_KV_BLOCK 16
-/* `layer` argument: run every layer in one launch (inputs at
+/* `layer` argument: every layer in each launch of the call (inputs at
  * base + l * layer_stride for l in 0..n_layer). */
 #define NI_ALL_LAYERS (-1)
 
