@@ -19,6 +19,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <functional>
+#include <queue>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -108,6 +110,7 @@ struct Plan {
     std::vector<MergeItem> pmerges;  //   and partial slots (a region after the others')
     std::vector<uint32_t> table;
     std::vector<PrefillSeq> pseqs;  // prompt-chunk step: the prefill launch appends, a workgroup per sequence
+    std::vector<uint16_t> order;    // balanced wide launch: the (item, layer, head) unit of each workgroup
     uint32_t n_slots = 0;
     uint32_t n_pslots = 0;
     uint32_t nq_tile = 1;
@@ -119,6 +122,7 @@ struct Plan {
         app.clear();
         orphans.clear();
         pseqs.clear();
+        order.clear();
         seq_prefill = false;
         items.clear();
         merges.clear();
@@ -136,7 +140,7 @@ struct Plan {
 
 // Byte offsets of each part of a serialised plan.
 struct Offsets {
-    size_t app, orphans, items, merges, pitems, pmerges, pseqs, table, total;
+    size_t app, orphans, items, merges, pitems, pmerges, pseqs, table, order, total;
 };
 
 // Where the kernels find a plan: in the launch arguments (small plans) or in
@@ -323,6 +327,56 @@ int layer_range(ni_kv* kv, int32_t layer, uint32_t* layer0, uint32_t* n_lay) {
     *layer0 = (uint32_t)layer;
     *n_lay = 1;
     return NI_OK;
+}
+
+// A wide launch whose workgroups are all resident at once ends with its most
+// loaded CU.  The dispatcher deals such a launch's workgroups to the CUs in
+// rounds: block b shares a CU with blocks b +- C, b +- 2C, ... (C = the
+// device's CUs; per-workgroup timestamps and hardware ids on MI355X put
+// blocks b, b + 256 and b + 512 of a 768-block launch on one CU in each of
+// 240 launches traced, and a CU's finish time followed the pages of its
+// blocks: correlation 0.8, an appended prompt row costing ~1.9 pages' time
+// per 16 rows beyond its page).  Items sorted longest first would give one CU
+// the largest item of every round.  Instead the (item, layer, head) units go
+// to CUs longest first, each to the least loaded CU with a free slot, and
+// P.order records the unit each block runs.
+void balance_units(ni_kv* kv, Plan& P, uint32_t n_lay) {
+    P.order.clear();
+    if (!P.wide || P.items.empty() || kv->host_only) return;
+    const uint64_t lh = (uint64_t)n_lay * kv->o.n_head;
+    const uint64_t n_units = (uint64_t)P.items.size() * lh;
+    const uint64_t C = device_cus();
+    const bool fused = P.napp_total > 0 || !P.orphans.empty();
+    const uint64_t S = wide_blocks_per_cu(kv->o.head_dim, is_q8(kv->o), P.nq_tile, fused);
+    // (one round: every block has a CU of its own already)
+    if (S == 0 || n_units <= C || n_units > C * S || n_units > 65536) return;
+    const uint64_t R = (n_units + C - 1) / C;  // rounds; CUs below `rem` receive R blocks, the others R - 1
+    const uint64_t rem = n_units - (R - 1) * C;
+    // cost in 1/16 pages: the item's pages, and 30/16 more per 16 appended rows
+    std::vector<std::pair<uint64_t, uint32_t>> cost(P.items.size());
+    for (uint32_t i = 0; i < P.items.size(); i++) {
+        const AttnItem& it = P.items[i];
+        const uint64_t pages = (it.kv_end + kPage - 1) / kPage - it.kv_begin / kPage;
+        cost[i] = {16 * pages + 30ull * it.napp, i};
+    }
+    std::stable_sort(cost.begin(), cost.end(),
+                     [](const std::pair<uint64_t, uint32_t>& x, const std::pair<uint64_t, uint32_t>& y) {
+                         return x.first > y.first;
+                     });
+    // (load << 16 | cu): the least loaded CU with a free slot on top
+    std::priority_queue<uint64_t, std::vector<uint64_t>, std::greater<uint64_t>> heap;
+    std::vector<uint32_t> used(C, 0);
+    for (uint64_t c = 0; c < C; c++) heap.push(c);
+    P.order.assign(n_units, 0);
+    for (const auto& ci : cost) {
+        for (uint64_t l = 0; l < lh; l++) {
+            const uint64_t top = heap.top();
+            heap.pop();
+            const uint64_t c = top & 0xffff, load = (top >> 16) + ci.first;
+            P.order[c + C * used[c]] = (uint16_t)(ci.second * lh + l);
+            if (++used[c] < (c < rem ? R : R - 1)) heap.push(load << 16 | c);
+        }
+    }
 }
 
 // Attention part of a plan: group consecutive query rows of one sequence at
@@ -551,6 +605,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     P.seq_prefill = !P.pseqs.empty();
     // Single queries stream on the vector kernel; groups go to matrix cores.
     P.nq_tile = (NI_ATTN_MFMA && max_nq > 1) ? kMfmaTile : max_nq;
+    balance_units(kv, P, n_lay);
     return NI_OK;
 }
 
@@ -654,7 +709,8 @@ Offsets layout(const Plan& P) {
     o.pmerges = align_up(o.pitems + P.pitems.size() * sizeof(AttnItem), kAlign);
     o.pseqs = align_up(o.pmerges + P.pmerges.size() * sizeof(MergeItem), kAlign);
     o.table = align_up(o.pseqs + P.pseqs.size() * sizeof(PrefillSeq), kAlign);
-    o.total = align_up(o.table + P.table.size() * sizeof(uint32_t), kAlign);
+    o.order = align_up(o.table + P.table.size() * sizeof(uint32_t), kAlign);
+    o.total = align_up(o.order + P.order.size() * sizeof(uint16_t), kAlign);
     return o;
 }
 
@@ -675,6 +731,7 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
         memcpy(blob.data() + off->pmerges, P.pmerges.data(), P.pmerges.size() * sizeof(MergeItem));
     if (!P.pseqs.empty()) memcpy(blob.data() + off->pseqs, P.pseqs.data(), P.pseqs.size() * sizeof(PrefillSeq));
     if (!P.table.empty()) memcpy(blob.data() + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
+    if (!P.order.empty()) memcpy(blob.data() + off->order, P.order.data(), P.order.size() * sizeof(uint16_t));
     *ref = PlanRef{};
     if (kv->no_alloc) {
         // No staging slot (it would be allocated): the plan travels inline.
@@ -784,6 +841,8 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
         a.nq_tile = P.nq_tile;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
         a.wide = P.wide ? 1u : 0u;
+        a.off_order = (uint32_t)off.order;
+        a.ordered = P.order.empty() ? 0u : 1u;
         a.n_orphan_blocks = P.fused ? orphan_blocks(a) : 0;
         {
             ProfileScope ps(kv, NI_K_ATTN);

@@ -357,6 +357,25 @@ __device__ __forceinline__ u32x4 load16(const u32x4* p) {
 #endif
 }
 
+// The (item, layer, head) unit workgroup b of an attention launch runs:
+// unit b itself (item-major, b = (item * n_lay + layer) * n_head + head), or
+// in a balanced wide launch the plan's block -> unit table (the blocks a CU
+// receives then carry an even share of the launch's pages).
+struct AttnUnit {
+    uint32_t item, lay, head;
+};
+__device__ __forceinline__ AttnUnit attn_unit(const AttnLaunch& a, const uint8_t* plan, uint32_t b) {
+    const uint32_t H = a.pool.n_head;
+    const uint32_t lh = a.n_lay * H;
+    const uint32_t u = a.ordered ? (uint32_t)reinterpret_cast<const uint16_t*>(plan + a.off_order)[b] : b;
+    AttnUnit r;
+    r.item = u / lh;
+    const uint32_t rem = u - r.item * lh;
+    r.lay = rem / H;
+    r.head = rem - r.lay * H;
+    return r;
+}
+
 // Fused append of one item: this step's new rows in [kv_begin, kv_end),
 // this (layer, head)'s slice.  No other workgroup of the launch reads or
 // writes these blocks and the vector L1 starts the kernel clean, so after a
@@ -488,10 +507,8 @@ __global__ __launch_bounds__(64 * W, W == 8 ? NI_WIDE_MIN_WAVES : 1) void attn_s
             return;
         }
     }
-    const uint32_t item_i = blockIdx.x / lh;
-    const uint32_t rem = blockIdx.x - item_i * lh;
-    const uint32_t lay = rem / H;
-    const uint32_t head = rem - lay * H;
+    const AttnUnit un = attn_unit(a, plan, blockIdx.x);
+    const uint32_t item_i = un.item, lay = un.lay, head = un.head;
     const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
     const int kl = lane / LPK;
     const int ds = lane % LPK;
@@ -861,10 +878,8 @@ __global__ __launch_bounds__(64 * W) void attn_q8_kernel(const AttnLaunch a, con
             return;
         }
     }
-    const uint32_t item_i = blockIdx.x / lh;
-    const uint32_t rem = blockIdx.x - item_i * lh;
-    const uint32_t lay = rem / H;
-    const uint32_t head = rem - lay * H;
+    const AttnUnit un = attn_unit(a, plan, blockIdx.x);
+    const uint32_t item_i = un.item, lay = un.lay, head = un.head;
     const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
     const int kl = lane / LPK;
     const int ds = lane % LPK;
@@ -1537,10 +1552,8 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
             return;
         }
     }
-    const uint32_t item_i = blockIdx.x / lh;
-    const uint32_t rem = blockIdx.x - item_i * lh;
-    const uint32_t lay = rem / H;
-    const uint32_t head = rem - lay * H;
+    const AttnUnit un = attn_unit(a, plan, blockIdx.x);
+    const uint32_t item_i = un.item, lay = un.lay, head = un.head;
     const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item_i];
     const int col = lane & 15;  // query slot of S^T / O^T columns
     const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
@@ -2822,9 +2835,9 @@ hipError_t launch_append(const AppendLaunch& a, const void* ip, uint32_t ib, hip
     });
 }
 
-// Compute units of the current device (a round of the QKV grid), looked up
-// once per device; 256 (MI355X) if the query fails.
-uint32_t qkv_cus() {
+// Compute units of the current device (a round of a grid), looked up once
+// per device; 256 (MI355X) if the query fails.
+uint32_t device_cus() {
     static std::mutex mu;
     static std::vector<uint32_t> per_device;
     int dev = 0;
@@ -2837,6 +2850,42 @@ uint32_t qkv_cus() {
             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
     }
     return per_device[dev];
+}
+
+uint32_t wide_blocks_per_cu(uint32_t head_dim, bool q8, uint32_t nq_tile, bool fused) {
+    if (head_dim != 64) return 0;
+    // the kernel attn_dispatch picks for a wide launch with these parameters
+    const void* f = nullptr;
+    int threads = 0;
+    constexpr int INL = (int)kInlinePlanSmall;
+    if (nq_tile == kMfmaTile) {
+        threads = 64 * kWideWaves;
+        f = q8 ? (fused ? (const void*)attn_mfma_kernel<64, kWideWaves, kMfmaPages, true, INL, true>
+                        : (const void*)attn_mfma_kernel<64, kWideWaves, kMfmaPages, false, INL, true>)
+               : (fused ? (const void*)attn_mfma_kernel<64, kWideWaves, kMfmaPages, true, INL, false>
+                        : (const void*)attn_mfma_kernel<64, kWideWaves, kMfmaPages, false, INL, false>);
+    } else if (nq_tile == 1 && q8) {
+        threads = 64 * kWideWavesQ8;
+        f = fused ? (const void*)attn_q8_kernel<64, kWideWavesQ8, NI_Q8_PAGES, true, INL>
+                  : (const void*)attn_q8_kernel<64, kWideWavesQ8, NI_Q8_PAGES, false, INL>;
+    } else if (nq_tile == 1) {
+        threads = 64 * kWideWaves;
+        f = fused ? (const void*)attn_split_kernel<64, 1, kWideWaves, NI_WIDE_PAGES, true, INL>
+                  : (const void*)attn_split_kernel<64, 1, kWideWaves, NI_WIDE_PAGES, false, INL>;
+    } else {
+        return 0;
+    }
+    static std::mutex mu;
+    static std::vector<std::pair<std::pair<int, const void*>, uint32_t>> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& c : cache)
+        if (c.first.first == dev && c.first.second == f) return c.second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess || n < 0) n = 0;
+    cache.push_back({{dev, f}, (uint32_t)n});
+    return (uint32_t)n;
 }
 
 template <int WF>
@@ -2874,7 +2923,7 @@ hipError_t launch_qkv_t(const QkvLaunch& a, const void* ip, uint32_t ib, hipStre
     // 376 against 387).  Both issue the same products in the same order.
     const uint32_t row_tiles = (a.n_rows + kQkvTileRows - 1) / kQkvTileRows;
     if (a.n_feat % 48 == 0) {
-        const uint64_t wg = (uint64_t)row_tiles * (a.n_feat / 48), round = 3ull * qkv_cus();
+        const uint64_t wg = (uint64_t)row_tiles * (a.n_feat / 48), round = 3ull * device_cus();
         if (wg >= 2 * round || (wg >= round && wg % round == 0)) {
             return with_plan(a, ip, ib, [&](auto pa) {
                 constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;

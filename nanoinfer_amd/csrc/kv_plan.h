@@ -230,6 +230,11 @@ struct AttnLaunch {
     uint32_t off_pseqs;       // prefill launch: PrefillSeq[n_pseqs]; 0 sequences: one workgroup per item
     uint32_t n_pseqs;
     uint32_t merge_split;     // merge launch: the largest merge_split_of over its items (0 = 1)
+    // Wide one-layer launches: workgroup b runs (item, layer, head) unit
+    // order[b] (uint16_t[n_items * n_lay * n_head] at off_order) instead of
+    // unit b, so that each CU receives an even share of the work.
+    uint32_t off_order;
+    uint32_t ordered;
 };
 
 // A plan travels to the device either inside the kernel arguments (up to
@@ -293,6 +298,14 @@ struct RowsLaunch {
 hipError_t launch_attention_rows(const RowsLaunch& a, hipStream_t s);
 // Blocks a fused launch needs for its orphan rows (n_orphans set).
 uint32_t orphan_blocks(const AttnLaunch& a);
+// Compute units of the current device, looked up once per device (256 if
+// the query fails).
+uint32_t device_cus();
+// Workgroups of the wide (one item per workgroup of several waves) attention
+// launch for these parameters that one CU holds at once, from the kernel's
+// own resource use (hipOccupancyMaxActiveBlocksPerMultiprocessor); 0 if
+// unknown.
+uint32_t wide_blocks_per_cu(uint32_t head_dim, bool q8, uint32_t nq_tile, bool fused);
 bool attention_supported(uint32_t head_dim);
 
 }  // namespace ni
