@@ -17,6 +17,17 @@
  *  - One host thread per handle.  Data-path calls enqueue work on the
  *    caller's HIP stream (`ni_stream`, a hipStream_t; NULL = null stream) and
  *    return without waiting; ni_kv_sync() waits.
+ *  - A handle's data-path calls run on the device in the order they are
+ *    made, whatever streams they are made on (they share the handle's split
+ *    partials, and a page that truncate or free_seq returns may go to the
+ *    very next append).  A call on a stream other than the one that holds
+ *    the handle's previous work makes its stream wait for that work first
+ *    (an event recorded on the previous stream, then hipStreamWaitEvent).
+ *    So a stream the handle's last call used must stay alive until the next
+ *    call on another stream, or until ni_kv_sync(kv, that stream).  Calls on
+ *    a stream that is capturing a graph are not ordered against other
+ *    streams: the captured work runs when the caller replays the graph, and
+ *    ordering replays is the caller's part.
  *  - Bookkeeping calls (add/free/truncate/reserve/commit) act on host state
  *    at once.  A data-path call snapshots the block tables it needs when it
  *    is made, so later bookkeeping never changes work already enqueued.
@@ -214,8 +225,11 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
  * the launch arguments.  A step whose plan exceeds 32 KB or whose partials
  * exceed 32 MiB returns NI_ERR_BAD_ARG with the limit in the message (its
  * pages stay reserved, as after any failed launch; nothing is launched).
- * Every call on one GPU shares that array: calls that overlap on one GPU
- * (other streams, other handles) race. */
+ * Every call on one GPU shares that array: calls of one handle are ordered
+ * (see the conventions above), but calls of different handles, and graph
+ * replays, that overlap on one GPU race.  ni_kv_profile does not time the
+ * launches of this call (timing would take events from the handle's pool,
+ * which may create them). */
 int ni_kv_step_noalloc(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
                        const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
                        int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream);
@@ -255,7 +269,8 @@ int ni_kv_decode_steps(ni_kv* kv, const uint32_t* seqs, uint32_t n, uint32_t ste
                        int64_t out_row_stride, int64_t out_layer_stride, int64_t out_step_stride,
                        uint32_t split_tokens, ni_stream stream);
 
-/* Wait for all work this handle enqueued on `stream`. */
+/* Wait for all work this handle enqueued on `stream`; afterwards no call of
+ * the handle waits for that work, and `stream` may be destroyed. */
 int ni_kv_sync(ni_kv* kv, ni_stream stream);
 
 /* The device pool, for inspection: one allocation of `bytes`, laid out

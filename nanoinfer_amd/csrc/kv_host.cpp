@@ -44,16 +44,6 @@ constexpr uint32_t kRingSlots = 4;
 #ifndef NI_WIDE_MIN_GROUP_UNITS
 #define NI_WIDE_MIN_GROUP_UNITS 256
 #endif
-// 1: every plan goes through the staging ring (none in the kernel arguments).
-#ifndef NI_STAGE_ALL_PLANS
-#define NI_STAGE_ALL_PLANS 0
-#endif
-// 1: ni_kv_step_begin uploads the step's plan to device memory once and each
-// layer's launch passes its address.  Off by default: config 3 one launch per
-// layer measured 3535 against 3722 GB/s with the plan inline in each launch's
-// arguments (the stream's wait for the upload costs more than the 16 KB of
-// arguments), and the host time per step did not change (the host runs ahead
-// until the device's queue is full either way).
 // Prefill groups ordered by sequence (1) or longest first (0): 16 x 512-row
 // prefill 504 -> 463 us per step, the attention launch's L2 hits 2.4M -> 10.4M
 // and misses 15.3M -> 7.3M (rocprofv3 TCC_HIT/TCC_MISS).
@@ -75,12 +65,6 @@ constexpr uint64_t kSeqPrefillMinUnits = NI_SEQ_PREFILL_MIN_UNITS;
 // an append launch of their own first (build_step_plan).
 #ifndef NI_SPLIT_PROLOGUE_APPEND
 #define NI_SPLIT_PROLOGUE_APPEND 1
-#endif
-#ifndef NI_LAYER_PLAN_STAGED
-#define NI_LAYER_PLAN_STAGED 0
-#endif
-#ifndef NI_PLAN_COPY_STREAM
-#define NI_PLAN_COPY_STREAM 1
 #endif
 constexpr size_t kAlign = 256;
 constexpr uint32_t kMinSplit = 64;  // smallest partition the planner uses (tokens)
@@ -186,15 +170,25 @@ struct ni_kv {
     hipStream_t copy_stream = nullptr;
     float* partials = nullptr;
     size_t partials_bytes = 0;
-    // Outgrown partials buffers: launches already enqueued may still use
-    // them, so they are freed only at ni_kv_destroy (each buffer is 1.5x the
-    // last, so together they stay below twice the current one).
-    std::vector<float*> partials_retired;
+    // Outgrown partials buffers, each with an event recorded when it was
+    // retired: launches enqueued before may still use it, so it is freed by
+    // the next ni_kv_sync that finds its event complete (or ni_kv_destroy).
+    std::vector<std::pair<float*, hipEvent_t>> partials_retired;
     // ni_kv_step_noalloc: this device's scratch array (null if its address
     // could not be found), and set for the duration of such a call.
     float* scratch = nullptr;
     hipError_t scratch_err = hipSuccess;
     bool no_alloc = false;
+
+    // Order of data-path calls across streams (begin_call): `dirty` says
+    // that work of this handle was enqueued on dirty_stream after `order`
+    // was last recorded; `order` (valid if order_valid) marks the end of the
+    // handle's work enqueued on order_stream before it.
+    hipEvent_t order = nullptr;
+    hipStream_t order_stream = nullptr;
+    bool order_valid = false;
+    hipStream_t dirty_stream = nullptr;
+    bool dirty = false;
 
     uint32_t profile = 0;  // bit k: bracket kernel k's launches with events
     std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_ev[NI_K_COUNT];
@@ -674,7 +668,7 @@ uint32_t merge_split(const std::vector<MergeItem>& merges, uint32_t D) {
     return split;
 }
 
-int ensure_partials(ni_kv* kv, size_t bytes, float** out) {
+int ensure_partials(ni_kv* kv, size_t bytes, hipStream_t s, float** out) {
     if (kv->no_alloc) {
         if (bytes > kScratchBytes)
             return kv->fail(NI_ERR_BAD_ARG,
@@ -687,12 +681,27 @@ int ensure_partials(ni_kv* kv, size_t bytes, float** out) {
     *out = kv->partials;
     if (bytes <= kv->partials_bytes) return NI_OK;
     // Launches already enqueued may still use the old buffer: retire it
-    // (no host wait here) rather than free it.
+    // (no host wait here) rather than free it.  Every earlier call's work is
+    // ordered before this point of `s` (begin_call), so an event recorded
+    // here marks when the old buffer is free.
     const size_t cap = align_up(bytes + bytes / 2, 1 << 20);
     float* p = nullptr;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p), cap);
     if (e != hipSuccess) return kv->hip_fail(e, "hipMalloc(partials)");
-    if (kv->partials) kv->partials_retired.push_back(kv->partials);
+    if (kv->partials) {
+        hipEvent_t ev = take_event(kv);
+        if (!ev) {
+            (void)hipFree(p);
+            return kv->fail(NI_ERR_HIP, "hipEventCreate(partials)");
+        }
+        e = hipEventRecord(ev, s);
+        if (e != hipSuccess) {
+            kv->ev_pool.push_back(ev);
+            (void)hipFree(p);
+            return kv->hip_fail(e, "hipEventRecord(partials)");
+        }
+        kv->partials_retired.push_back({kv->partials, ev});
+    }
     kv->partials = p;
     kv->partials_bytes = cap;
     *out = p;
@@ -714,11 +723,40 @@ Offsets layout(const Plan& P) {
     return o;
 }
 
-// Serialise plan P into `blob` and make it reachable from `s`.  stage:
-// always through a staging slot (never inline); with s == nullptr the upload
-// is left for the caller to wait on (the slot's `uploaded` event).
-int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t s, Offsets* off, PlanRef* ref,
-               bool stage = false) {
+// Data-path calls of one handle run in call order, whatever streams they are
+// made on: they share the handle's split partials and staging slots, and
+// the pages they read or write change owners at once on the host (a page
+// that truncate or free_seq returns may go to the next append).  So a call
+// on a stream other than the one of the handle's previous work first makes
+// its stream wait for that work: an event recorded on the previous stream
+// (at the switch, so a call on one stream costs nothing extra), then
+// hipStreamWaitEvent.  Work captured into a graph runs when the caller
+// replays the graph, so calls on a capturing stream are not ordered here.
+int begin_call(ni_kv* kv, hipStream_t s) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &cap);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone) return NI_OK;
+    if (kv->dirty && kv->dirty_stream != s) {
+        e = hipEventRecord(kv->order, kv->dirty_stream);
+        if (e != hipSuccess) return kv->hip_fail(e, "hipEventRecord(call order)");
+        kv->order_stream = kv->dirty_stream;
+        kv->order_valid = true;
+    }
+    if (kv->order_valid && kv->order_stream != s) {
+        e = hipStreamWaitEvent(s, kv->order, 0);
+        if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(call order)");
+    }
+    kv->dirty = true;
+    kv->dirty_stream = s;
+    return NI_OK;
+}
+
+// Serialise plan P into `blob` and make it reachable from `s`: inside the
+// launch arguments when it fits, else through a staging slot uploaded on the
+// handle's copy stream (`s` waits for the upload).
+int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t s, Offsets* off, PlanRef* ref) {
+    if (int rc = begin_call(kv, s)) return rc;
     *off = layout(P);
     blob.resize(off->total);
     if (!P.app.empty()) memcpy(blob.data() + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
@@ -744,7 +782,7 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
         ref->inl_bytes = (uint32_t)off->total;
         return NI_OK;
     }
-    if (!NI_STAGE_ALL_PLANS && !stage && off->total <= kInlinePlanBytes) {
+    if (off->total <= kInlinePlanBytes) {
         ref->inl = blob.data();
         ref->inl_bytes = (uint32_t)off->total;
         return NI_OK;
@@ -753,20 +791,12 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
     int rc = acquire_slot(kv, off->total, &sl);
     if (rc) return rc;
     memcpy(sl->host, blob.data(), off->total);
-#if NI_PLAN_COPY_STREAM
     hipError_t e = hipMemcpyAsync(sl->dev, sl->host, off->total, hipMemcpyHostToDevice, kv->copy_stream);
     if (e != hipSuccess) return kv->hip_fail(e, "hipMemcpyAsync(plan)");
     e = hipEventRecord(sl->uploaded, kv->copy_stream);
     if (e != hipSuccess) return kv->hip_fail(e, "hipEventRecord(upload)");
-    if (s) {
-        e = hipStreamWaitEvent(s, sl->uploaded, 0);
-        if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
-    }
-#else
-    if (!s) return kv->fail(NI_ERR_BAD_ARG, "a staged plan needs a stream to upload on");
-    hipError_t e = hipMemcpyAsync(sl->dev, sl->host, off->total, hipMemcpyHostToDevice, s);
-    if (e != hipSuccess) return kv->hip_fail(e, "hipMemcpyAsync(plan)");
-#endif
+    e = hipStreamWaitEvent(s, sl->uploaded, 0);
+    if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
     ref->dev = sl->dev;
     ref->slot = sl;
     return NI_OK;
@@ -793,7 +823,7 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
     const size_t pre_floats = (size_t)P.n_pslots * n_lay * H * kPrefillRows * (D + 2);
     float* partials = nullptr;
     if (main_floats + pre_floats > 0) {
-        int rc = ensure_partials(kv, (main_floats + pre_floats) * sizeof(float), &partials);
+        int rc = ensure_partials(kv, (main_floats + pre_floats) * sizeof(float), s, &partials);
         if (rc) return rc;
     }
     if (!P.app.empty() && !P.fused && !P.seq_prefill) {
@@ -1016,6 +1046,7 @@ int ni_kv_create(const ni_kv_opts* opts, ni_kv** out) {
             e = hipEventCreateWithFlags(&kv->ring[i].done, hipEventDisableTiming);
             if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->ring[i].uploaded, hipEventDisableTiming);
         }
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->order, hipEventDisableTiming);
         // Default priority: the copy stream only moves plans.
         if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->copy_stream, hipStreamNonBlocking);
         // The no-allocation entry point's scratch on this device (a failure
@@ -1053,8 +1084,12 @@ void ni_kv_destroy(ni_kv* kv) {
                 (void)hipEventDestroy(pr.second);
             }
         for (hipEvent_t e : kv->ev_pool) (void)hipEventDestroy(e);
+        if (kv->order) (void)hipEventDestroy(kv->order);
         if (kv->partials) (void)hipFree(kv->partials);
-        for (float* p : kv->partials_retired) (void)hipFree(p);
+        for (auto& pr : kv->partials_retired) {
+            (void)hipFree(pr.first);
+            (void)hipEventDestroy(pr.second);
+        }
         if (kv->kpool) (void)hipFree(kv->kpool);
         if (kv->copy_stream) (void)hipStreamDestroy(kv->copy_stream);
     }
@@ -1414,19 +1449,6 @@ int ni_kv_step_begin(ni_kv* kv, const ni_work* work, uint32_t n_work, uint32_t s
     st.placed = false;
     st.ref = PlanRef{};
     st.stream = nullptr;
-#if NI_LAYER_PLAN_STAGED && NI_PLAN_COPY_STREAM
-    // The step's plan goes to device memory once, here, on the handle's copy
-    // stream (the host is usually ahead of the device, so the upload is done
-    // before the first layer's launch waits for it); every layer's launch then
-    // carries only its arguments and the plan's address.
-    if (!kv->host_only && !(st.plan.items.empty() && st.plan.pitems.empty() && st.plan.app.empty())) {
-        if (int rc = place_plan(kv, st.plan, st.blob, nullptr, &st.off, &st.ref, true)) {
-            st.plan.clear();
-            return rc;
-        }
-        if (st.ref.slot) st.ref.slot->held = true;
-    }
-#endif
     st.open = true;
     return NI_OK;
 }
@@ -1454,15 +1476,12 @@ int ni_kv_step_layer(ni_kv* kv, int32_t layer, const float* q, const float* k, c
     if (st.placed && s != st.stream)
         return kv->fail(NI_ERR_BAD_ARG, "every layer of a step must run on the stream of its first layer");
     if (!st.placed) {
-        if (st.ref.slot) {  // uploaded by ni_kv_step_begin: this stream waits for it once
-            hipError_t e = hipStreamWaitEvent(s, st.ref.slot->uploaded, 0);
-            if (e != hipSuccess) return kv->hip_fail(e, "hipStreamWaitEvent(upload)");
-        } else {
-            if (int rc = place_plan(kv, P, st.blob, s, &st.off, &st.ref)) return rc;
-            if (st.ref.slot) st.ref.slot->held = true;
-        }
+        if (int rc = place_plan(kv, P, st.blob, s, &st.off, &st.ref)) return rc;
+        if (st.ref.slot) st.ref.slot->held = true;
         st.placed = true;
         st.stream = s;
+    } else if (int rc = begin_call(kv, s)) {  // (calls on other streams may have come between the layers)
+        return rc;
     }
     return run_placed(kv, P, st.off, st.ref, (uint32_t)layer, 1, k, v, row_stride, 0, q, row_stride, 0, out,
                       out_row_stride, 0, s);
@@ -1474,13 +1493,7 @@ int ni_kv_step_end(ni_kv* kv) {
     if (!st.open) return kv->fail(NI_ERR_BAD_ARG, "no step is open (ni_kv_step_begin)");
     st.open = false;
     int rc = NI_OK;
-    if (st.placed) {
-        rc = release_plan(kv, st.ref, st.stream);
-    } else if (st.ref.slot) {
-        // Uploaded by ni_kv_step_begin but never launched: the slot is free
-        // once its upload has finished.
-        rc = release_plan(kv, st.ref, kv->copy_stream);
-    }
+    if (st.placed) rc = release_plan(kv, st.ref, st.stream);
     if (st.ref.slot) st.ref.slot->held = false;
     st.placed = false;
     st.ref = PlanRef{};
@@ -1667,8 +1680,24 @@ extern "C" {
 int ni_kv_sync(ni_kv* kv, ni_stream stream) {
     if (!kv) return NI_ERR_BAD_ARG;
     if (kv->host_only) return NI_OK;
-    hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+    const hipStream_t s = (hipStream_t)stream;
+    hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess) return kv->hip_fail(e, "hipStreamSynchronize");
+    // The handle's work on `s` is done: no later call needs to wait for it.
+    if (kv->dirty && kv->dirty_stream == s) kv->dirty = false;
+    if (kv->order_valid && kv->order_stream == s) kv->order_valid = false;
+    // Outgrown partials buffers that no enqueued launch can still read.
+    for (size_t i = 0; i < kv->partials_retired.size();) {
+        auto& pr = kv->partials_retired[i];
+        if (hipEventQuery(pr.second) != hipSuccess) {
+            i++;
+            continue;
+        }
+        (void)hipFree(pr.first);
+        kv->ev_pool.push_back(pr.second);
+        pr = kv->partials_retired.back();
+        kv->partials_retired.pop_back();
+    }
     return NI_OK;
 }
 

@@ -52,8 +52,14 @@ int main(int argc, char** argv) {
         else if (!strcmp(a, "--q8")) q8 = true;
         else if (!strcmp(a, "--wfmt")) {  // qkv: f32 (default), f16, q8_0, q4_0
             const char* f = val(a);
-            o.qkv_wformat = !strcmp(f, "f16") ? NI_W_F16 : !strcmp(f, "q8_0") ? NI_W_Q8_0
-                          : !strcmp(f, "q4_0") ? NI_W_Q4_0 : NI_W_F32;
+            if (!strcmp(f, "f32")) o.qkv_wformat = NI_W_F32;
+            else if (!strcmp(f, "f16")) o.qkv_wformat = NI_W_F16;
+            else if (!strcmp(f, "q8_0")) o.qkv_wformat = NI_W_Q8_0;
+            else if (!strcmp(f, "q4_0")) o.qkv_wformat = NI_W_Q4_0;
+            else {
+                fprintf(stderr, "ni_drive: --wfmt must be f32, f16, q8_0 or q4_0 (got \"%s\")\n", f);
+                return 2;
+            }
         }
         else if (!strcmp(a, "--per-layer")) o.launch = NI_DRIVE_PER_LAYER;
         else if (!strcmp(a, "--step-layers")) o.launch = NI_DRIVE_STEP_LAYERS;

@@ -209,7 +209,10 @@ def preset(name: str, steps: int, warmup: int, launch: int = NI_DRIVE_STEP, spli
     o.launch, o.steps, o.warmup, o.split_tokens, o.data_seed, o.profile_mask = launch, steps, warmup, split, seed, \
         profile_mask
     o.ramp = ramp
-    q8 = name.endswith("q8")  # the same workload on a Q8 cache
+    # A trailing "q8" names the same workload on a Q8 cache -- except after
+    # "qkv<rows>", where it names the q8_0 weight format (the fused QKV epilogue
+    # writes f16 pages only).
+    q8 = name.endswith("q8") and not name.startswith("qkv")
     if q8:
         name = name[:-2]
     if name == "config3":

@@ -122,3 +122,18 @@ def test_serve_plan_errors_when_trace_is_exhausted():
     assert cxx.done() == 1 and not a.is_live(0)
     with pytest.raises(RuntimeError, match="every request has finished"):
         cxx.plan()
+
+
+@pytest.mark.parametrize("name,fmt,q8", [("qkv64", 0, False), ("qkv64f16", 1, False), ("qkv64q8", 2, False),
+                                         ("qkv16q4", 3, False), ("config3q8", 0, True), ("config3", 0, False)])
+def test_preset_weight_format_and_q8_suffix(name, fmt, q8):
+    """After "qkv<rows>" a trailing q8 names the q8_0 weight format, not the
+    Q8 KV cache (whose pages the fused QKV epilogue cannot write); elsewhere
+    it names the Q8 cache."""
+    from nanoinfer_amd import _abi
+
+    o = drivers.preset(name, 1, 0)
+    assert bool(o.kv.flags & _abi.NI_KV_Q8) == q8
+    if name.startswith("qkv"):
+        assert o.qkv_wformat == fmt
+        assert o.workload == drivers.NI_DRIVE_QKV

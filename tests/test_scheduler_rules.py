@@ -1,0 +1,217 @@
+"""The C++ serving drivers checked against the reference's scheduling rules,
+stated here as invariants on every iteration of their traces -- not against
+another restatement of the scheduler.
+
+Continuous batching (crates/cli/src/metal_serve.rs:271-359):
+* requests are admitted first come, first served, while a slot is free and
+  the pool's free pages cover pages(prompt + 1) plus one page per running
+  sequence (:283-293); the first request that does not fit stops admission;
+* each iteration lists one decode row per running sequence whose prompt is
+  done, in the order of the running list, before any prefill chunk (:296-304);
+* prefill chunks follow in that order, oldest first, under the budget
+  min(budget, max_rows - decode_rows) (:306-315);
+* a sequence retires exactly when its generated count reaches its output
+  length, and the running list drops it by swap_remove (:337-359).
+Speculative verify (metal_spec.rs:137-163): each round appends g + k drafts
+and queries them all, then truncates to tlen + 1 + accepted.
+
+The request stream and the acceptance draws come from the reference's
+xorshift generator (metal_serve.rs:97-111, seeded as :114), pinned below by
+known answers computed from the recurrence.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import nanoinfer_amd as na
+from nanoinfer_amd import drivers, workloads
+
+M64 = (1 << 64) - 1
+
+
+class Rng:
+    """metal_serve.rs:97-111, :114 (written from the reference for this test)."""
+
+    def __init__(self, seed):
+        self.s = ((seed * 0x9E3779B97F4A7C15) & M64) | 1
+
+    def next(self):
+        self.s ^= (self.s << 13) & M64
+        self.s ^= self.s >> 7
+        self.s ^= (self.s << 17) & M64
+        return self.s
+
+    def unif(self):
+        return (self.next() >> 11) / float(1 << 53)
+
+    def range(self, lo, hi):
+        return lo + self.next() % (hi - lo + 1)
+
+
+# (seed, seeded state, first four outputs of next())
+KNOWN = [
+    (7, 0x538454127B096493, [0xF63F752DD400329A, 0xECCEE9DD2109D47F, 0x7F596005939F3817, 0x905A513B5F3AE3A7]),
+    (5, 0x1715609F7C746C69, [0xBE6F263AAFF8BEF1, 0x1C59458F94CED3CC, 0xF871A22C18FC3D6B, 0x5F4FB9AE07CDFFD1]),
+]
+
+
+@pytest.mark.parametrize("seed,state,outs", KNOWN)
+def test_xorshift_known_answers(seed, state, outs):
+    for gen in (Rng(seed), workloads.XorShift.seeded(seed)):
+        assert gen.s == state
+        assert [gen.next() for _ in range(4)] == outs
+
+
+def requests(seed, n, rate, prompt, out, text_len):
+    """metal_serve.rs:113-126: (arrival, prompt length, output length)."""
+    rng, t, reqs = Rng(seed), 0.0, []
+    for _ in range(n):
+        if rate > 0:
+            t += -math.log(max(rng.unif(), 1e-12)) / rate
+        pl = rng.range(*prompt)
+        rng.range(0, text_len - pl - 1)  # the prompt's text offset
+        reqs.append((t, pl, rng.range(*out)))
+    return reqs
+
+
+def pages(n):
+    return (n + 15) // 16
+
+
+def host(kv_blocks, max_seqs, n_ctx=1024):
+    return na.PagedKv(na.BatchOpts(**workloads.GPT2, kv_blocks=kv_blocks, max_seqs=max_seqs, n_ctx=n_ctx,
+                                   max_rows=512, host_only=True))
+
+
+@pytest.mark.parametrize("cfg", [dict(max_batch=64, budget=256, pool=3080, rate=1.0, prompt=(32, 512), out=(16, 256),
+                                      steps=1200),
+                                 dict(max_batch=8, budget=64, pool=200, rate=0.5, prompt=(32, 512), out=(16, 32),
+                                      steps=1500),
+                                 dict(max_batch=16, budget=40, pool=60, rate=2.0, prompt=(8, 100), out=(1, 12),
+                                      steps=1500, pool_stops=True)],
+                         ids=["config3", "tight-pool", "small-budget"])
+def test_serve_follows_the_reference_rules(cfg):
+    seed, n_req, max_rows = 7, 100000, 512
+    reqs = requests(seed, n_req, cfg["rate"], cfg["prompt"], cfg["out"], 4 * cfg["prompt"][1] + 64)
+    kv = host(cfg["pool"], cfg["max_batch"])
+    drv = drivers.Serve(kv, seed=seed, rate=cfg["rate"], max_batch=cfg["max_batch"], prompt=cfg["prompt"],
+                        out=cfg["out"], budget=cfg["budget"], max_rows=max_rows)
+    live = []          # running sequences in the running list's order
+    req_of, prefilled, generated = {}, {}, {}
+    next_req, clock, retired_prev = 0, 0.0, []
+    seen = {"admit_stopped_by_pool": 0, "partial_chunks": 0, "retired": 0, "budget_full": 0}
+    for it in range(cfg["steps"]):
+        free0 = kv.free_block_count()
+        work, ctx, adm, ret = drv.plan()
+        # the step clock (one tick per iteration; an idle engine jumps to the next arrival)
+        if not live and reqs[next_req][0] > clock:
+            clock = reqs[next_req][0]
+        # retirements of the previous iteration, in the order they were removed
+        assert ret == retired_prev, f"iteration {it}"
+        # admission: first come first served, each with pages(prompt + 1) + running of headroom
+        for k, s in enumerate(adm):
+            arrival, pl, ol = reqs[next_req]
+            assert arrival <= clock, f"iteration {it}: admitted before arriving"
+            assert len(live) < cfg["max_batch"]
+            assert free0 >= pages(pl + 1) + len(live), f"iteration {it}: admitted without headroom"
+            assert s not in req_of
+            req_of[s], prefilled[s], generated[s] = next_req, 0, 0
+            live.append(s)
+            next_req += 1
+        if len(live) < cfg["max_batch"] and reqs[next_req][0] <= clock:
+            # the next request has arrived and a slot is free: the pool stopped it
+            assert free0 < pages(reqs[next_req][1] + 1) + len(live), f"iteration {it}: head of the queue skipped"
+            seen["admit_stopped_by_pool"] += 1
+        # decode rows first, one per running sequence whose prompt is done, in running order
+        done = [s for s in live if prefilled[s] == reqs[req_of[s]][1]]
+        n_dec = len(done)
+        assert [tuple(w) for w in work[:n_dec]] == [(s, 1, 1) for s in done], f"iteration {it}"
+        # then prefill chunks, oldest first, under min(budget, max_rows - decode rows)
+        left = min(cfg["budget"], max_rows - n_dec)
+        chunks = [tuple(w) for w in work[n_dec:]]
+        want = []
+        for s in live:
+            pl = reqs[req_of[s]][1]
+            if prefilled[s] < pl and left > 0:
+                n = min(pl - prefilled[s], left)
+                want.append((s, n, 1 if prefilled[s] + n == pl else 0))
+                left -= n
+        assert chunks == want, f"iteration {it}"
+        assert sum(c[1] for c in chunks) <= min(cfg["budget"], max_rows - n_dec)
+        seen["partial_chunks"] += sum(1 for c in chunks if c[2] == 0)
+        seen["budget_full"] += left == 0
+        for (s, n_new, _), c in zip(work, ctx):
+            assert c == kv.seq_len(int(s)) + n_new
+        # the step's bookkeeping, as ni_kv_step does it
+        for s, n_new, _ in work:
+            kv.reserve(int(s), kv.seq_len(int(s)) + int(n_new))
+            kv.commit(int(s), int(n_new))
+        drv.commit()
+        clock += 1.0
+        for s, n_new, _ in work:
+            s = int(s)
+            pl = reqs[req_of[s]][1]
+            if prefilled[s] < pl:
+                prefilled[s] += int(n_new)
+                if prefilled[s] < pl:
+                    continue  # mid-prompt chunk: no token yet
+            generated[s] += 1
+        # retire exactly at generated == out_len, swap_remove from the running list
+        retired_prev, k = [], 0
+        while k < len(live):
+            s = live[k]
+            assert generated[s] <= reqs[req_of[s]][2]
+            if generated[s] == reqs[req_of[s]][2]:
+                assert not kv.is_live(s), f"iteration {it}: sequence {s} not freed"
+                retired_prev.append(s)
+                del req_of[s]
+                live[k] = live[-1]
+                live.pop()
+                seen["retired"] += 1
+            else:
+                assert kv.is_live(s)
+                k += 1
+        # pages: every running sequence holds exactly pages(seq_len)
+        for s in live:
+            assert len(kv.block_table(s)) == pages(kv.seq_len(s))
+    # the rules above were exercised, not vacuous
+    assert seen["retired"] > 20 and seen["partial_chunks"] > 10 and seen["budget_full"] > 10, seen
+    if cfg.get("pool_stops"):
+        assert seen["admit_stopped_by_pool"] > 0, seen
+
+
+@pytest.mark.parametrize("window", [0, 64])
+def test_spec_follows_the_reference_rules(window):
+    ctx, _ = workloads.config5_contexts()
+    kv = host(32 * 128, 32, n_ctx=2048)
+    seqs = []
+    for L in ctx:
+        s = kv.add_seq()
+        kv.reserve(s, L)
+        kv.commit(s, L)
+        seqs.append(s)
+    base = {s: kv.seq_len(s) for s in seqs}
+    k, seed = 4, 55
+    drv = drivers.Spec(kv, seqs, k=k, seed=seed, window=window)
+    rng = Rng(seed)
+    for rnd in range(200):
+        tlen = {s: kv.seq_len(s) for s in seqs}
+        work, ctx_after = drv.plan()
+        # every sequence appends g + k drafts and queries all of them
+        assert [tuple(w) for w in work] == [(s, k + 1, k + 1) for s in seqs]
+        assert list(ctx_after) == [tlen[s] + k + 1 for s in seqs]
+        for s, n_new, _ in work:
+            kv.reserve(int(s), kv.seq_len(int(s)) + int(n_new))
+            kv.commit(int(s), int(n_new))
+        acc = drv.commit()
+        for s, a in zip(seqs, acc):
+            assert a == rng.range(0, k)  # accepted drafts, drawn from the seeded generator
+            keep = tlen[s] + 1 + a
+            if window and keep > base[s] + window:
+                keep = base[s]  # the request ends and the next takes its slot
+            assert kv.seq_len(s) == keep
+            assert len(kv.block_table(s)) == pages(keep)  # emptied pages freed
+        # pages come back to the pool: the free count is what the lengths leave
+        used = sum(pages(kv.seq_len(s)) for s in seqs)
+        assert kv.free_block_count() == 32 * 128 - used

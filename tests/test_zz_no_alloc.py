@@ -76,7 +76,8 @@ def test_noalloc_equals_step_on_two_calls(gpu):
     # Call 2: fewer, smaller rows, another partition size.
     work2 = [(1, 1, 1), (6, 2, 2), (4, 1, 1)]
     # Call 3: prompt chunks only, every sequence queried at more than 16 rows
-    # and no partitions: the prefill launch appends the rows itself.
+    # and no partitions (on this f16 pool: an append launch, then the prefill
+    # launch; the Q8 test below covers the prefill launch that appends).
     work3 = [(4, 40, 40), (7, 30, 20)]
     for i, (work, split) in enumerate(((work1, 64), (work2, 128), (work3, 1024))):
         n = sum(w[1] for w in work)
@@ -98,6 +99,51 @@ def test_noalloc_equals_step_on_two_calls(gpu):
         assert torch.isfinite(out_a[:, qi]).all()
         assert torch.equal(out_a[:, qi], out_b[:, qi])
         same_state(a, b, seqs)
+
+
+def test_noalloc_q8_prompt_chunks_appended_by_the_prefill_launch(gpu):
+    """A Q8 step of prompt chunks only with 64 x 2 x 12 = 1536 (sequence,
+    layer, head) units: its prefill launch appends each sequence's rows
+    itself (no append launch, checked on the ni_kv_step twin's launch
+    counts); outputs and the stored int8 values and scales bit-identical."""
+    L, H, D = 2, 12, 64
+    C_ = H * D
+    opts = na.BatchOpts(n_layer=L, n_head=H, head_dim=D, kv_blocks=200, max_seqs=64, n_ctx=256, max_rows=2048,
+                        q8=True)
+    a, b = na.PagedKv(opts), na.PagedKv(opts)
+    g = torch.Generator(device="cuda").manual_seed(77)
+    for kv in (a, b):
+        assert [kv.add_seq() for _ in range(64)] == list(range(64))
+    lib = _abi.lib()
+    work = [(s, 17 + (s % 3), 17 + (s % 3)) for s in range(64)]
+    n = sum(w[1] for w in work)
+    q, k, v = (torch.randn((L, n, C_), device="cuda", generator=g) for _ in range(3))
+    out_a = torch.full((L, n, C_), float("nan"), device="cuda")
+    out_b = torch.full((L, n, C_), float("nan"), device="cuda")
+    say(f"no-alloc Q8 prompt chunks: 64 sequences, {n} rows")
+    a.profile([_abi.NI_K_APPEND, _abi.NI_K_ATTN])
+    rc = call(a, lib.ni_kv_step, work, q, k, v, out_a, 0)
+    assert rc == 0, lib.ni_kv_last_error(a.handle).decode()
+    torch.cuda.synchronize()
+    _, n_append = a.profile_read(_abi.NI_K_APPEND)
+    _, n_attn = a.profile_read(_abi.NI_K_ATTN)
+    a.profile([])
+    assert n_append == 0 and n_attn == 1, (n_append, n_attn)
+    free0 = torch.cuda.mem_get_info()[0]
+    rc = call(b, lib.ni_kv_step_noalloc, work, q, k, v, out_b, 0)
+    assert rc == 0, lib.ni_kv_last_error(b.handle).decode()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] >= free0
+    assert torch.isfinite(out_a).all()
+    assert torch.equal(out_a, out_b)
+    for s in range(64):
+        assert a.seq_len(s) == b.seq_len(s) and a.block_table(s) == b.block_table(s)
+    rows = [(s, p) for s in range(64) for p in range(a.seq_len(s))]
+    for i in range(0, len(rows), 1024):
+        ga, gb = a.gather_q8(rows[i:i + 1024]), b.gather_q8(rows[i:i + 1024])
+        for x, y in zip(ga, gb):
+            for xx, yy in zip(x, y):
+                assert torch.equal(xx, yy)
 
 
 def test_noalloc_limits(gpu):
