@@ -432,6 +432,51 @@ def measured_traffic(workload, args, ramp):
     return vals
 
 
+def kv_serving_summary(r, n_iters):
+    """The reference's paged-KV serving figures (metal_serve.rs:320-331,
+    361, 440-464) for the config-3 run -- blocks in use after each step (peak
+    and mean) and the internal fragmentation of the block-table snapshots
+    taken every 10 iterations -- and, beside them, the reference's own
+    recorded run with every request at t = 0 (bench/serving.json, rate=0,
+    via tests/golden/serving_rate0.json) replayed on ni_serve over a
+    host-only handle, which must give the reference's figures exactly."""
+    import nanoinfer_amd as na
+    from nanoinfer_amd import drivers, workloads
+
+    st = r["serve_stats"]
+    out = {"window": f"trace steps 0..{n_iters - 1} (ramp, warmup and timed steps)",
+           "kv_pages_peak": st["kv_pages_peak"], "kv_pages_total": cfg3_pages(),
+           "kv_pages_avg_used": round(st["kv_pages_avg_used"], 1),
+           "kv_pages_avg_weighting": "every iteration the same (step clock; the reference weighs by measured GPU time)",
+           "snapshots": st["snapshots"], "avg_live_seqs": round(st["avg_live_seqs"], 2),
+           "avg_pages_per_seq": round(st["avg_pages_per_seq"], 2),
+           "internal_fragmentation": round(st["internal_fragmentation"], 5)}
+    g = json.load(open(os.path.join(ROOT, "tests", "golden", "serving_rate0.json")))
+    w = g["workload"]
+    kv = na.PagedKv(na.BatchOpts(**workloads.GPT2, kv_blocks=w["kv_pages"], max_seqs=w["max_batch"], n_ctx=1024,
+                                 max_rows=w["max_rows"], host_only=True))
+    sv = drivers.Serve(kv, seed=w["seed"], rate=w["rate"], n_requests=w["requests"], max_batch=w["max_batch"],
+                       prompt=tuple(w["prompt"]), out=tuple(w["output"]), budget=w["prefill_budget"],
+                       max_rows=w["max_rows"])
+    while sv.done() < w["requests"]:
+        work, _, _, _ = sv.plan()
+        for s, n_new, _ in work:
+            kv.reserve(int(s), kv.seq_len(int(s)) + int(n_new))
+            kv.commit(int(s), int(n_new))
+        sv.commit()
+    rs = sv.stats()
+    mine = {"iterations": rs["iterations"], "kv_pages_peak": rs["kv_pages_peak"],
+            "internal_fragmentation": round(rs["internal_fragmentation"], 5),
+            "avg_pages_per_seq": round(rs["avg_pages_per_seq"], 2)}
+    ref = {"iterations": g["continuous"]["iterations"], "kv_pages_peak": g["continuous"]["kv_pages_peak"],
+           "internal_fragmentation": g["kv_stats"]["internal_fragmentation"],
+           "avg_pages_per_seq": g["kv_stats"]["avg_pages_per_seq"]}
+    out["reference_record"] = {"workload": "128 requests at t=0, prompt/output U[16,256], 32 slots, 1032 pages "
+                                           "(bench/serving.json rate=0, M4)",
+                               "reference": ref, "ni_serve_host_replay": mine, "equal": mine == ref}
+    return out
+
+
 def run_config3(args):
     from nanoinfer_amd import drivers
 
@@ -451,6 +496,7 @@ def run_config3(args):
                 "synthetic (seeded N(0,1) q/k/v resident in HBM, seeded Poisson request trace)")
     res["repetitions"] = spread
     res["host_idle_us"] = {"ni_kv_step": round(r["idle_us_plan_call"], 2)}  # per call, device idle
+    res["config"]["kv_serving"] = kv_serving_summary(r, ramp + args.warmup + args.steps)
     res["copy_ceiling"] = copy_ceiling()
     res["stream_ceiling"] = stream_ceiling()
     try:

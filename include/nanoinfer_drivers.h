@@ -75,6 +75,29 @@ int ni_serve_commit(ni_serve* s);
 /* Requests finished so far. */
 uint32_t ni_serve_done(const ni_serve* s);
 
+/* The serving summary of the reference's KV figures (metal_serve.rs:320-331,
+ * 361, 440-464), taken in ni_serve_commit after each iteration's step and
+ * before its retirements, as the reference takes them after b.step:
+ * blocks in use (peak and mean), and every KV_SNAP_EVERY = 10 iterations a
+ * snapshot of the running sequences' lengths and pages.  Internal
+ * fragmentation = 1 - sum(len) / sum(pages * 16) over every snapshot.  On
+ * the step clock every iteration weighs the same in the mean (the reference
+ * weighs it by its measured GPU time).  ni_serve_reset_stats starts a new
+ * window (the next iteration is snapshot 0 of it). */
+typedef struct ni_serve_stats {
+    uint32_t iterations;
+    uint64_t rows;             /* rows appended (decode rows + prompt rows) */
+    uint64_t generated;        /* tokens produced: decode rows + prompts completed */
+    uint32_t kv_pages_peak;
+    double kv_pages_avg_used;
+    uint32_t snapshots;
+    double avg_live_seqs;
+    double avg_pages_per_seq;
+    double internal_fragmentation;
+} ni_serve_stats;
+int ni_serve_get_stats(const ni_serve* s, ni_serve_stats* out);
+int ni_serve_reset_stats(ni_serve* s);
+
 typedef struct ni_spec ni_spec;
 /* Verify driver over sequences that are live and filled: each round appends
  * draft_k + 1 rows to every sequence, all queried. */
@@ -162,6 +185,9 @@ typedef struct ni_drive_result {
      * ni_kv_step_layer; 0 where the launch path makes no such call. */
     double idle_us_plan_call;
     double idle_us_layer_call;
+    /* NI_DRIVE_SERVE: the scheduler's KV summary (ni_serve_get_stats) over
+     * every iteration from the first (ramp included) to the last timed one */
+    ni_serve_stats serve_stats;
 } ni_drive_result;
 
 int ni_drive_run(const ni_drive_opts* opts, ni_drive_result* result);

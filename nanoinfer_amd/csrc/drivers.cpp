@@ -104,6 +104,9 @@ struct ni_serve {
     std::vector<ni_work> work;
     std::vector<uint32_t> ctx, admitted, retired, pending_retired;
     bool planned = false;
+    // summary of the current stats window (ni_serve_get_stats)
+    uint32_t iters = 0, snaps = 0, peak = 0;
+    uint64_t rows = 0, generated = 0, pages_sum = 0, snap_seqs = 0, snap_len = 0, snap_slots = 0;
 };
 
 struct ni_spec {
@@ -221,8 +224,30 @@ int ni_serve_commit(ni_serve* s) {
             if (l.prefilled < reqs[l.req].prompt_len) continue;  // mid-prompt chunk: no token yet
         }
         l.generated++;
+        s->generated++;
     }
     s->clock += 1.0;
+    // metal_serve.rs:320-331: blocks in use after the step, and every
+    // KV_SNAP_EVERY iterations the running sequences' lengths and pages,
+    // before this iteration's retirements.
+    const uint32_t used = ni_kv_blocks_used(s->kv);
+    s->peak = std::max(s->peak, used);
+    s->pages_sum += used;
+    for (const auto& w : s->work) s->rows += w.n_new;
+    if (s->iters % 10 == 0) {
+        for (const auto& l : s->live) {
+            uint32_t len = 0;
+            const uint32_t* pg = nullptr;
+            uint32_t np = 0;
+            if (int rc = ni_kv_seq_len(s->kv, l.seq, &len)) return rc;
+            if (int rc = ni_kv_block_table(s->kv, l.seq, &pg, &np)) return rc;
+            s->snap_len += len;
+            s->snap_slots += (uint64_t)np * NI_KV_BLOCK;
+            s->snap_seqs++;
+        }
+        s->snaps++;
+    }
+    s->iters++;
     size_t k = 0;
     while (k < s->live.size()) {
         const auto& l = s->live[k];
@@ -236,6 +261,29 @@ int ni_serve_commit(ni_serve* s) {
             k++;
         }
     }
+    return NI_OK;
+}
+
+int ni_serve_get_stats(const ni_serve* s, ni_serve_stats* out) {
+    if (!s || !out) return NI_ERR_BAD_ARG;
+    ni_serve_stats r{};
+    r.iterations = s->iters;
+    r.rows = s->rows;
+    r.generated = s->generated;
+    r.kv_pages_peak = s->peak;
+    r.kv_pages_avg_used = s->iters ? (double)s->pages_sum / s->iters : 0.0;
+    r.snapshots = s->snaps;
+    r.avg_live_seqs = s->snaps ? (double)s->snap_seqs / s->snaps : 0.0;
+    r.avg_pages_per_seq = s->snap_seqs ? (double)s->snap_slots / NI_KV_BLOCK / s->snap_seqs : 0.0;
+    r.internal_fragmentation = s->snap_slots ? 1.0 - (double)s->snap_len / (double)s->snap_slots : 0.0;
+    *out = r;
+    return NI_OK;
+}
+
+int ni_serve_reset_stats(ni_serve* s) {
+    if (!s) return NI_ERR_BAD_ARG;
+    s->iters = s->snaps = s->peak = 0;
+    s->rows = s->generated = s->pages_sum = s->snap_seqs = s->snap_len = s->snap_slots = 0;
     return NI_OK;
 }
 
@@ -552,6 +600,7 @@ int run_serve(Runner& r, ni_drive_result* res) {
     ni_serve* sv = nullptr;
     if (int rc = ni_serve_create(r.kv, &r.o.serve, &sv)) return rc;
     double live = 0, ctx = 0;
+    uint32_t timed = 0;
     int rc = timed_run(r, res, [&](Phase ph) -> int {
         ni_serve_iter it{};
         if (int e = ni_serve_plan(sv, &it)) return e;
@@ -565,7 +614,10 @@ int run_serve(Runner& r, ni_drive_result* res) {
                     ctx += it.ctx_after[i];
                 }
         }
-        return ni_serve_commit(sv);
+        if (int e = ni_serve_commit(sv)) return e;
+        // the summary over every iteration up to the last timed one
+        if (ph == TIMED && ++timed == r.o.steps) return ni_serve_get_stats(sv, &res->serve_stats);
+        return NI_OK;
     });
     ni_serve_destroy(sv);
     res->mean_live = live / std::max(1u, r.o.steps);

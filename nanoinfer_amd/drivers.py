@@ -42,13 +42,23 @@ class ni_drive_opts(C.Structure):
                 ("fixed_rows", _u32), ("qkv_wformat", _u32)]
 
 
+class ni_serve_stats(C.Structure):
+    _fields_ = [("iterations", _u32), ("rows", C.c_uint64), ("generated", C.c_uint64), ("kv_pages_peak", _u32),
+                ("kv_pages_avg_used", C.c_double), ("snapshots", _u32), ("avg_live_seqs", C.c_double),
+                ("avg_pages_per_seq", C.c_double), ("internal_fragmentation", C.c_double)]
+
+    def as_dict(self) -> dict:
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
 class ni_drive_result(C.Structure):
     _fields_ = [("seconds", C.c_double), ("gpu_seconds", C.c_double), ("bytes", C.c_double),
                 ("seq_tokens", C.c_double), ("host_us_per_step", C.c_double), ("steps", _u32),
                 ("launches", C.c_uint64), ("mean_live", C.c_double), ("mean_context", C.c_double),
                 ("flops", C.c_double),
                 ("kernel_ms", C.c_double * _abi.NI_K_COUNT), ("kernel_launches", C.c_uint64 * _abi.NI_K_COUNT),
-                ("idle_us_plan_call", C.c_double), ("idle_us_layer_call", C.c_double)]
+                ("idle_us_plan_call", C.c_double), ("idle_us_layer_call", C.c_double),
+                ("serve_stats", ni_serve_stats)]
 
 
 NI_DRIVE_SERVE, NI_DRIVE_SPEC, NI_DRIVE_FIXED, NI_DRIVE_QKV = 0, 1, 2, 3
@@ -70,6 +80,8 @@ def lib():
     L.ni_serve_commit.argtypes = [_vp]
     L.ni_serve_done.argtypes = [_vp]
     L.ni_serve_done.restype = _u32
+    L.ni_serve_get_stats.argtypes = [_vp, C.POINTER(ni_serve_stats)]
+    L.ni_serve_reset_stats.argtypes = [_vp]
     L.ni_spec_create.argtypes = [_vp, C.POINTER(_u32), _u32, _u32, C.c_uint64, C.POINTER(_vp)]
     L.ni_spec_destroy.argtypes = [_vp]
     L.ni_spec_destroy.restype = None
@@ -129,6 +141,16 @@ class Serve:
     def done(self) -> int:
         return int(self._L.ni_serve_done(self._h))
 
+    def stats(self) -> dict:
+        """The KV summary of metal_serve.rs:320-331,440-464 over the current
+        window (ni_serve_get_stats)."""
+        st = ni_serve_stats()
+        _check(self._L.ni_serve_get_stats(self._h, C.byref(st)), "ni_serve_get_stats")
+        return st.as_dict()
+
+    def reset_stats(self):
+        _check(self._L.ni_serve_reset_stats(self._h), "ni_serve_reset_stats")
+
     def __del__(self):
         if getattr(self, "_h", None):
             self._L.ni_serve_destroy(self._h)
@@ -177,6 +199,7 @@ def drive(opts: ni_drive_opts) -> dict:
     r = ni_drive_result()
     _check(lib().ni_drive_run(C.byref(opts), C.byref(r)), "ni_drive_run")
     out = {f: getattr(r, f) for f, _ in ni_drive_result._fields_}
+    out["serve_stats"] = r.serve_stats.as_dict()
     out["kernel_ms"] = list(r.kernel_ms)
     out["kernel_launches"] = list(r.kernel_launches)
     return out

@@ -215,3 +215,42 @@ def test_spec_follows_the_reference_rules(window):
         # pages come back to the pool: the free count is what the lengths leave
         used = sum(pages(kv.seq_len(s)) for s in seqs)
         assert kv.free_block_count() == 32 * 128 - used
+
+
+def test_serve_reproduces_the_reference_serving_record():
+    """The reference's recorded continuous-batching run with every request
+    arriving at t = 0 (bench/serving.json runs['rate=0'], its CLI defaults:
+    seed 7, 128 requests, prompts and outputs U[16,256], 32 slots, budget
+    256, 1032 pages): with no arrivals to wait for, its iterations, rows,
+    KV page peak and block-table snapshot statistics depend only on the
+    request stream, the scheduling policy and the page allocator.  ni_serve
+    on a host-only handle must reproduce them (tests/golden/serving_rate0.json;
+    the figures are the reference's, rounded as it recorded them)."""
+    import json
+    import os
+
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "serving_rate0.json")))
+    w = g["workload"]
+    reqs = requests(w["seed"], w["requests"], w["rate"], tuple(w["prompt"]), tuple(w["output"]), 4 * w["prompt"][1] + 64)
+    assert sum(r[1] for r in reqs) == w["prompt_tokens"] and sum(r[2] for r in reqs) == w["output_tokens"]
+    kv = host(w["kv_pages"], w["max_batch"])
+    drv = drivers.Serve(kv, seed=w["seed"], rate=w["rate"], n_requests=w["requests"], max_batch=w["max_batch"],
+                        prompt=tuple(w["prompt"]), out=tuple(w["output"]), budget=w["prefill_budget"],
+                        max_rows=w["max_rows"])
+    while drv.done() < w["requests"]:
+        work, _, _, _ = drv.plan()
+        for s, n_new, _ in work:
+            kv.reserve(int(s), kv.seq_len(int(s)) + int(n_new))
+            kv.commit(int(s), int(n_new))
+        drv.commit()
+    st = drv.stats()
+    c, k = g["continuous"], g["kv_stats"]
+    assert st["iterations"] == c["iterations"]
+    assert st["rows"] == c["rows_computed"]
+    assert st["generated"] == c["generated_tokens"]
+    assert st["kv_pages_peak"] == c["kv_pages_peak"]
+    assert st["snapshots"] == k["snapshots"]
+    assert round(st["avg_live_seqs"], 2) == k["avg_live_seqs"]
+    assert round(st["avg_pages_per_seq"], 2) == k["avg_pages_per_seq"]
+    assert round(st["internal_fragmentation"], 5) == k["internal_fragmentation"]
+    assert kv.blocks_used() == 0 and kv.free_block_count() == w["kv_pages"]
