@@ -41,31 +41,13 @@ constexpr uint32_t kRingSlots = 4;
 // step's kernels instead of sitting between them.
 // Query groups (matrix-core kernel) take wide workgroups from this many
 // (item, layer, head) units on, instead of splitting into partitions.
-#ifndef NI_WIDE_MIN_GROUP_UNITS
-#define NI_WIDE_MIN_GROUP_UNITS 256
-#endif
-// Prefill groups ordered by sequence (1) or longest first (0): 16 x 512-row
-// prefill 504 -> 463 us per step, the attention launch's L2 hits 2.4M -> 10.4M
-// and misses 15.3M -> 7.3M (rocprofv3 TCC_HIT/TCC_MISS).
-#ifndef NI_PREFILL_SEQ_ORDER
-#define NI_PREFILL_SEQ_ORDER 1
-#endif
+constexpr uint64_t kWideMinGroupUnits = 256;
 // A step of prompt chunks (every sequence queried as prefill groups, no
-// partitions) on a Q8 pool (NI_PREFILL_SEQ_F16: f16 too): the prefill launch
-// appends each sequence's rows (one workgroup per sequence, layer and head,
-// its groups in turn) instead of an append launch before it.
-#ifndef NI_PREFILL_SEQ_APPEND
-#define NI_PREFILL_SEQ_APPEND 1
-#endif
-#ifndef NI_SEQ_PREFILL_MIN_UNITS
-#define NI_SEQ_PREFILL_MIN_UNITS 1536
-#endif
-constexpr uint64_t kSeqPrefillMinUnits = NI_SEQ_PREFILL_MIN_UNITS;
-// 1: all-layer steps whose fused form would append in workgroup prologues take
-// an append launch of their own first (build_step_plan).
-#ifndef NI_SPLIT_PROLOGUE_APPEND
-#define NI_SPLIT_PROLOGUE_APPEND 1
-#endif
+// partitions) on a Q8 pool with at least this many (sequence, layer, head)
+// units: the prefill launch appends each sequence's rows (one workgroup per
+// sequence, layer and head, its groups in turn) instead of an append launch
+// before it (plan_attention).
+constexpr uint64_t kSeqPrefillMinUnits = 1536;
 constexpr size_t kAlign = 256;
 constexpr uint32_t kMinSplit = 64;  // smallest partition the planner uses (tokens)
 constexpr size_t kProfileEvents = 8192;  // events created when profiling starts
@@ -387,8 +369,9 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     };
     std::vector<Group> groups;
     groups.reserve(qr.size());
-    // Runs longer than one matrix tile form prefill groups (f16 pools).
-    const bool prefill = NI_ATTN_MFMA && NI_ATTN_PREFILL && (!is_q8(kv->o) || kv->o.head_dim == 64);
+    // Runs longer than one matrix tile form prefill groups (f16 pools, and Q8
+    // pools at head_dim 64).
+    const bool prefill = !is_q8(kv->o) || kv->o.head_dim == 64;
     const uint32_t max_group = prefill ? kPrefillRows : max_group_rows(kv);
     for (const QRow& r : qr) {
         if (!groups.empty()) {
@@ -425,7 +408,6 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     if (part == 0) {
         constexpr uint64_t kFillWorkgroups = 2048;
         constexpr uint64_t kWideMinUnits = 512;
-        constexpr uint64_t kWideMinGroupUnits = NI_WIDE_MIN_GROUP_UNITS;
         static const uint32_t kChoices[] = {1024, 512, 256, 128};
         pre_part = kLongItem;
         const uint64_t per_unit = (uint64_t)n_lay * kv->o.n_head;
@@ -541,11 +523,13 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         return (x.kv_end - x.kv_begin) > (y.kv_end - y.kv_begin);
     };
     std::stable_sort(P.items.begin(), P.items.end(), longest_first);
-#if NI_PREFILL_SEQ_ORDER
     // Prefill groups of one sequence next to each other (its longest first),
     // sequences by their longest group: a launch's workgroups of one (item,
     // layer, head) are n_lay * n_head apart, so the groups of one sequence
-    // sharing a (layer, head)'s keys then run at about the same time.
+    // sharing a (layer, head)'s keys then run at about the same time (16 x
+    // 512-row prefill 504 -> 463 us per step against longest first; the
+    // attention launch's L2 hits 2.4M -> 10.4M and misses 15.3M -> 7.3M,
+    // rocprofv3 TCC_HIT/TCC_MISS).
     {
         std::vector<uint32_t> longest;  // by table offset (one per sequence)
         for (const AttnItem& it : P.pitems) {
@@ -558,9 +542,6 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
             return (x.kv_end - x.kv_begin) > (y.kv_end - y.kv_begin);
         });
     }
-#else
-    std::stable_sort(P.pitems.begin(), P.pitems.end(), longest_first);
-#endif
     // Prompt-chunk step without partitions: one prefill workgroup per
     // (sequence, layer, head) runs the sequence's groups shortest first, each
     // after appending the new rows up to its last key (the last group: all
@@ -573,7 +554,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     uint32_t n_seqs = 0;
     for (uint32_t i = 0; i < P.pitems.size(); i++) n_seqs += i == 0 || P.pitems[i].tab != P.pitems[i - 1].tab;
     if (P.seq_prefill && (uint64_t)n_seqs * n_lay * kv->o.n_head < kSeqPrefillMinUnits) P.seq_prefill = false;
-    if (P.seq_prefill && NI_PREFILL_SEQ_ORDER && P.items.empty() && P.n_pslots == 0 && !P.pitems.empty()) {
+    if (P.seq_prefill && P.items.empty() && P.n_pslots == 0 && !P.pitems.empty()) {
         uint64_t rows = 0;  // the sequences' new rows: all of the step's, or an append launch
         for (uint32_t i = 0; i < P.pitems.size(); i++)
             if (i == 0 || P.pitems[i].tab != P.pitems[i - 1].tab)
@@ -598,7 +579,7 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     }
     P.seq_prefill = !P.pseqs.empty();
     // Single queries stream on the vector kernel; groups go to matrix cores.
-    P.nq_tile = (NI_ATTN_MFMA && max_nq > 1) ? kMfmaTile : max_nq;
+    P.nq_tile = max_nq > 1 ? kMfmaTile : 1;
     balance_units(kv, P, n_lay);
     return NI_OK;
 }
@@ -1596,7 +1577,7 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
     // launch's extra blocks like a sequence without queries, and all its
     // query groups run in the prefill launch that follows; the others still
     // fuse.
-    const bool prefill = NI_ATTN_MFMA && NI_ATTN_PREFILL && (!is_q8(kv->o) || kv->o.head_dim == 64);
+    const bool prefill = !is_q8(kv->o) || kv->o.head_dim == 64;
     // A step of prompt chunks only keeps the append launch of its own (the
     // plain append kernel moves those rows faster than extra blocks of an
     // attention launch: 16 x 512 prefill 3521 against 3340 GB/s).
@@ -1621,7 +1602,7 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
     // f16 single rows take their rows as their pages stream (no prologue),
     // and stay fused (config 3: 6146 fused against 6118); so does one layer
     // per launch (a second launch per layer: f16 config 5 3808 -> 3411).
-    if (NI_SPLIT_PROLOGUE_APPEND && fused && n_lay > 1) {
+    if (fused && n_lay > 1) {
         constexpr uint64_t kQ8SplitUnits = 8192;
         bool any_group = false, any_single = false, long_rows = false;
         uint64_t units = 0;
@@ -1640,8 +1621,7 @@ static int build_step_plan(ni_kv* kv, const ni_work* work, uint32_t n_work, uint
     // itself (one workgroup per sequence, layer and head), no append launch.
     bool every_big = n_work > 0;
     for (uint32_t w = 0; w < n_work; w++) every_big &= work[w].n_query > max_group_rows(kv);
-    kv->plan.seq_prefill =
-        NI_PREFILL_SEQ_APPEND && prefill && !fused && every_big && (is_q8(kv->o) || NI_PREFILL_SEQ_F16);
+    kv->plan.seq_prefill = prefill && !fused && every_big && is_q8(kv->o);
     uint32_t row = 0;
     for (uint32_t w = 0; w < n_work; w++) {
         const ni_work& it = work[w];

@@ -331,31 +331,15 @@ __global__ __launch_bounds__(256) void stream_kernel(const u32x4* __restrict__ s
 
 // --------------------------------------------------------------- attention
 
-// Tuning knobs of the split kernel (compile-time; the defaults are the
-// measured best on MI355X for the GPT-2 and long-context shapes).
-#ifndef NI_ATTN_WAVES
-#define NI_ATTN_WAVES 4      // waves per workgroup sharing one item's pages
-#endif
-#ifndef NI_ATTN_PAGES
-#define NI_ATTN_PAGES 2      // pages per wave per loop iteration
-#endif
-#ifndef NI_ATTN_PREFETCH
-#define NI_ATTN_PREFETCH 1   // issue the next iteration's loads before computing
-#endif
-#ifndef NI_ATTN_NT
-#define NI_ATTN_NT 1         // non-temporal K/V loads (streamed once per step)
-#endif
-#ifndef NI_ATTN_LDS_PAD
-#define NI_ATTN_LDS_PAD 0    // extra LDS floats per workgroup (caps workgroups per CU)
-#endif
+// Shape of the split kernel's launches (measured best on MI355X for the
+// GPT-2 and long-context shapes).
+constexpr int kWaves = 4;         // waves per workgroup sharing one item's pages
+constexpr int kPagesPerIter = 2;  // pages per wave per loop iteration (head_dim 64)
+constexpr int kPagesD128 = 2;     // the same at head_dim 128
 
-__device__ __forceinline__ u32x4 load16(const u32x4* p) {
-#if NI_ATTN_NT
-    return __builtin_nontemporal_load(p);
-#else
-    return *p;
-#endif
-}
+// K/V loads are non-temporal: each byte is streamed once per step (156 -> 140
+// us per config-3 launch against ordinary loads).
+__device__ __forceinline__ u32x4 load16(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
 // The (item, layer, head) unit workgroup b of an attention launch runs:
 // unit b itself (item-major, b = (item * n_lay + layer) * n_head + head), or
@@ -475,21 +459,23 @@ __device__ __forceinline__ void load_pages(PageRegs<PB, LPP>& r, const uint32_t*
 // keys its key-row group sees; the groups are merged once at the end (wave
 // shuffles, then LDS across waves).
 // Waves per SIMD the wide (8-wave, one-layer) workgroups' registers must allow:
-// with one page per iteration (NI_WIDE_PAGES) the fused kernel fits 80 VGPRs
+// with one page per iteration (kWidePages) the fused kernel fits 80 VGPRs
 // without spilling, so a layer's 768 workgroups of config 3 (64 sequences x
 // 12 heads) are all resident at once instead of 512 and then a tail of 256:
 // one launch per layer 3711 -> 4183 GB/s (two pages per iteration, 119
 // VGPRs, 4 waves per SIMD, before).
-#ifndef NI_WIDE_MIN_WAVES
-#define NI_WIDE_MIN_WAVES 6
-#endif
+constexpr int kWideMinWaves = 6;
+// Pages per wave iteration of the wide launches (two, at 119 VGPRs and 4
+// waves per SIMD: 3711 against 4183 GB/s; separate append + attention calls
+// per layer 3501 against 3780).
+constexpr int kWidePages = 1;
 template <int D, int NQ, int W, int PB, bool FUSED, int INL>
-__global__ __launch_bounds__(64 * W, W == 8 ? NI_WIDE_MIN_WAVES : 1) void attn_split_kernel(const AttnLaunch a,
+__global__ __launch_bounds__(64 * W, W == 8 ? kWideMinWaves : 1) void attn_split_kernel(const AttnLaunch a,
                                                                                             const PlanArg<INL> pa) {
     constexpr int LPK = D / 8;
     constexpr int KPL = 64 / LPK;
     constexpr int LPP = kPage / KPL;
-    __shared__ float red[W][NQ][D + 2 + NI_ATTN_LDS_PAD / (W * NQ)];
+    __shared__ float red[W][NQ][D + 2];
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -574,10 +560,9 @@ __global__ __launch_bounds__(64 * W, W == 8 ? NI_WIDE_MIN_WAVES : 1) void attn_s
     }
 
     for (; pg < pg_end; pg += STRIDE) {
-#if NI_ATTN_PREFETCH
+        // the next iteration's pages in flight while this one computes
         PageRegs<PB, LPP> nxt;
         if (pg + STRIDE < pg_end) load_pages(nxt, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane, nr, kl);
-#endif
         float s[NQ][PB][LPP];
 #pragma unroll
         for (int b = 0; b < PB; b++) {
@@ -634,11 +619,7 @@ __global__ __launch_bounds__(64 * W, W == 8 ? NI_WIDE_MIN_WAVES : 1) void attn_s
                 }
             }
         }
-#if NI_ATTN_PREFETCH
         cur = nxt;
-#else
-        if (pg + STRIDE < pg_end) load_pages(cur, tab, pg + STRIDE, pg_end, kbase, vbase, page_stride, lane, nr, kl);
-#endif
     }
 
     // Merge the KPL key-row groups of the wave (lanes ds, ds+LPK, ...).
@@ -824,9 +805,7 @@ __device__ __forceinline__ float i8f(uint32_t w, int j) { return (float)((int32_
 
 // Pages per wave iteration of attn_q8_kernel: 1 measured 1% faster than 2
 // and 6% faster than 4 on config 3.
-#ifndef NI_Q8_PAGES
-#define NI_Q8_PAGES 1
-#endif
+constexpr int kQ8Pages = 1;
 
 // item_append for a Q8 pool: each aligned group of D/8 threads quantises one
 // (row, K|V) of the head.
@@ -900,7 +879,7 @@ __global__ __launch_bounds__(64 * W) void attn_q8_kernel(const AttnLaunch a, con
     // (streaming them costs ~24 registers, 7 -> 5 waves per SIMD, which all
     // layers in one launch lose: 5202 against 4638 GB/s; one layer per
     // launch gains, 2641 -> 2823).
-    constexpr bool STREAM = D == 64 && W == (int)kWideWavesQ8 && (int)kWideWavesQ8 != NI_ATTN_WAVES;
+    constexpr bool STREAM = D == 64 && W == (int)kWideWavesQ8 && (int)kWideWavesQ8 != kWaves;
     NewRows nr{};
     if constexpr (FUSED) {
         if (it.napp) {
@@ -1125,12 +1104,10 @@ constexpr int kQkvParts = 8;
 // 768 -> 2304: 1 row 4.66 against 7.11 us, 16 rows 6.15 against 7.61 us; from
 // 24 rows its 64-byte row pieces per load lose to the LDS-staged kernel's
 // whole-row reads: 24 rows 8.98 against 7.65 us, 64 rows 11.9 against 9.5).
-#ifndef NI_QKV_SMALL_ROWS
-#define NI_QKV_SMALL_ROWS 16
-#endif
-#ifndef NI_QKV_SMALL_RB
-#define NI_QKV_SMALL_RB 1      // 16-row blocks per workgroup of the small-batch kernel
-#endif
+constexpr uint32_t kQkvSmallRows = 16;
+// 16-row blocks per workgroup of the small-batch kernel (2 and 4 measured
+// 154 and 141 us per 12 layers of 64 rows).
+constexpr int kQkvSmallRb = 1;
 
 // Large row counts: the tile is 32 rows x 16*FB features.  x and W arrive
 // through LDS in chunks of kQkvChunk values of d_in (8 slices, one per
@@ -1488,7 +1465,7 @@ typedef __fp16 v4fp16_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 #define NI_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 // p in [0, 1] enters PV scaled by 2^14 (through the exponent reference:
 // exp2(s - (m - 14))), so that p down to ~4e-9 is a normal f16.
-constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f, kLog2PScale = 14.f;
+constexpr float kPUnscale = 1.f / 16384.f, kLog2PScale = 14.f;
 
 // Groups of 2..16 queries of one sequence (speculative verify, prefill
 // chunks) on matrix cores: one wave per page walks S^T = K Q^T (16 keys x 16
@@ -1504,17 +1481,12 @@ constexpr float kPScale = 16384.f, kPUnscale = 1.f / 16384.f, kLog2PScale = 14.f
 // Waves per SIMD the register allocation must allow at head_dim 64: 4 (<= 128
 // registers, no spills) measured 3.9% faster on config 5 than the
 // unconstrained 3.  (head_dim 128 needs ~250 registers: 2 waves.)
-#ifndef NI_MFMA_MIN_WAVES
-#define NI_MFMA_MIN_WAVES 4
-#endif
-#ifndef NI_MFMA_K_LDS
-#define NI_MFMA_K_LDS 1
-#endif
+constexpr int kMfmaMinWaves = 4;
 // Q8: the pool holds int8 values with a scale per (position, head); K
 // values enter the products as f16 (int8 converts exactly), the key scale
 // multiplies the scores and the value scale multiplies p before its split.
 template <int D, int W, int PB, bool FUSED, int INL, bool Q8>
-__global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_mfma_kernel(const AttnLaunch a,
+__global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma_kernel(const AttnLaunch a,
                                                                                             const PlanArg<INL> pa) {
     constexpr int QC = D / 32;      // 32-dim chunks of the QK product
     constexpr int VC = D / 16;      // 16-dim chunks of the PV product
@@ -1529,8 +1501,10 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     // with 16-byte writes, V^T comes out through transposing reads.
     __shared__ __attribute__((aligned(16))) _Float16 vt[W][PB * kPage * D];
     // f16: K rows load coalesced (as V) and reach the A operand through a
-    // per-wave tile of the same layout.
-    constexpr bool KT = !Q8 && NI_MFMA_K_LDS;
+    // per-wave tile of the same layout (config 5 5684 -> 5852 GB/s against
+    // each lane loading its operand chunk directly; Q8 keeps its direct
+    // 8-byte loads: an int8 tile measured 12% slower).
+    constexpr bool KT = !Q8;
     __shared__ __attribute__((aligned(16))) _Float16 kt[KT ? W : 1][KT ? PB * kPage * D : 8];
 
     const int lane = threadIdx.x & 63;
@@ -1661,10 +1635,10 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
     float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
 #pragma unroll
     for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
-    // Q8: p enters PV as p * vs / vref (at most kPScale after scaling, so its
+    // Q8: p enters PV as p * vs / vref (at most 2^14 after scaling, so its
     // f16 hi never overflows) and the accumulators hold the sum in units of
     // vref: vref starts at 1 (scales up to 1, values up to 127 in magnitude,
-    // leave it there, and the products match p * vs * kPScale bit for bit)
+    // leave it there, and the products match p * vs * 2^14 bit for bit)
     // and follows the largest scale seen beyond that.
     float vref = 1.f, vinv = 1.f;  // vinv = 1 / vref
     _Float16* my_vt = vt[wave];
@@ -1765,7 +1739,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
                 vinv = 1.f / vm;
             }
         }
-        // Weights scaled by kPScale through the exponent reference, so lsum
+        // Weights scaled by 2^14 through the exponent reference, so lsum
         // is in those units too; Q8 weighs p by vs / vref before the split.
         const float mref = mn - kLog2PScale;
         half4_t ph[PB], pl[PB];
@@ -1894,17 +1868,10 @@ __global__ __launch_bounds__(64 * W, D == 64 ? NI_MFMA_MIN_WAVES : 1) void attn_
 // key instead (finite data; their weights are 0), and a wave skips pages
 // past its own last query.  No cross-wave merge: each wave writes its own
 // rows (or their partials when the group is split into partitions).
-#ifndef NI_PREFILL_PAGES
-#define NI_PREFILL_PAGES 2
-#endif
-constexpr int kPrefillPages = NI_PREFILL_PAGES;  // pages per LDS tile
-#ifndef NI_PREFILL_STAGES
-#define NI_PREFILL_STAGES 3
-#endif
-#ifndef NI_PREFILL_MIN_WAVES
-#define NI_PREFILL_MIN_WAVES 1
-#endif
-constexpr int kPrefillStages = NI_PREFILL_STAGES;  // LDS tiles in the ring (3 or 4)
+// Pages per LDS tile (4: 383 against 364 us) and tiles in the ring (a
+// 4-tile ring measured within 2%).
+constexpr int kPrefillPages = 2;
+constexpr int kPrefillStages = 3;
 static_assert(kPrefillStages == 3 || kPrefillStages == 4, "ring of 3 or 4 tiles");
 
 // 16 bytes per lane from g to LDS at the wave-uniform dst + 16 * lane
@@ -1948,7 +1915,7 @@ __device__ __forceinline__ void wait_tiles(uint32_t ahead) {
         __builtin_amdgcn_s_waitcnt(0x0f70);
 }
 
-// QKV projection of mid-size batches (NI_QKV_SMALL_ROWS < n <= NI_QKV_MID_ROWS):
+// QKV projection of mid-size batches (kQkvSmallRows < n <= kQkvMidRows):
 // a workgroup of 8 waves owns a 16-row x 16-feature tile, as
 // qkv_small_kernel with one row block, but x and W reach the matrix cores
 // through LDS.  Loading operands straight into the matrix-core layout reads
@@ -1966,9 +1933,7 @@ __device__ __forceinline__ void wait_tiles(uint32_t ahead) {
 // two kernels -- and the parts meet in LDS, so the bits are the same at
 // every row count.  (A 3-stage DMA ring of chunks instead, two in flight:
 // 103 us per 12 layers at 64 rows, latency-bound.)
-#ifndef NI_QKV_MID_ROWS
-#define NI_QKV_MID_ROWS 64
-#endif
+constexpr uint32_t kQkvMidRows = 64;
 constexpr int kQkvMidChunks = 8;  // chunks of d_in held in registers: d_in up to 1024 on this kernel
 
 template <int INL, int WF, int NC>
@@ -2077,9 +2042,7 @@ __global__ __launch_bounds__(64 * kQkvParts) void qkv_mid_kernel(const QkvLaunch
 // before any is stored, so a prompt's hundreds of rows stream instead of
 // paying a load latency per chunk.  Loads past the end read the last chunk
 // again (in bounds) and are not stored; Q8's D/8-lane groups stay whole.
-#ifndef NI_SEQ_APPEND_UNROLL
-#define NI_SEQ_APPEND_UNROLL 4
-#endif
+constexpr int kSeqAppendUnroll = 4;
 template <int D, bool Q8, int U>
 __device__ __forceinline__ void seq_append(const AttnLaunch& a, const uint8_t* plan, uint32_t app0, uint32_t napp,
                                            uint32_t lay, uint32_t head, uint64_t layer_off, uint32_t nthreads) {
@@ -2124,7 +2087,7 @@ __device__ __forceinline__ void seq_append(const AttnLaunch& a, const uint8_t* p
 }
 
 template <int D, int PT, int INL, bool Q8, bool SEQ>
-__global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_prefill_kernel(const AttnLaunch a,
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
                                                                                              const PlanArg<INL> pa) {
     constexpr int QC = D / 32;              // 32-dim chunks of the QK product
     constexpr int VC = D / 16;              // 16-dim chunks of the PV product
@@ -2167,7 +2130,7 @@ __global__ __launch_bounds__(256, D == 64 ? NI_PREFILL_MIN_WAVES : 1) void attn_
         if (it.napp) {  // rows past the previous item's keys: no wave still reads them
             const uint64_t loff =
                 (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
-            seq_append<D, Q8, NI_SEQ_APPEND_UNROLL>(a, plan, it.app0, it.napp, lay, head, loff, 256);
+            seq_append<D, Q8, kSeqAppendUnroll>(a, plan, it.app0, it.napp, lay, head, loff, 256);
         }
         if (item_i != item0 || it.napp) __syncthreads();  // ring free again; the rows stored
     }
@@ -2596,12 +2559,10 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnLau
     }
 }
 
-constexpr int kWaves = NI_ATTN_WAVES;
-constexpr int kPagesPerIter = NI_ATTN_PAGES;
-#ifndef NI_MFMA_PAGES
-#define NI_MFMA_PAGES 1
-#endif
-constexpr int kMfmaPages = NI_MFMA_PAGES;  // pages per wave iteration of the matrix-core kernel
+// Pages per wave iteration of the matrix-core kernel (two, with the pair's
+// PV through the 32-key product, 154 registers and 3 waves per SIMD: config 5
+// -0.9%, Q8 -3.3%).
+constexpr int kMfmaPages = 1;
 
 // One kernel launch; with timing events the dispatch packet itself records
 // the kernel's start and end (no separate event commands in the stream).
@@ -2630,27 +2591,17 @@ hipError_t with_plan(const L& a, const void* inline_plan, uint32_t inline_bytes,
     return launch(PlanArg<0>{});
 }
 
-// Pages per wave iteration of the wide (one-layer) single-row launches (see
-// NI_WIDE_MIN_WAVES; separate append + attention calls per layer, whose
-// kernel is not fused, 3501 -> 3780 GB/s).
-#ifndef NI_WIDE_PAGES
-#define NI_WIDE_PAGES 1
-#endif
 
 template <int D, int NQ>
 hipError_t attn_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
-    // Several queries per item hold NQ times the softmax state: one page per
-    // iteration keeps their registers (and occupancy) in check.
-#ifndef NI_ATTN_PAGES_D128
-#define NI_ATTN_PAGES_D128 2
-#endif
-    constexpr int PB = NQ > 1 ? 1 : (D == 128 ? NI_ATTN_PAGES_D128 : kPagesPerIter);
+    constexpr int PB = D == 128 ? kPagesD128 : kPagesPerIter;
+    static_assert(NQ == 1, "groups of several rows run on the matrix cores");
     const uint64_t blocks = (uint64_t)a.n_items * a.n_lay * a.pool.n_head + a.n_orphan_blocks;
     if (blocks == 0) return hipSuccess;
     if constexpr (D == 64 && NQ == 1) {
         if (a.wide) {
             constexpr int WW = kWideWaves;
-            constexpr int WPB = NI_WIDE_PAGES;
+            constexpr int WPB = kWidePages;
             return with_plan(a, ip, ib, [&](auto pa) {
                 constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
                 if (a.napp_total || a.n_orphan_blocks)
@@ -2717,11 +2668,7 @@ hipError_t prefill_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hi
                            : go(attn_prefill_kernel<D, PT, INL, true, false>, blocks, 256, s, t, a, pa);
         }
         if (a.pool.q8) return hipErrorInvalidValue;
-#if NI_PREFILL_SEQ_F16
-        if (seq) return go(attn_prefill_kernel<D, PT, INL, false, true>, blocks, 256, s, t, a, pa);
-#else
         if (seq) return hipErrorInvalidValue;  // the host plans sequences on Q8 pools only
-#endif
         return go(attn_prefill_kernel<D, PT, INL, false, false>, blocks, 256, s, t, a, pa);
     });
 }
@@ -2735,7 +2682,7 @@ hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStre
             constexpr int WW = kWideWavesQ8;
             return with_plan(a, ip, ib, [&](auto pa) {
                 constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-                constexpr int PB = NI_Q8_PAGES;
+                constexpr int PB = kQ8Pages;
                 if (a.napp_total || a.n_orphan_blocks)
                     return go(attn_q8_kernel<D, WW, PB, true, INL>, blocks, 64 * WW, s, t, a, pa);
                 return go(attn_q8_kernel<D, WW, PB, false, INL>, blocks, 64 * WW, s, t, a, pa);
@@ -2745,7 +2692,7 @@ hipError_t q8_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hipStre
     if (a.wide) return hipErrorInvalidValue;
     return with_plan(a, ip, ib, [&](auto pa) {
         constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
-        constexpr int PB = NI_Q8_PAGES;
+        constexpr int PB = kQ8Pages;
         if (a.napp_total || a.n_orphan_blocks)
             return go(attn_q8_kernel<D, kWaves, PB, true, INL>, blocks, 64 * kWaves, s, t, a, pa);
         return go(attn_q8_kernel<D, kWaves, PB, false, INL>, blocks, 64 * kWaves, s, t, a, pa);
@@ -2764,24 +2711,11 @@ hipError_t attn_dispatch_nq(const AttnLaunch& a, const void* ip, uint32_t ib, hi
         if (a.nq_tile != 1) return hipErrorInvalidValue;
         return merge ? merge_launch_t<D, 1>(a, ip, ib, s, t) : q8_launch_t<D>(a, ip, ib, s, t);
     }
-#define NI_NQ_CASE(N) \
-    case N: return merge ? merge_launch_t<D, N>(a, ip, ib, s, t) : attn_launch_t<D, N>(a, ip, ib, s, t);
-#if NI_ATTN_MFMA
     // Groups of several rows always take the 16-row matrix tile.
     if (a.nq_tile == kMfmaTile)
         return merge ? merge_launch_t<D, kMfmaTile>(a, ip, ib, s, t) : mfma_launch_t<D, false>(a, ip, ib, s, t);
-    switch (a.nq_tile) {
-        NI_NQ_CASE(1)
-        default: return hipErrorInvalidValue;
-    }
-#else
-    switch (a.nq_tile) {
-        NI_NQ_CASE(1) NI_NQ_CASE(2) NI_NQ_CASE(3) NI_NQ_CASE(4)
-        NI_NQ_CASE(5) NI_NQ_CASE(6) NI_NQ_CASE(7) NI_NQ_CASE(8)
-        default: return hipErrorInvalidValue;
-    }
-#endif
-#undef NI_NQ_CASE
+    if (a.nq_tile != 1) return hipErrorInvalidValue;
+    return merge ? merge_launch_t<D, 1>(a, ip, ib, s, t) : attn_launch_t<D, 1>(a, ip, ib, s, t);
 }
 
 hipError_t attn_dispatch(const AttnLaunch& a, const void* ip, uint32_t ib, hipStream_t s, bool merge,
@@ -2866,12 +2800,12 @@ uint32_t wide_blocks_per_cu(uint32_t head_dim, bool q8, uint32_t nq_tile, bool f
                         : (const void*)attn_mfma_kernel<64, kWideWaves, kMfmaPages, false, INL, false>);
     } else if (nq_tile == 1 && q8) {
         threads = 64 * kWideWavesQ8;
-        f = fused ? (const void*)attn_q8_kernel<64, kWideWavesQ8, NI_Q8_PAGES, true, INL>
-                  : (const void*)attn_q8_kernel<64, kWideWavesQ8, NI_Q8_PAGES, false, INL>;
+        f = fused ? (const void*)attn_q8_kernel<64, kWideWavesQ8, kQ8Pages, true, INL>
+                  : (const void*)attn_q8_kernel<64, kWideWavesQ8, kQ8Pages, false, INL>;
     } else if (nq_tile == 1) {
         threads = 64 * kWideWaves;
-        f = fused ? (const void*)attn_split_kernel<64, 1, kWideWaves, NI_WIDE_PAGES, true, INL>
-                  : (const void*)attn_split_kernel<64, 1, kWideWaves, NI_WIDE_PAGES, false, INL>;
+        f = fused ? (const void*)attn_split_kernel<64, 1, kWideWaves, kWidePages, true, INL>
+                  : (const void*)attn_split_kernel<64, 1, kWideWaves, kWidePages, false, INL>;
     } else {
         return 0;
     }
@@ -2890,8 +2824,8 @@ uint32_t wide_blocks_per_cu(uint32_t head_dim, bool q8, uint32_t nq_tile, bool f
 
 template <int WF>
 hipError_t launch_qkv_t(const QkvLaunch& a, const void* ip, uint32_t ib, hipStream_t s, const LaunchTiming& t) {
-    if (a.n_rows <= NI_QKV_SMALL_ROWS) {
-        constexpr int RB = NI_QKV_SMALL_RB;
+    if (a.n_rows <= kQkvSmallRows) {
+        constexpr int RB = kQkvSmallRb;
         const dim3 grid((a.n_rows + 16 * RB - 1) / (16 * RB), a.n_feat / 16);
         return with_plan(a, ip, ib, [&](auto pa) {
             constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;
@@ -2900,7 +2834,7 @@ hipError_t launch_qkv_t(const QkvLaunch& a, const void* ip, uint32_t ib, hipStre
             return hipGetLastError();
         });
     }
-    if (a.n_rows <= NI_QKV_MID_ROWS && a.d_in <= (uint32_t)(kQkvMidChunks * kQkvChunk)) {
+    if (a.n_rows <= kQkvMidRows && a.d_in <= (uint32_t)(kQkvMidChunks * kQkvChunk)) {
         const dim3 grid((a.n_rows + 15) / 16 * (a.n_feat / 16));  // (row tile, feature tile), dealt by XCD
         return with_plan(a, ip, ib, [&](auto pa) {
             constexpr int INL = sizeof(pa.b) > 4 ? (int)sizeof(pa.b) : 0;

@@ -15,35 +15,22 @@ namespace ni {
 
 constexpr uint32_t kPage = 16;           // positions per page (batch.rs:33)
 constexpr uint32_t kNoSlot = 0xffffffffu; // AttnItem::part_slot: the item is its group's only partition
-// Groups of several queries run on matrix cores (tile of 16 query slots);
-// with NI_ATTN_MFMA=0 they run on the vector kernel in tiles of up to 8.
-#ifndef NI_ATTN_MFMA
-#define NI_ATTN_MFMA 1
-#endif
+// Groups of several queries run on matrix cores (tile of 16 query slots).
 constexpr uint32_t kMfmaTile = 16;
 // Prefill: groups of kMfmaTile+1 .. kPrefillRows consecutive query rows of one
-// sequence run on attn_prefill_kernel (f16 pools), one 16-row tile per wave,
-// every wave reading the same K/V tiles from LDS.
-#ifndef NI_ATTN_PREFILL
-#define NI_ATTN_PREFILL 1
-#endif
+// sequence run on attn_prefill_kernel, one 16-row tile per wave, every wave
+// reading the same K/V tiles from LDS.
 constexpr uint32_t kPrefillRows = 64;
 // Waves per workgroup of a "wide" launch of single-row items: when a launch has
 // too few (item, layer, head) units to fill the GPU, each item's pages are
 // spread over this many waves of one workgroup (merged through LDS) instead of
 // being split into partitions merged by a second kernel.  8 measured best (per
 // layer, config 3: 2900 -> 3464 GB/s f16, 1697 -> 2167 Q8; 16 waves: 3078, 1594).
-#ifndef NI_WIDE_WAVES
-#define NI_WIDE_WAVES 8
-#endif
-constexpr uint32_t kWideWaves = NI_WIDE_WAVES;
+constexpr uint32_t kWideWaves = 8;
 // The same for single rows on the Q8 cache (attn_q8_kernel), one layer per
 // launch config 3: 5 waves 2634 GB/s, 6 2602, 8 2444.
-#ifndef NI_Q8_WIDE_WAVES
-#define NI_Q8_WIDE_WAVES 5
-#endif
-constexpr uint32_t kWideWavesQ8 = NI_Q8_WIDE_WAVES;
-constexpr uint32_t kMaxGroupRows = NI_ATTN_MFMA ? kMfmaTile : 8;  // most query rows sharing one K/V stream
+constexpr uint32_t kWideWavesQ8 = 5;
+constexpr uint32_t kMaxGroupRows = kMfmaTile;  // most query rows sharing one K/V stream
 
 // Where one appended row goes: pool page `page`, position `slot` (0..15) in it.
 struct AppendEntry {
@@ -71,17 +58,12 @@ struct AttnItem {
     uint32_t pad;
 };
 
-// Sequences of prompt-chunk steps (PrefillSeq) on f16 pools too, not only
-// Q8 (measured 1% slower on f16: 16 x 512 prompts 470 against 465 us; Q8
-// 511 against 533).
-#ifndef NI_PREFILL_SEQ_F16
-#define NI_PREFILL_SEQ_F16 0
-#endif
-
-// A sequence of a prompt-chunk step run by one prefill workgroup per (layer,
-// head): its prefill items item0 .. item0 + n_items - 1 in turn, each first
-// appending, for the workgroup's head, the item's new rows (append entries
-// app0 .. app0 + napp - 1 of the item).
+// A sequence of a prompt-chunk step on a Q8 pool run by one prefill
+// workgroup per (layer, head): its prefill items item0 .. item0 + n_items - 1
+// in turn, each first appending, for the workgroup's head, the item's new
+// rows (append entries app0 .. app0 + napp - 1 of the item).  (On f16 pools
+// the same measured 1% slower, 16 x 512 prompts 470 against 465 us, so they
+// take an append launch; Q8 511 against 533.)
 struct PrefillSeq {
     uint32_t item0;
     uint32_t n_items;
@@ -90,9 +72,7 @@ struct PrefillSeq {
 // A group split into n_parts partitions, merged by log-sum-exp.
 // Threads per merge workgroup.
 constexpr int kMergeThreads = 512;
-#ifndef NI_MERGE_SPLIT_MAX
-#define NI_MERGE_SPLIT_MAX 8
-#endif
+constexpr uint32_t kMergeSplitMax = 8;
 // Workgroups that merge one (merge item, layer, head) of nq rows and n_parts
 // partitions: enough that each thread merges at most 4 partitions (the loads
 // of one unrolled batch).  A function of the item alone, so a row's merge
@@ -101,7 +81,7 @@ __host__ __device__ inline uint32_t merge_split_of(uint32_t n_parts, uint32_t nq
     const uint32_t per = nq * D;
     const uint32_t G = per >= (uint32_t)kMergeThreads ? 1u : (uint32_t)kMergeThreads / per;
     uint32_t split = 1;
-    while (split < NI_MERGE_SPLIT_MAX && n_parts > 4 * G * split) split *= 2;
+    while (split < kMergeSplitMax && n_parts > 4 * G * split) split *= 2;
     return split;
 }
 
