@@ -84,6 +84,11 @@ struct Plan {
     bool fused = false;
     bool wide = false;        // kWideWaves waves per attention workgroup
     bool seq_prefill = false; // every row belongs to a sequence queried as prefill groups (see pseqs)
+    // Some launch of the plan reads the append entries `app` (an append
+    // launch, a workgroup prologue, a prefill workgroup's appends); a fused
+    // launch whose items take their new rows as their pages stream and whose
+    // other rows are orphans reads none, and its plan leaves them out.
+    bool app_read = true;
     void clear() {
         app.clear();
         orphans.clear();
@@ -101,6 +106,7 @@ struct Plan {
         napp_total = 0;
         fused = false;
         wide = false;
+        app_read = true;
     }
 };
 
@@ -328,12 +334,13 @@ void balance_units(ni_kv* kv, Plan& P, uint32_t n_lay) {
     if (S == 0 || n_units <= C || n_units > C * S || n_units > 65536) return;
     const uint64_t R = (n_units + C - 1) / C;  // rounds; CUs below `rem` receive R blocks, the others R - 1
     const uint64_t rem = n_units - (R - 1) * C;
-    // cost in 1/16 pages: the item's pages, and 30/16 more per 16 appended rows
+    // cost in 1/16 pages: the item's pages, and ~1.9 pages more per 16
+    // appended rows (2/16 per row)
     std::vector<std::pair<uint64_t, uint32_t>> cost(P.items.size());
     for (uint32_t i = 0; i < P.items.size(); i++) {
         const AttnItem& it = P.items[i];
         const uint64_t pages = (it.kv_end + kPage - 1) / kPage - it.kv_begin / kPage;
-        cost[i] = {16 * pages + 30ull * it.napp, i};
+        cost[i] = {16 * pages + 2ull * it.napp, i};
     }
     std::stable_sort(cost.begin(), cost.end(),
                      [](const std::pair<uint64_t, uint32_t>& x, const std::pair<uint64_t, uint32_t>& y) {
@@ -580,6 +587,11 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
     P.seq_prefill = !P.pseqs.empty();
     // Single queries stream on the vector kernel; groups go to matrix cores.
     P.nq_tile = max_nq > 1 ? kMfmaTile : 1;
+    // Only single rows at head_dim 64 take their new rows as their pages
+    // stream (attn_split_kernel; on Q8 pools its wide launches); every other
+    // fused launch appends in workgroup prologues from the entries.
+    const bool streams = kv->o.head_dim == 64 && P.nq_tile == 1 && (!is_q8(kv->o) || P.wide);
+    P.app_read = !P.fused || P.seq_prefill || !streams;
     balance_units(kv, P, n_lay);
     return NI_OK;
 }
@@ -692,7 +704,7 @@ int ensure_partials(ni_kv* kv, size_t bytes, hipStream_t s, float** out) {
 Offsets layout(const Plan& P) {
     Offsets o;
     o.app = 0;
-    o.orphans = align_up(o.app + P.app.size() * sizeof(AppendEntry), kAlign);
+    o.orphans = align_up(o.app + (P.app_read ? P.app.size() : 0) * sizeof(AppendEntry), kAlign);
     o.items = align_up(o.orphans + P.orphans.size() * sizeof(AppendEntry), kAlign);
     o.merges = align_up(o.items + P.items.size() * sizeof(AttnItem), kAlign);
     o.pitems = align_up(o.merges + P.merges.size() * sizeof(MergeItem), kAlign);
@@ -740,7 +752,8 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
     if (int rc = begin_call(kv, s)) return rc;
     *off = layout(P);
     blob.resize(off->total);
-    if (!P.app.empty()) memcpy(blob.data() + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
+    if (P.app_read && !P.app.empty())
+        memcpy(blob.data() + off->app, P.app.data(), P.app.size() * sizeof(AppendEntry));
     if (!P.orphans.empty())
         memcpy(blob.data() + off->orphans, P.orphans.data(), P.orphans.size() * sizeof(AppendEntry));
     if (!P.items.empty()) memcpy(blob.data() + off->items, P.items.data(), P.items.size() * sizeof(AttnItem));
