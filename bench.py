@@ -258,14 +258,14 @@ def cpu_baseline_cfg3(args, ramp, threads, reps=5):
             "tokens": sum(r[5] for r in recorded), "steps": len(recorded), "threads": runner.threads}
 
 
-def _drive(name, args, launch=None, profile_mask=0, ramp=0):
+def _drive(name, args, launch=None, profile_mask=0, ramp=0, all_prompt_rows=False):
     """One ni_drive_run of a preset: the C++ driver's host loop (the
     scheduler, ni_kv_step and its bookkeeping) with inputs resident in HBM."""
     from nanoinfer_amd import drivers
 
     launch = drivers.NI_DRIVE_STEP if launch is None else launch
     o = drivers.preset(name, args.steps, args.warmup, launch=launch, split=args.split, seed=args.seed,
-                       profile_mask=profile_mask, ramp=ramp)
+                       profile_mask=profile_mask, ramp=ramp, query_all_prompt_rows=all_prompt_rows)
     r = drivers.drive(o)
     gbs = r["bytes"] / r["seconds"] / 1e9
     log(f"bench: {name} launch {launch}{' (profiled)' if profile_mask else ''}: {gbs:.1f} GB/s, "
@@ -563,14 +563,26 @@ def run_config3(args):
 
 # Workloads measured beside the headline in the default run, each over a fixed
 # window (their own steps, not the caller's), so that the driver's run records
-# them too: name -> (steps, warmup, kernel(s) the roofline prices).
+# them too: line -> (preset, steps, warmup, kernel(s) the roofline prices,
+# launch form, every prompt row queried).  "step": one ni_kv_step per step
+# (all layers per launch); "layers": ni_kv_step_begin, one ni_kv_step_layer
+# per layer (the form a model's forward runs, batch.rs:390-416), ni_kv_step_end.
 SECONDARY_LINES = {
-    "config2": (200, 20, "attn_split_kernel (fused append)"),
-    "config4": (100, 10, "attn_split_kernel + attn_merge_kernel"),
-    "config5": (200, 20, "kv_append_kernel + attn_mfma_kernel"),
-    "config3q8": (200, 20, "kv_append_kernel + attn_q8_kernel, Q8 cache"),
-    "prefill": (100, 10, "attn_prefill_kernel (after its append launch)"),
-    "qkv64": (200, 20, "qkv_mid_kernel (append in the epilogue)"),
+    "config2": ("config2", 200, 20, "attn_split_kernel (fused append)", "step", False),
+    "config4": ("config4", 100, 10, "attn_split_kernel + attn_merge_kernel", "step", False),
+    "config5": ("config5", 200, 20, "kv_append_kernel + attn_mfma_kernel", "step", False),
+    "config3q8": ("config3q8", 200, 20, "kv_append_kernel + attn_q8_kernel, Q8 cache", "step", False),
+    "prefill": ("prefill", 100, 10, "attn_prefill_kernel (after its append launch)", "step", False),
+    "qkv64": ("qkv64", 200, 20, "qkv_mid_kernel (append in the epilogue)", "step", False),
+    # every prompt row queried (the reference's attention covers every row of a
+    # step, batch.rs:577-600): decode rows fused, prompt chunks appended by the
+    # same launch's extra blocks, then their prefill launch
+    "config3_all_prompt_rows": ("config3", 200, 20, "attn_split_kernel (fused) + attn_prefill_kernel", "step", True),
+    "config3_per_layer_q8": ("config3q8", 200, 20, "attn_q8_kernel (wide, fused), per layer", "layers", False),
+    "config5_per_layer": ("config5", 200, 20, "attn_mfma_kernel (wide, fused), per layer", "layers", False),
+    "config5_per_layer_q8": ("config5q8", 200, 20, "attn_mfma_kernel (wide, fused), per layer, Q8 cache", "layers",
+                             False),
+    "prefill_per_layer": ("prefill", 50, 5, "kv_append_kernel + attn_prefill_kernel, per layer", "layers", False),
 }
 
 
@@ -580,12 +592,14 @@ def secondary_lines(args, reps=3):
     kernels with per-launch events.  config3q8 runs the headline's trace after
     the same append-only ramp."""
     import argparse as _ap
+    from nanoinfer_amd import drivers
 
     out = {}
-    for name, (steps, warmup, kernel) in SECONDARY_LINES.items():
+    for name, (preset, steps, warmup, kernel, form, all_rows) in SECONDARY_LINES.items():
         a = _ap.Namespace(steps=steps, warmup=warmup, split=0, seed=args.seed)
-        ramp = RAMP_STEPS if name.startswith("config3") else 0
-        runs = [_drive(name, a, ramp=ramp) for _ in range(reps)]
+        ramp = RAMP_STEPS if preset.startswith("config3") else 0
+        launch = drivers.NI_DRIVE_STEP_LAYERS if form == "layers" else drivers.NI_DRIVE_STEP
+        runs = [_drive(preset, a, launch=launch, ramp=ramp, all_prompt_rows=all_rows) for _ in range(reps)]
         gbs = sorted(r["bytes"] / r["seconds"] / 1e9 for r in runs)
         med = gbs[len(gbs) // 2]
         r = runs[[round(r["bytes"] / r["seconds"] / 1e9, 6) for r in runs].index(round(med, 6))]
@@ -593,7 +607,10 @@ def secondary_lines(args, reps=3):
                 "ms_per_step": round(r["seconds"] / r["steps"] * 1e3, 5),
                 "seq_tokens_per_s": round(r["seq_tokens"] / r["seconds"], 1),
                 "algorithmic_bytes_per_step": int(r["bytes"] / r["steps"]), "steps": steps, "warmup": warmup,
-                "ramp_steps": ramp, "reps_gbs": [round(g, 1) for g in gbs]}
+                "ramp_steps": ramp, "reps_gbs": [round(g, 1) for g in gbs],
+                "launch": "one ni_kv_step_layer launch per layer" if form == "layers" else "all layers per launch"}
+        if all_rows:
+            line["prefill_attention"] = "every prompt row queried"
         if name.startswith("qkv"):
             line["tflops"] = round(r["flops"] / r["seconds"] / 1e12, 2)
             mask, ids = 1 << 3, (3,)
@@ -602,7 +619,7 @@ def secondary_lines(args, reps=3):
             # prefill line below takes its attention launch alone
             mask = (1 << 0) | (1 << 1) | (1 << 2)
             ids = (1, 2) if name == "prefill" else (0, 1, 2)
-        rp = _drive(name, a, profile_mask=mask, ramp=ramp)
+        rp = _drive(preset, a, launch=launch, profile_mask=mask, ramp=ramp, all_prompt_rows=all_rows)
         kms = sum(rp["kernel_ms"][i] for i in ids)
         if name == "prefill" and rp["kernel_launches"][0]:
             # the attention launch alone: the step's bytes less its append launch's

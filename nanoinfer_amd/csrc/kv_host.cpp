@@ -19,8 +19,6 @@
 
 #include <algorithm>
 #include <cmath>
-#include <functional>
-#include <queue>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -346,18 +344,23 @@ void balance_units(ni_kv* kv, Plan& P, uint32_t n_lay) {
                      [](const std::pair<uint64_t, uint32_t>& x, const std::pair<uint64_t, uint32_t>& y) {
                          return x.first > y.first;
                      });
-    // (load << 16 | cu): the least loaded CU with a free slot on top
-    std::priority_queue<uint64_t, std::vector<uint64_t>, std::greater<uint64_t>> heap;
-    std::vector<uint32_t> used(C, 0);
-    for (uint64_t c = 0; c < C; c++) heap.push(c);
+    // Longest first, round by round: round r gives block c + r * C to every
+    // CU c that takes one (all but the last round: every CU; the last: CUs
+    // below rem), the largest units of the round to the least loaded CUs.
+    std::vector<uint64_t> load(C, 0);
+    std::vector<uint32_t> cus(C);
     P.order.assign(n_units, 0);
-    for (const auto& ci : cost) {
-        for (uint64_t l = 0; l < lh; l++) {
-            const uint64_t top = heap.top();
-            heap.pop();
-            const uint64_t c = top & 0xffff, load = (top >> 16) + ci.first;
-            P.order[c + C * used[c]] = (uint16_t)(ci.second * lh + l);
-            if (++used[c] < (c < rem ? R : R - 1)) heap.push(load << 16 | c);
+    uint64_t u = 0;  // position in the cost order, (item, unit of the item)
+    for (uint64_t r = 0; r < R; r++) {
+        const uint32_t n_r = (uint32_t)(r + 1 < R ? C : rem);
+        for (uint32_t c = 0; c < n_r; c++) cus[c] = c;
+        if (r > 0)
+            std::stable_sort(cus.begin(), cus.begin() + n_r, [&](uint32_t x, uint32_t y) { return load[x] < load[y]; });
+        for (uint32_t k = 0; k < n_r; k++, u++) {
+            const auto& ci = cost[u / lh];
+            const uint32_t c = cus[k];
+            P.order[c + C * r] = (uint16_t)(ci.second * lh + u % lh);
+            load[c] += ci.first;
         }
     }
 }
