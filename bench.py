@@ -772,7 +772,7 @@ def run_prefill(args):
         tfl = rp["flops"] / steps / t / 1e12
         res["roofline"] = {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_GBS, "unit": "GB/s",
                            "frac": round(gbs / PEAK_GBS, 4), "traffic": None,
-                           "kernel": "attn_prefill_kernel<64,2,q8>" if q8 else "attn_prefill_kernel<64,2>",
+                           "kernel": "attn_prefill_q8_kernel" if q8 else "attn_prefill_kernel<64,2>",
                            "avg_launch_us": round(t * 1e6, 3), "launches": rp["kernel_launches"][1],
                            "algorithmic_bytes_per_launch": int(attn_bytes),
                            "flops_per_launch": int(rp["flops"] / steps), "achieved_tflops": round(tfl, 2),

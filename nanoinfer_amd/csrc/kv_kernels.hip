@@ -17,9 +17,10 @@
 //   attn_mfma_kernel   the same for groups of 2..16 causal query rows of one
 //                      sequence, on the matrix cores
 //   attn_prefill_kernel  groups of 17..64 rows (prompt chunks), K/V tiles DMA'd
-//                      into an LDS ring shared by four waves (attn.metal:100-222);
-//                      in a Q8 step of prompt chunks only, a workgroup runs one
-//                      sequence's groups, appending the rows each needs first
+//                      into an LDS ring shared by four waves (attn.metal:100-222)
+//   attn_prefill_q8_kernel  the same on the Q8 cache; in a step of prompt
+//                      chunks only, a workgroup runs one sequence's groups,
+//                      appending the rows each needs first
 //   attn_q8_kernel     single rows on the int8 + scale (Q8) cache (kv8.metal)
 //   attn_merge_kernel  log-sum-exp merge of partitions (b_attn_merge, :403-424)
 //   qkv_kernel         the QKV projection with the append in its epilogue
@@ -1879,10 +1880,19 @@ static_assert(kPrefillStages == 3 || kPrefillStages == 4, "ring of 3 or 4 tiles"
 // so that the compiler does not add a wait for every DMA in flight before
 // each LDS read it cannot prove disjoint from them: the caller waits
 // (vmcnt) and synchronises itself.  The "memory" clobber and dst as an
-// operand tell the compiler that LDS may change here.
+// operand tell the compiler that LDS may change here.  The s_nop is the one
+// wait state CDNA requires between a scalar write of M0 and an LDS-DMA load
+// reading it; the compiler inserts it for its own code but cannot see into
+// the asm.
 __device__ __forceinline__ void lds_dma16(const void* g, void* dst) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)NI_LDS(dst));
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(m0) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(m0) : "memory", "m0");
+}
+// The same from a wave-uniform base plus a per-lane 32-bit byte offset (the
+// SADDR form: no 64-bit address per lane), to the LDS byte address lds.
+__device__ __forceinline__ void lds_dma16_sbase(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "s"(lds)
+                 : "memory", "m0");
 }
 // The prefill kernel keeps its exponent reference m until some query's max
 // exceeds it by more than kRefSlack (log2 units): weights are then up to
@@ -2086,21 +2096,22 @@ __device__ __forceinline__ void seq_append(const AttnLaunch& a, const uint8_t* p
     }
 }
 
-template <int D, int PT, int INL, bool Q8, bool SEQ>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
-                                                                                             const PlanArg<INL> pa) {
+// Prompt-chunk groups on the Q8 cache (head_dim 64): int8 K/V tiles and
+// their scales by DMA, K converted to f16 after an 8-byte LDS read, V^T
+// through the 8-bit transposing read; p enters PV weighted by the value
+// scales.  SEQ: one workgroup per (sequence, layer, head) running the
+// sequence's groups in turn, each after appending its rows for the head.
+template <int INL, bool SEQ>
+__global__ __launch_bounds__(256) void attn_prefill_q8_kernel(const AttnLaunch a, const PlanArg<INL> pa) {
+    constexpr int D = 64, PT = kPrefillPages;
     constexpr int QC = D / 32;              // 32-dim chunks of the QK product
     constexpr int VC = D / 16;              // 16-dim chunks of the PV product
     constexpr int TK = PT * (int)kPage;     // keys per tile
-    constexpr int CH = D / 8;               // 16-byte chunks per key row
-    constexpr int TH = TK * D;              // halves per K (or V) tile
-    constexpr int CPT = TK * CH / 256;      // chunks of K (and of V) per thread per tile
-    static_assert(TK * CH % 256 == 0, "a tile must split evenly over the workgroup");
-    // A stage: f16, [K | V] tiles of TH halves; Q8, [K int8 | V int8 | K
-    // scales | V scales], TK * D bytes each, then TK floats each.
-    constexpr int QS = 2 * TK * D;          // Q8: byte offset of the K scales in a stage
-    constexpr int SB = Q8 ? QS + 8 * TK : 4 * TH;
-    static_assert(!Q8 || (D == 64 && PT == 2), "Q8 tiles: head_dim 64, two pages");
+    static_assert(PT == 2, "Q8 tiles: two pages");
+    // A stage: [K int8 | V int8 | K scales | V scales], TK * D bytes each,
+    // then TK floats each.
+    constexpr int QS = 2 * TK * D;          // byte offset of the K scales in a stage
+    constexpr int SB = QS + 8 * TK;
     __shared__ __attribute__((aligned(16))) uint8_t ring[kPrefillStages][SB];
 
     const int lane = threadIdx.x & 63;
@@ -2130,7 +2141,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
         if (it.napp) {  // rows past the previous item's keys: no wave still reads them
             const uint64_t loff =
                 (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
-            seq_append<D, Q8, kSeqAppendUnroll>(a, plan, it.app0, it.napp, lay, head, loff, 256);
+            seq_append<D, true, kSeqAppendUnroll>(a, plan, it.app0, it.napp, lay, head, loff, 256);
         }
         if (item_i != item0 || it.napp) __syncthreads();  // ring free again; the rows stored
     }
@@ -2138,11 +2149,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
     const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
 
     const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
-    const uint16_t* kbase = a.pool.k + layer_off;
-    const uint16_t* vbase = a.pool.v + layer_off;
     const uint64_t page_stride = a.pool.page_halves;
-    const uint8_t* kb8 = reinterpret_cast<const uint8_t*>(kbase);  // Q8 pools, in bytes
-    const uint8_t* vb8 = reinterpret_cast<const uint8_t*>(vbase);
+    const uint8_t* kb8 = reinterpret_cast<const uint8_t*>(a.pool.k + layer_off);  // in bytes
+    const uint8_t* vb8 = reinterpret_cast<const uint8_t*>(a.pool.v + layer_off);
     // Page ids through the constant address space: wave-uniform scalar loads,
     // which a wait for the DMA tiles (in order with every vector load) does
     // not depend on.
@@ -2160,14 +2169,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
     // Keys below this are visible to every query of the wave (no masking).
     const uint32_t kfull_w = min(it.kv_end, it.pos0 + r0 + 1);
 
-    // Tile DMA, f16: thread t copies LDS chunks u = t + 256 c (c < CPT) of
-    // each tile (K and V): row u / CH, logical chunk (u % CH) ^ sw --
-    // tile_chunk's inverse.  Every wave issues exactly 2 CPT DMA loads per
-    // tile, so "tile i landed" is "at most the later tiles' 2 CPT loads each
-    // outstanding".  Q8: thread t copies int8 chunk t % 128 of K (waves 0, 1)
-    // or V (waves 2, 3), and lanes 0..15 of wave 0 the 16 chunks of scales
-    // (4 keys each, K then V): one DMA load per tile, wave 0 two.
-    auto issue8 = [&](int st, uint32_t pg) {
+    // Tile DMA: thread t copies int8 chunk t % 128 of K (waves 0, 1) or V
+    // (waves 2, 3), and lanes 0..15 of wave 0 the 16 chunks of scales (4 keys
+    // each, K then V): one DMA load per tile, wave 0 two, so "tile i landed"
+    // is "at most the later tiles' loads outstanding".  A row past the item's
+    // end reads the tile's first row, a key of this item.
+    auto issue = [&](int st, uint32_t pg) {
         uint64_t base[PT];  // bytes
 #pragma unroll
         for (int b = 0; b < PT; b++) base[b] = (uint64_t)tab[min(pg + b, pg_end - 1)] * page_stride * 2;
@@ -2191,37 +2198,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
             lds_dma16((lane < 8 ? kb8 : vb8) + spb + soff, &ring[st][QS]);
         }
     };
-    auto issue = [&](int st, uint32_t pg) {
-        if constexpr (Q8) {
-            issue8(st, pg);
-            return;
-        }
-        // Page bases are wave-uniform (scalar); a row past the end reads
-        // page pg's first row, a key of this item.
-        uint64_t base[PT];
-#pragma unroll
-        for (int b = 0; b < PT; b++) base[b] = (uint64_t)tab[min(pg + b, pg_end - 1)] * page_stride;
-#pragma unroll
-        for (int c = 0; c < CPT; c++) {
-            const uint32_t u = threadIdx.x + 256 * c, dkey = u / CH;
-            const uint32_t dq = u % CH ^ (tile_chunk<CH>(dkey, 0) - dkey * CH);
-            const bool in = pg * kPage + dkey < it.kv_end;
-            uint64_t pb = base[0];
-#pragma unroll
-            for (int b = 1; b < PT; b++)
-                if (in && dkey / kPage == (uint32_t)b) pb = base[b];
-            const uint32_t off = (in ? (dkey % kPage) * D : 0u) + dq * 8;
-            _Float16* const dst = reinterpret_cast<_Float16*>(&ring[st][0]) + (256 * c + 64 * wave) * 8;  // this wave's 1 KB
-            lds_dma16(kbase + pb + off, dst);
-            lds_dma16(vbase + pb + off, dst + TH);
-        }
-    };
     const uint32_t n_tiles = (pg_end - pg_begin + PT - 1) / PT;
 #pragma unroll
     for (int t = 0; t < kPrefillStages - 1; t++)
         if ((uint32_t)t < n_tiles) issue(t, pg_begin + t * PT);
 
-    // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo.
+    // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo
+    // (lo = f16(q - hi) unscaled: the matrix cores take its subnormals
+    // exactly, so both halves accumulate into one product); K^T's int8
+    // values are exact in f16.
     half8_t qh[QC], ql[QC];
     {
         const float* qb = a.q + (int64_t)lay * a.q_layer_stride +
@@ -2236,18 +2221,23 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
                 x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
             }
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                _Float16 h, l;
-                split_f16(x[e] * a.qscale, h, l);
-                qh[c][e] = h;
-                ql[c][e] = l;
+            for (int e = 0; e < 8; e += 2) {
+                float x0 = x[e] * a.qscale, x1 = x[e + 1] * a.qscale;
+                asm("" : "+v"(x0), "+v"(x1));  // the f32 products, as the split's residual sees them
+                uint32_t h, l;
+                split_w16x2(x0, x1, h, l);
+                const half2_t hh = __builtin_bit_cast(half2_t, h), ll = __builtin_bit_cast(half2_t, l);
+                qh[c][e] = hh[0];
+                qh[c][e + 1] = hh[1];
+                ql[c][e] = ll[0];
+                ql[c][e + 1] = ll[1];
             }
         }
     }
     // Weights are exp2(s - mref) with mref = m - kLog2PScalePre: p already
     // scaled by 2^7, and lsum and the accumulators in the same units.
     float m = kMinScore, mref = kMinScore - kLog2PScalePre, lsum = 0.f;
-    // Q8: p enters PV as p * vs / vref and the accumulators hold the sum in
+    // p enters PV as p * vs / vref and the accumulators hold the sum in
     // units of vref, which starts at 1 and follows the largest value scale
     // seen beyond that (as in attn_mfma_kernel): p * vs / vref <= 2^15.
     float vref = 1.f, vinv = 1.f;
@@ -2263,19 +2253,13 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
         // outstanding); after the barrier every wave's part has, and every
         // wave is done with tile ti-1, whose stage the next tile takes.
         const uint32_t ahead = min(n_tiles - 1 - ti, (uint32_t)(kPrefillStages - 2));
-        if constexpr (Q8) {
-            if (wave == 0)
-                wait_tiles<2>(ahead);
-            else
-                wait_tiles<1>(ahead);
-        } else {
-            wait_tiles<2 * CPT>(ahead);
-        }
+        if (wave == 0)
+            wait_tiles<2>(ahead);
+        else
+            wait_tiles<1>(ahead);
         __syncthreads();
         if (ti + kPrefillStages - 1 < n_tiles)
             issue(st == 0 ? kPrefillStages - 1 : st - 1, pg + (kPrefillStages - 1) * PT);
-        const _Float16* const kt = reinterpret_cast<const _Float16*>(&ring[st][0]);
-        const _Float16* const vt = kt + TH;
         const uint8_t* const kt8 = &ring[st][0];
         const uint8_t* const vt8 = kt8 + TK * D;
         const float* const kst = reinterpret_cast<const float*>(&ring[st][QS]);  // Q8 scales
@@ -2290,29 +2274,26 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
                 // S^T = K Q^T: scores of keys 4*rg+j of page b for query col
                 // (also of a page past nb: its rows are finite, its scores
                 // masked below).
-                float4_t st = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+                float4_t st = {0.f, 0.f, 0.f, 0.f};
+                half8_t kh[QC];
 #pragma unroll
-                for (int c = 0; c < QC; c++) {
-                    half8_t kh;
-                    if constexpr (Q8) {  // 8 int8 of the row (chunk 2c + rg/2, half rg%2) as f16
-                        const uint2 w = *reinterpret_cast<const uint2*>(
-                            kt8 + tile_chunk_q8(b * kPage + col, 2 * c + (rg >> 1)) * 16 + (rg & 1) * 8);
-                        kh = __builtin_shufflevector(i8x4_f16(w.x), i8x4_f16(w.y), 0, 1, 2, 3, 4, 5, 6, 7);
-                    } else {
-                        kh = *reinterpret_cast<const half8_t*>(kt + tile_chunk<CH>(b * kPage + col, 4 * c + rg) * 8);
-                    }
-                    st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[c], st, 0, 0, 0);
-                    sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[c], sl, 0, 0, 0);
+                for (int c = 0; c < QC; c++) {  // 8 int8 of the row (chunk 2c + rg/2, half rg%2) as f16
+                    const uint2 w = *reinterpret_cast<const uint2*>(
+                        kt8 + tile_chunk_q8(b * kPage + col, 2 * c + (rg >> 1)) * 16 + (rg & 1) * 8);
+                    kh[c] = __builtin_shufflevector(i8x4_f16(w.x), i8x4_f16(w.y), 0, 1, 2, 3, 4, 5, 6, 7);
                 }
 #pragma unroll
-                for (int j = 0; j < 4; j++) sc[b][j] = st[j] + sl[j] * kLoUnscale;
-                if constexpr (Q8) {  // key scales of keys 4*rg .. 4*rg+3
-                    const float4 ks = *reinterpret_cast<const float4*>(kst + b * kPage + 4 * rg);
-                    sc[b][0] *= ks.x;
-                    sc[b][1] *= ks.y;
-                    sc[b][2] *= ks.z;
-                    sc[b][3] *= ks.w;
-                }
+                for (int c = 0; c < QC; c++) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], qh[c], st, 0, 0, 0);
+#pragma unroll
+                for (int c = 0; c < QC; c++) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], ql[c], st, 0, 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; j++) sc[b][j] = st[j];
+                // key scales of keys 4*rg .. 4*rg+3
+                const float4 ks = *reinterpret_cast<const float4*>(kst + b * kPage + 4 * rg);
+                sc[b][0] *= ks.x;
+                sc[b][1] *= ks.y;
+                sc[b][2] *= ks.z;
+                sc[b][3] *= ks.w;
             }
             if (!full) {
 #pragma unroll
@@ -2344,29 +2325,27 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
                     ol[c] *= alpha;
                 }
             }
-            float4 vs[Q8 ? PT : 1];
-            if constexpr (Q8) {
-                // Value scales of keys 4*rg .. 4*rg+3 of each page; past the
-                // reference vref, move it to the tile's largest (rows of
-                // pages past the end hold other keys' finite scales) and
-                // shrink the accumulators with it.
-                float vm = 0.f;
+            // Value scales of keys 4*rg .. 4*rg+3 of each page; past the
+            // reference vref, move it to the tile's largest (rows of pages
+            // past the end hold other keys' finite scales) and shrink the
+            // accumulators with it.
+            float4 vs[PT];
+            float vm = 0.f;
 #pragma unroll
-                for (int b = 0; b < PT; b++) {
-                    vs[b] = *reinterpret_cast<const float4*>(vst + b * kPage + 4 * rg);
-                    vm = fmaxf(fmaxf(vm, fmaxf(vs[b].x, vs[b].y)), fmaxf(vs[b].z, vs[b].w));
-                }
-                if (__any(vm > vref)) {
-                    vm = rows4_max(vm);
-                    const float f = vref / vm;
+            for (int b = 0; b < PT; b++) {
+                vs[b] = *reinterpret_cast<const float4*>(vst + b * kPage + 4 * rg);
+                vm = fmaxf(fmaxf(vm, fmaxf(vs[b].x, vs[b].y)), fmaxf(vs[b].z, vs[b].w));
+            }
+            if (__any(vm > vref)) {
+                vm = rows4_max(vm);
+                const float f = vref / vm;
 #pragma unroll
-                    for (int c = 0; c < VC; c++) {
-                        o[c] *= f;
-                        ol[c] *= f;
-                    }
-                    vref = vm;
-                    vinv = 1.f / vm;
+                for (int c = 0; c < VC; c++) {
+                    o[c] *= f;
+                    ol[c] *= f;
                 }
+                vref = vm;
+                vinv = 1.f / vm;
             }
             half4_t ph[PT], pl[PT];
             float ps[PT];
@@ -2376,12 +2355,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
 #pragma unroll
                 for (int j = 0; j < 4; j++) p[j] = fast_exp2(sc[b][j] - mref);
                 ps[b] = (p[0] + p[1]) + (p[2] + p[3]);
-                if constexpr (Q8) {
-                    p[0] *= vs[b].x * vinv;
-                    p[1] *= vs[b].y * vinv;
-                    p[2] *= vs[b].z * vinv;
-                    p[3] *= vs[b].w * vinv;
-                }
+                p[0] *= vs[b].x * vinv;
+                p[1] *= vs[b].y * vinv;
+                p[2] *= vs[b].z * vinv;
+                p[3] *= vs[b].w * vinv;
                 uint32_t h0, l0, h1, l1;
                 split_w16x2(p[0], p[1], h0, l0);
                 split_w16x2(p[2], p[3], h1, l1);
@@ -2390,22 +2367,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
             }
 #pragma unroll
             for (int b = 0; b < PT; b++) lsum += ps[b];
-            // O^T += V^T P^T, 16 dims per product.  A lane's V^T operand,
-            // keys 4*rg .. 4*rg+3 of dim c*16 + col of a page, comes from
-            // the row-major tile by a transposing read
-            // (ds_read_b64_tr_b16: within 16 lanes, lane 4t+a reads dims
-            // c*16 + 4a .. +3 of key 4*rg + t and lane 4a'+b' receives
-            // element b' of lanes a', 4+a', 8+a', 12+a', i.e. dim c*16 +
-            // 4a'+b' of keys 4*rg .. 4*rg+3).  Pages go in pairs through the
-            // 32-key product (nearly twice the work per issue of the 16-key
-            // one): k-slot 8*rg + 4*i + j of the pair is key 4*rg + j of its
-            // page i, in both operands.
-            const int vt_t = (lane >> 2) & 3, vt_a = lane & 3;
-            // Q8: one 8-bit transposing read (ds_read_b64_tr_b8: within 16
-            // lanes, lane 2e+a reads bytes 8a .. 8a+7 of its row and lane
-            // 8a'+b' receives byte b' of lanes a', 2+a', .., 14+a') gives
-            // dim c*16 + col of the pair's 8 keys: lane 2e+a reads dims c*16 +
-            // 8a .. of key 4*rg + e of page b (e < 4) or b+1.
+            // O^T += V^T P^T, 16 dims per product, the pages in pairs through
+            // the 32-key product (k-slot 8*rg + 4*i + j of the pair is key
+            // 4*rg + j of its page i, in both operands).  A lane's V^T operand
+            // comes from one 8-bit transposing read (ds_read_b64_tr_b8:
+            // within 16 lanes, lane 2e+a reads bytes 8a .. 8a+7 of its row and
+            // lane 8a'+b' receives byte b' of lanes a', 2+a', .., 14+a'),
+            // giving dim c*16 + col of the pair's 8 keys: lane 2e+a reads dims
+            // c*16 + 8a .. of key 4*rg + e of page b (e < 4) or b+1.
             auto vread8 = [&](int b, int c) {
                 const int e = (lane & 15) >> 1, av = lane & 1;
                 const uint32_t key = (e < 4 ? b : b + 1) * kPage + 4 * rg + (e & 3);
@@ -2414,40 +2383,16 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
                 return __builtin_shufflevector(i8x4_f16((uint32_t)r.x), i8x4_f16((uint32_t)r.y), 0, 1, 2, 3, 4, 5, 6,
                                                7);
             };
-            auto vread = [&](int b, int c) {
-                const _Float16* vp =
-                    vt + tile_chunk<CH>(b * kPage + 4 * rg + vt_t, 2 * c + (vt_a >> 1)) * 8 + (vt_a & 1) * 4;
-                const v4fp16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                    (__attribute__((address_space(3))) v4fp16_t*)(vp));
-                return __builtin_bit_cast(half4_t, r);
-            };
-            if constexpr (PT % 2 == 0) {
 #pragma unroll
-                for (int b = 0; b < PT; b += 2) {
-                    if (b >= (int)nb) break;  // a page past nb has p = 0 and finite V
-                    const half8_t p8h = __builtin_shufflevector(ph[b], ph[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-                    const half8_t p8l = __builtin_shufflevector(pl[b], pl[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+            for (int b = 0; b < PT; b += 2) {
+                if (b >= (int)nb) break;  // a page past nb has p = 0 and finite V
+                const half8_t p8h = __builtin_shufflevector(ph[b], ph[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+                const half8_t p8l = __builtin_shufflevector(pl[b], pl[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-                    for (int c = 0; c < VC; c++) {
-                        half8_t v8;
-                        if constexpr (Q8)
-                            v8 = vread8(b, c);
-                        else
-                            v8 = __builtin_shufflevector(vread(b, c), vread(b + 1, c), 0, 1, 2, 3, 4, 5, 6, 7);
-                        o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8h, o[c], 0, 0, 0);
-                        ol[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, ol[c], 0, 0, 0);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int b = 0; b < PT; b++) {
-                    if (b >= (int)nb) break;
-#pragma unroll
-                    for (int c = 0; c < VC; c++) {
-                        const half4_t v4 = vread(b, c);
-                        o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph[b], o[c], 0, 0, 0);
-                        ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl[b], ol[c], 0, 0, 0);
-                    }
+                for (int c = 0; c < VC; c++) {
+                    const half8_t v8 = vread8(b, c);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8h, o[c], 0, 0, 0);
+                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, ol[c], 0, 0, 0);
                 }
             }
         }
@@ -2459,7 +2404,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
     const uint32_t row = it.row0 + r0 + col;
     if (it.part_slot == kNoSlot) {
         float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)row * a.out_row_stride + head * D;
-        const float scale = vref / lsum;  // lsum and o both carry the 2^7; Q8: o in units of vref
+        const float scale = vref / lsum;  // lsum and o both carry the 2^7; o in units of vref
 #pragma unroll
         for (int c = 0; c < VC; c++) {
             float4 y;
@@ -2482,6 +2427,319 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnLaunch a,
     }
     }  // qok
     }  // items
+}
+
+// Prompt-chunk groups on f16 pools: the tiles, ring and products of
+// attn_prefill_q8_kernel (64-row groups, four 16-query waves, K/V tiles by
+// LDS DMA through a 3-tile ring, q and p split into f16 hi + lo on the
+// matrix cores), with the per-tile work cut to what the products need:
+//  * a wave's rows of a tile lie in one page (64 / CH rows per wave), so its
+//    DMA takes a scalar page base plus a fixed per-lane offset (the
+//    global_load_lds SADDR form: no per-lane address arithmetic), the page id
+//    read by v_readlane from a register holding 64 of the item's page ids;
+//  * the loop body is instantiated once per ring stage, so every LDS address
+//    is a per-lane constant plus an immediate offset;
+//  * scores come out of the QK product already relative to the exponent
+//    reference (its negation is the accumulator's initial value), and the
+//    per-tile test of "some score moved more than kRefSlack above the
+//    reference" is a per-lane max against a constant; the cross-lane max
+//    and the rescale run only when it fires (and on a wave's first tile,
+//    which sets the reference);
+//  * each query's sum of weights accumulates on the matrix cores (the
+//    weights times a V^T of ones), in the same f16 hi + lo parts as PV.
+// The prologue issues the item's q rows and page ids together, then the
+// first tiles' DMA, then splits q while those land.  One workgroup per
+// (head, layer, item): blockIdx.x, .y, .z.
+template <int ST>
+struct RingStage {
+    static constexpr int value = ST;
+};
+
+template <int D, int PT, int INL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 5 : 1, 8))) void attn_prefill_kernel(
+    const AttnLaunch a, const PlanArg<INL> pa) {
+    constexpr int QC = D / 32;           // 32-dim chunks of the QK product
+    constexpr int VC = D / 16;           // 16-dim chunks of the PV product
+    constexpr int TK = PT * (int)kPage;  // keys per tile
+    constexpr int CH = D / 8;            // 16-byte chunks per key row
+    constexpr int TH = TK * D;           // halves per K (or V) tile
+    constexpr int SB = 4 * TH;           // bytes per ring stage: K tile, V tile
+    constexpr int NS = kPrefillStages;
+    constexpr int WR = 64 / CH;          // tile rows one wave's DMA covers
+    static_assert(TK * CH == 256, "one 16-byte chunk of K and one of V per thread per tile");
+    static_assert(kPage % WR == 0, "a wave's DMA rows lie in one page");
+    constexpr float kHi = kRefSlack + kLog2PScalePre;  // scores relative to the reference past this
+    __shared__ __attribute__((aligned(16))) uint8_t ring[NS][SB];
+
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t head = blockIdx.x, lay = blockIdx.y;
+    const uint8_t* plan = plan_base(pa, a.plan);
+    const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[blockIdx.z];
+    const int col = lane & 15;  // query slot of S^T / O^T columns
+    const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
+
+    const uint64_t layer_off = (uint64_t)(a.layer0 + lay) * a.pool.layer_halves + (uint64_t)head * a.pool.head_halves;
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.pool.k + layer_off);
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.pool.v + layer_off);
+    const uint64_t page_bytes = 2 * a.pool.page_halves;
+    const __attribute__((address_space(4))) uint32_t* tab =
+        (const __attribute__((address_space(4))) uint32_t*)(plan + a.off_table) + it.tab;
+    const uint32_t pg_begin = it.kv_begin / kPage;
+    const uint32_t pg_end = (it.kv_end + kPage - 1) / kPage;
+    const uint32_t n_tiles = (pg_end - pg_begin + PT - 1) / PT;
+
+    // This wave's queries: rows r0 .. r0+nqw-1 of the group.
+    const uint32_t r0 = wave * 16;
+    const uint32_t nqw = it.nq > r0 ? min(16u, it.nq - r0) : 0u;
+    const bool qok = col < (int)nqw;
+    const uint32_t qpos = it.pos0 + r0 + col;
+    const uint32_t kend_w = min(it.kv_end, it.pos0 + r0 + nqw);  // keys this wave needs end here
+    const uint32_t kfull_w = min(it.kv_end, it.pos0 + r0 + 1);   // keys below this: visible to all its queries
+
+    // q rows and 64 page ids (from the item's first page) in one round trip.
+    float4 xq[2 * QC];
+    {
+        const float* qb = a.q + (int64_t)lay * a.q_layer_stride +
+                          (int64_t)(it.row0 + r0 + (qok ? col : 0)) * a.q_row_stride + head * D + 8 * rg;
+#pragma unroll
+        for (int c = 0; c < QC; c++) {
+            xq[2 * c] = reinterpret_cast<const float4*>(qb + c * 32)[0];
+            xq[2 * c + 1] = reinterpret_cast<const float4*>(qb + c * 32)[1];
+        }
+    }
+    uint32_t id_base = pg_begin;
+    uint32_t ids = tab[min(id_base + (uint32_t)lane, pg_end - 1)];
+    // The loads land before the DMA below is issued (its waits count DMA loads only).
+#pragma unroll
+    for (int c = 0; c < 2 * QC; c++) asm volatile("" : : "v"(xq[c].x), "v"(xq[c].y), "v"(xq[c].z), "v"(xq[c].w));
+    asm volatile("" : : "v"(ids));
+
+    // Tile DMA: thread t copies LDS chunk t of the tile's K and of its V (row
+    // t / CH, logical chunk (t % CH) ^ sw, tile_chunk's inverse); a row past
+    // the item's end copies row 0 of its page (a key of this item).
+    const uint32_t wb = (64 * wave / CH) / kPage;  // this wave's page within a tile
+    const uint32_t dk = threadIdx.x / CH;
+    const uint32_t doff0 = ((threadIdx.x % CH) ^ (tile_chunk<CH>(dk, 0) - dk * CH)) * 16;  // bytes, in row 0
+    const uint32_t doff = doff0 + (dk % kPage) * D * 2;
+    const uint32_t lds_ring = (uint32_t)(uintptr_t)NI_LDS(&ring[0][0]) + 1024 * wave;  // this wave's 1 KB of stage 0
+    auto issue = [&](auto stc, uint32_t pg) {
+        constexpr int S = decltype(stc)::value;
+        const uint32_t idx = pg + wb;
+        const bool inr = idx < pg_end;
+        const uint32_t want = inr ? idx : pg;
+        if (want >= id_base + 64) {  // past the window of page ids (items over 64 pages)
+            id_base = pg;
+            ids = tab[min(id_base + (uint32_t)lane, pg_end - 1)];
+            asm volatile("" : : "v"(ids));
+        }
+        const uint32_t pid = __builtin_amdgcn_readlane(ids, want - id_base);
+        const uint64_t pb = (uint64_t)pid * page_bytes;
+        uint32_t off = doff;
+        if ((pg + PT) * kPage > it.kv_end) off = inr && pg * kPage + dk < it.kv_end ? doff : doff0;
+        lds_dma16_sbase(kbase + pb, off, lds_ring + S * SB);
+        lds_dma16_sbase(vbase + pb, off, lds_ring + S * SB + 2 * TH);
+    };
+    if (n_tiles > 0) issue(RingStage<0>{}, pg_begin);
+    if (n_tiles > 1) issue(RingStage<1>{}, pg_begin + PT);
+
+    // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo
+    // (lo = f16(q - hi) unscaled: the matrix cores take its subnormals
+    // exactly, so both halves accumulate into one product).
+    half8_t qh[QC], ql[QC];
+#pragma unroll
+    for (int c = 0; c < QC; c++) {
+        const float x[8] = {xq[2 * c].x, xq[2 * c].y, xq[2 * c].z, xq[2 * c].w,
+                            xq[2 * c + 1].x, xq[2 * c + 1].y, xq[2 * c + 1].z, xq[2 * c + 1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            float x0 = qok ? x[e] * a.qscale : 0.f, x1 = qok ? x[e + 1] * a.qscale : 0.f;
+            asm("" : "+v"(x0), "+v"(x1));  // the f32 products, as the split's residual sees them
+            uint32_t h, l;
+            split_w16x2(x0, x1, h, l);
+            const half2_t hh = __builtin_bit_cast(half2_t, h), ll = __builtin_bit_cast(half2_t, l);
+            qh[c][e] = hh[0];
+            qh[c][e + 1] = hh[1];
+            ql[c][e] = ll[0];
+            ql[c][e + 1] = ll[1];
+        }
+    }
+    // Weights are exp2(s - mref): mref = m - kLog2PScalePre for the running
+    // reference m, so p enters PV scaled by 2^7 (at most 2^15).  The scores
+    // come out of QK as s - mref (the product's accumulator starts at -mref).
+    float mref = 0.f;
+    float4_t negref = {0.f, 0.f, 0.f, 0.f};
+    float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
+#pragma unroll
+    for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float4_t lacc = {0.f, 0.f, 0.f, 0.f};  // sum of weights (every lane of a query column)
+    const half8_t ones8 = {1, 1, 1, 1, 1, 1, 1, 1};
+    const half4_t ones4 = {1, 1, 1, 1};
+    // Per-lane LDS offsets (bytes in a stage): K operand chunk 4c + rg of row
+    // col of page 0 (page b: + b * kPage * CH chunks, the same swizzle), V^T
+    // operand of the transposing read (ds_read_b64_tr_b16: within 16 lanes,
+    // lane 4t+a reads dims c*16 + 4a .. +3 of key 4*rg + t).
+    uint32_t koff[QC], voff[VC];
+    const int vt_t = (lane >> 2) & 3, vt_a = lane & 3;
+#pragma unroll
+    for (int c = 0; c < QC; c++) koff[c] = tile_chunk<CH>(col, 4 * c + rg) * 16;
+#pragma unroll
+    for (int c = 0; c < VC; c++)
+        voff[c] = 2 * TH + tile_chunk<CH>(4 * rg + vt_t, 2 * c + (vt_a >> 1)) * 16 + (vt_a & 1) * 8;
+
+    auto tile = [&](auto stc, uint32_t ti) {
+        constexpr int S = decltype(stc)::value;
+        const uint32_t pg = pg_begin + ti * PT;
+        // This wave's part of tile ti has landed (vmcnt is in order: only
+        // the two loads of each later tile already issued may still be
+        // outstanding); after the barrier every wave's part has, and every
+        // wave is done with tile ti-1, whose stage the next tile takes.
+        wait_tiles<2>(min(n_tiles - 1 - ti, (uint32_t)(NS - 2)));
+        __syncthreads();
+        if (ti + NS - 1 < n_tiles) issue(RingStage<(S + NS - 1) % NS>{}, pg + (NS - 1) * PT);
+        if (pg * kPage >= kend_w) return;  // wave-uniform: no key of the tile for this wave
+        const uint8_t* const st_base = &ring[S][0];
+        const uint32_t nb = min((uint32_t)PT, (kend_w - pg * kPage + kPage - 1) / kPage);
+        float sc[PT][4];
+#pragma unroll
+        for (int b = 0; b < PT; b++) {
+            half8_t kh[QC];
+#pragma unroll
+            for (int c = 0; c < QC; c++)
+                kh[c] = *reinterpret_cast<const half8_t*>(st_base + koff[c] + b * kPage * CH * 16);
+            float4_t acc = negref;
+#pragma unroll
+            for (int c = 0; c < QC; c++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], qh[c], acc, 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < QC; c++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[c], ql[c], acc, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; j++) sc[b][j] = acc[j];
+        }
+        if ((pg + PT) * kPage > kfull_w) {  // some key is hidden from some query of the wave
+#pragma unroll
+            for (int b = 0; b < PT; b++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t key = (pg + b) * kPage + 4 * rg + j;
+                    const bool ok = qok && b < (int)nb && key < it.kv_end && key <= qpos;
+                    sc[b][j] = ok ? sc[b][j] : -INFINITY;
+                }
+        }
+        float lm = sc[0][0];
+#pragma unroll
+        for (int b = 0; b < PT; b++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) lm = fmaxf(lm, sc[b][j]);
+        if (ti == 0 || __any(lm > kHi)) {
+            // Column max relative to the reference; the first tile moves the
+            // reference to it, later ones only up, and only past the slack.
+            const float mx = rows4_max(lm) - kLog2PScalePre;
+            // (a column with no visible key keeps a finite reference)
+            const float d = fmaxf(ti == 0 ? mx : fmaxf(mx, 0.f), -65536.f);
+            if (ti != 0) {
+                const float alpha = fast_exp2(-d);
+                lacc *= alpha;
+#pragma unroll
+                for (int c = 0; c < VC; c++) {
+                    o[c] *= alpha;
+                    ol[c] *= alpha;
+                }
+            }
+            mref += d;
+            negref = float4_t{-mref, -mref, -mref, -mref};
+#pragma unroll
+            for (int b = 0; b < PT; b++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) sc[b][j] -= d;
+        }
+        half4_t ph[PT], pl[PT];
+#pragma unroll
+        for (int b = 0; b < PT; b++) {
+            float p[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) p[j] = fast_exp2(sc[b][j]);
+            uint32_t h0, l0, h1, l1;
+            split_w16x2(p[0], p[1], h0, l0);
+            split_w16x2(p[2], p[3], h1, l1);
+            ph[b] = __builtin_bit_cast(half4_t, u32x2_t{h0, h1});
+            pl[b] = __builtin_bit_cast(half4_t, u32x2_t{l0, l1});
+        }
+        // O^T += V^T P^T, 16 dims per product; pages in pairs through the
+        // 32-key product (k-slot 8*rg + 4*i + j of the pair is key 4*rg + j
+        // of its page i, in both operands).
+        auto vread = [&](int b, int c) {
+            const v4fp16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                (__attribute__((address_space(3))) v4fp16_t*)(st_base + voff[c] + b * kPage * CH * 16));
+            return __builtin_bit_cast(half4_t, r);
+        };
+        if constexpr (PT % 2 == 0) {
+#pragma unroll
+            for (int b = 0; b < PT; b += 2) {
+                if (b >= (int)nb) break;  // a page past nb has p = 0 and finite V
+                const half8_t p8h = __builtin_shufflevector(ph[b], ph[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+                const half8_t p8l = __builtin_shufflevector(pl[b], pl[b + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int c = 0; c < VC; c++) {
+                    const half8_t v8 = __builtin_shufflevector(vread(b, c), vread(b + 1, c), 0, 1, 2, 3, 4, 5, 6, 7);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8h, o[c], 0, 0, 0);
+                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, ol[c], 0, 0, 0);
+                }
+                lacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones8, p8h, lacc, 0, 0, 0);
+                lacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones8, p8l, lacc, 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < PT; b++) {
+                if (b >= (int)nb) break;
+#pragma unroll
+                for (int c = 0; c < VC; c++) {
+                    const half4_t v4 = vread(b, c);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, ph[b], o[c], 0, 0, 0);
+                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(v4, pl[b], ol[c], 0, 0, 0);
+                }
+                lacc = __builtin_amdgcn_mfma_f32_16x16x16f16(ones4, ph[b], lacc, 0, 0, 0);
+                lacc = __builtin_amdgcn_mfma_f32_16x16x16f16(ones4, pl[b], lacc, 0, 0, 0);
+            }
+        }
+    };
+    for (uint32_t ti = 0; ti < n_tiles;) {
+        tile(RingStage<0>{}, ti);
+        if (++ti == n_tiles) break;
+        tile(RingStage<1>{}, ti);
+        if (++ti == n_tiles) break;
+        tile(RingStage<2>{}, ti);
+        ++ti;
+    }
+    static_assert(kPrefillStages == 3, "the loop body is instantiated per ring stage");
+
+    if (!qok) return;
+    const float lsum = lacc[0];
+    const uint32_t row = it.row0 + r0 + col;
+    if (it.part_slot == kNoSlot) {
+        float* dst = a.out + (int64_t)lay * a.out_layer_stride + (int64_t)row * a.out_row_stride + head * D;
+        const float scale = 1.f / lsum;  // lsum and o both carry the 2^7
+#pragma unroll
+        for (int c = 0; c < VC; c++) {
+            float4 y;
+            y.x = (o[c][0] + ol[c][0]) * scale;
+            y.y = (o[c][1] + ol[c][1]) * scale;
+            y.z = (o[c][2] + ol[c][2]) * scale;
+            y.w = (o[c][3] + ol[c][3]) * scale;
+            *reinterpret_cast<float4*>(dst + c * 16 + 4 * rg) = y;
+        }
+    } else {
+        // (m, l, o) with l and o in units of exp2(s - m), m = mref + 2^7's
+        // exponent; a row with no key of the partition weighs nothing.
+        float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * gridDim.x + head) * kPrefillRows + r0 + col) * (D + 2);
+        if (rg == 0) {
+            p[0] = lsum > 0.f ? mref + kLog2PScalePre : kMinScore;
+            p[1] = lsum * kPUnscalePre;
+        }
+#pragma unroll
+        for (int c = 0; c < VC; c++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) p[2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j]) * kPUnscalePre;
+    }
 }
 
 // One workgroup per (merge item, layer, head).  Thread t owns output unit
@@ -2664,12 +2922,15 @@ hipError_t prefill_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hi
         const bool seq = a.n_pseqs != 0;
         if constexpr (D == 64 && PT == 2) {
             if (a.pool.q8)
-                return seq ? go(attn_prefill_kernel<D, PT, INL, true, true>, blocks, 256, s, t, a, pa)
-                           : go(attn_prefill_kernel<D, PT, INL, true, false>, blocks, 256, s, t, a, pa);
+                return seq ? go(attn_prefill_q8_kernel<INL, true>, blocks, 256, s, t, a, pa)
+                           : go(attn_prefill_q8_kernel<INL, false>, blocks, 256, s, t, a, pa);
         }
         if (a.pool.q8) return hipErrorInvalidValue;
         if (seq) return hipErrorInvalidValue;  // the host plans sequences on Q8 pools only
-        return go(attn_prefill_kernel<D, PT, INL, false, false>, blocks, 256, s, t, a, pa);
+        if (a.n_items > 65535 || a.n_lay > 65535) return hipErrorInvalidValue;  // grid y and z
+        hipExtLaunchKernelGGL(attn_prefill_kernel<D, PT, INL>, dim3(a.pool.n_head, a.n_lay, a.n_items), dim3(256),
+                              0, s, t.start, t.stop, 0, a, pa);
+        return hipGetLastError();
     });
 }
 
