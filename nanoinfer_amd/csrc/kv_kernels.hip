@@ -2830,13 +2830,18 @@ hipError_t go(K kern, uint64_t blocks, uint32_t threads, hipStream_t s, const La
     return hipGetLastError();
 }
 
-// Launch `kern<INL>` with the plan inline (kInlinePlanSmall or
-// kInlinePlanBytes of arguments, the smallest that holds it) or through the
+// Launch `kern<INL>` with the plan inline (kInlinePlanTiny, kInlinePlanSmall
+// or kInlinePlanBytes of arguments, the smallest that holds it) or through the
 // device pointer in the launch struct.
 template <typename L, typename Fn>
 hipError_t with_plan(const L& a, const void* inline_plan, uint32_t inline_bytes, Fn&& launch) {
     if (inline_plan) {
         if (inline_bytes > kInlinePlanBytes) return hipErrorInvalidValue;
+        if (inline_bytes <= kInlinePlanTiny) {
+            PlanArg<kInlinePlanTiny> pa;
+            memcpy(pa.b, inline_plan, inline_bytes);
+            return launch(pa);
+        }
         if (inline_bytes <= kInlinePlanSmall) {
             PlanArg<kInlinePlanSmall> pa;
             memcpy(pa.b, inline_plan, inline_bytes);

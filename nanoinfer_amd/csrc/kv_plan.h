@@ -221,11 +221,14 @@ struct AttnLaunch {
 // kInlinePlanBytes: the runtime copies arguments with the launch, so no
 // separate transfer sits on the stream) or in a device staging buffer.
 // Launch structs locate each part of the plan by its byte offset.  Inline
-// plans go in an argument block of kInlinePlanSmall bytes when they fit,
-// else kInlinePlanBytes: a launch's host cost grows with the block (measured
-// ~3.5 us at 256 B, ~4.1-4.7 us at 16 KB, ~6.0 us at 32 KB), and a
-// per-layer call's plan (64 sequences) is 5-9 KB.
-constexpr uint32_t kInlinePlanBytes = 32768, kInlinePlanSmall = 16384;
+// plans go in the smallest argument block of kInlinePlanTiny,
+// kInlinePlanSmall or kInlinePlanBytes bytes that holds them: a launch's
+// host cost grows with the block (measured ~3.5 us at 256 B, ~4.1-4.7 us at
+// 16 KB, ~6.0 us at 32 KB; back-to-back launches of an empty 768-workgroup
+// kernel every 2.3 us at 1 KB, 2.9 at 2 KB, 3.3 at 4 KB, 4.1 at 8 KB, 3-6 at
+// 16 KB), a per-layer call's plan (64 sequences) is 5-9 KB and a 64-row
+// projection's 1 KB.
+constexpr uint32_t kInlinePlanBytes = 32768, kInlinePlanSmall = 16384, kInlinePlanTiny = 2048;
 
 // Device scratch of the no-allocation entry point (ni_kv_step_noalloc): the
 // split-K partials of its launches, in a file-scope device array of this
