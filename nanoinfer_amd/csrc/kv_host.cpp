@@ -588,6 +588,15 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         }
     }
     P.seq_prefill = !P.pseqs.empty();
+    // f16 prefill items carry their first pages' ids (the prefill kernel
+    // issues its first tiles' DMA from them, beside the item's q and page-id
+    // loads instead of after them).
+    if (!is_q8(kv->o)) {
+        for (AttnItem& it : P.pitems) {
+            const uint32_t pb = it.kv_begin / kPage, pe = (it.kv_end + kPage - 1) / kPage;
+            for (uint32_t i = 0; i < 4; i++) it.first_pages[i] = pe > pb ? P.table[it.tab + std::min(pb + i, pe - 1)] : 0u;
+        }
+    }
     // Single queries stream on the vector kernel; groups go to matrix cores.
     P.nq_tile = max_nq > 1 ? kMfmaTile : 1;
     // Only single rows at head_dim 64 take their new rows as their pages

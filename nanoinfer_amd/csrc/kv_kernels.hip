@@ -2447,9 +2447,9 @@ __global__ __launch_bounds__(256) void attn_prefill_q8_kernel(const AttnLaunch a
 //    which sets the reference);
 //  * each query's sum of weights accumulates on the matrix cores (the
 //    weights times a V^T of ones), in the same f16 hi + lo parts as PV.
-// The prologue issues the item's q rows and page ids together, then the
-// first tiles' DMA, then splits q while those land.  One workgroup per
-// (head, layer, item): blockIdx.x, .y, .z.
+// The prologue issues the first tiles' DMA from the page ids the item
+// carries, the item's q rows and 64 page ids beside it, then splits q while
+// the tiles land.  One workgroup per (head, layer, item): blockIdx.x, .y, .z.
 template <int ST>
 struct RingStage {
     static constexpr int value = ST;
@@ -2497,7 +2497,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 5
     const uint32_t kend_w = min(it.kv_end, it.pos0 + r0 + nqw);  // keys this wave needs end here
     const uint32_t kfull_w = min(it.kv_end, it.pos0 + r0 + 1);   // keys below this: visible to all its queries
 
-    // q rows and 64 page ids (from the item's first page) in one round trip.
+
+    // Tile DMA: thread t copies LDS chunk t of the tile's K and of its V (row
+    // t / CH, logical chunk (t % CH) ^ sw, tile_chunk's inverse); a row past
+    // the item's end copies row 0 of its page (a key of this item).
+    const uint32_t wb = (64 * wave / CH) / kPage;  // this wave's page within a tile
+    const uint32_t dk = threadIdx.x / CH;
+    const uint32_t doff0 = ((threadIdx.x % CH) ^ (tile_chunk<CH>(dk, 0) - dk * CH)) * 16;  // bytes, in row 0
+    const uint32_t doff = doff0 + (dk % kPage) * D * 2;
+    const uint32_t lds_ring = (uint32_t)(uintptr_t)NI_LDS(&ring[0][0]) + 1024 * wave;  // this wave's 1 KB of stage 0
+    // Tile at page pg from this wave's page id `pid` (page pg + wb, or a page
+    // of the item when that one is past its end: its rows are then masked).
+    auto issue_pid = [&](auto stc, uint32_t pg, uint32_t pid) {
+        constexpr int S = decltype(stc)::value;
+        const bool inr = pg + wb < pg_end;
+        const uint64_t pb = (uint64_t)pid * page_bytes;
+        uint32_t off = doff;
+        if ((pg + PT) * kPage > it.kv_end) off = inr && pg * kPage + dk < it.kv_end ? doff : doff0;
+        lds_dma16_sbase(kbase + pb, off, lds_ring + S * SB);
+        lds_dma16_sbase(vbase + pb, off, lds_ring + S * SB + 2 * TH);
+    };
+    // The first two tiles from the ids in the item (pages pg_begin .. +3,
+    // the last repeated past the item's end).
+    // (selected, not indexed: a runtime index would put the item in memory)
+    const uint32_t fp0 = wb ? it.first_pages[1] : it.first_pages[0];
+    const uint32_t fp1 = PT == 1 ? it.first_pages[1] : (wb ? it.first_pages[3] : it.first_pages[2]);
+    if (n_tiles > 0) issue_pid(RingStage<0>{}, pg_begin, fp0);
+    if (n_tiles > 1) issue_pid(RingStage<1>{}, pg_begin + PT, fp1);
+    // q rows and 64 page ids (from the item's first page) while those land.
     float4 xq[2 * QC];
     {
         const float* qb = a.q + (int64_t)lay * a.q_layer_stride +
@@ -2510,38 +2537,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 5
     }
     uint32_t id_base = pg_begin;
     uint32_t ids = tab[min(id_base + (uint32_t)lane, pg_end - 1)];
-    // The loads land before the DMA below is issued (its waits count DMA loads only).
+    // The loads have landed before any DMA is issued after them (the loop's
+    // waits count DMA loads only); waiting here also covers the first tiles,
+    // issued before them.
 #pragma unroll
     for (int c = 0; c < 2 * QC; c++) asm volatile("" : : "v"(xq[c].x), "v"(xq[c].y), "v"(xq[c].z), "v"(xq[c].w));
     asm volatile("" : : "v"(ids));
-
-    // Tile DMA: thread t copies LDS chunk t of the tile's K and of its V (row
-    // t / CH, logical chunk (t % CH) ^ sw, tile_chunk's inverse); a row past
-    // the item's end copies row 0 of its page (a key of this item).
-    const uint32_t wb = (64 * wave / CH) / kPage;  // this wave's page within a tile
-    const uint32_t dk = threadIdx.x / CH;
-    const uint32_t doff0 = ((threadIdx.x % CH) ^ (tile_chunk<CH>(dk, 0) - dk * CH)) * 16;  // bytes, in row 0
-    const uint32_t doff = doff0 + (dk % kPage) * D * 2;
-    const uint32_t lds_ring = (uint32_t)(uintptr_t)NI_LDS(&ring[0][0]) + 1024 * wave;  // this wave's 1 KB of stage 0
     auto issue = [&](auto stc, uint32_t pg) {
-        constexpr int S = decltype(stc)::value;
         const uint32_t idx = pg + wb;
-        const bool inr = idx < pg_end;
-        const uint32_t want = inr ? idx : pg;
+        const uint32_t want = idx < pg_end ? idx : pg;
         if (want >= id_base + 64) {  // past the window of page ids (items over 64 pages)
             id_base = pg;
             ids = tab[min(id_base + (uint32_t)lane, pg_end - 1)];
             asm volatile("" : : "v"(ids));
         }
-        const uint32_t pid = __builtin_amdgcn_readlane(ids, want - id_base);
-        const uint64_t pb = (uint64_t)pid * page_bytes;
-        uint32_t off = doff;
-        if ((pg + PT) * kPage > it.kv_end) off = inr && pg * kPage + dk < it.kv_end ? doff : doff0;
-        lds_dma16_sbase(kbase + pb, off, lds_ring + S * SB);
-        lds_dma16_sbase(vbase + pb, off, lds_ring + S * SB + 2 * TH);
+        issue_pid(stc, pg, __builtin_amdgcn_readlane(ids, want - id_base));
     };
-    if (n_tiles > 0) issue(RingStage<0>{}, pg_begin);
-    if (n_tiles > 1) issue(RingStage<1>{}, pg_begin + PT);
 
     // Q^T as the B operand: query col, dims c*32 + 8*rg .. +7, f16 hi + lo
     // (lo = f16(q - hi) unscaled: the matrix cores take its subnormals

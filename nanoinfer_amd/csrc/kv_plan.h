@@ -51,12 +51,21 @@ struct AttnItem {
     uint32_t kv_begin;  // first key (multiple of 16)
     uint32_t kv_end;    // one past the last key: min(partition end, pos0 + nq)
     uint32_t part_slot; // partial-result slot, or kNoSlot (write out directly)
-    uint32_t app0;      // fused launches: first append entry of this step's new
-    uint32_t napp;      //   rows inside [kv_begin, kv_end), and their count,
-    uint32_t app_pos;   //   the position of the first of them
-    uint32_t app_src;   //   and its k/v input row (the others follow consecutively)
+    union {
+        struct {
+            uint32_t app0;     // fused launches: first append entry of this step's new
+            uint32_t napp;     //   rows inside [kv_begin, kv_end), and their count,
+            uint32_t app_pos;  //   the position of the first of them
+            uint32_t app_src;  //   and its k/v input row (the others follow consecutively)
+        };
+        // Prefill items on f16 pools (never appending): the page ids of pages
+        // kv_begin/16 .. +3 (the last page repeated past the item's end), so
+        // the first tiles' DMA needs no table read.
+        uint32_t first_pages[4];
+    };
     uint32_t pad;
 };
+static_assert(sizeof(AttnItem) == 48, "plan item layout");
 
 // A sequence of a prompt-chunk step on a Q8 pool run by one prefill
 // workgroup per (layer, head): its prefill items item0 .. item0 + n_items - 1
