@@ -225,11 +225,13 @@ int ni_kv_step(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, 
  * the launch arguments.  A step whose plan exceeds 32 KB or whose partials
  * exceed 32 MiB returns NI_ERR_BAD_ARG with the limit in the message (its
  * pages stay reserved, as after any failed launch; nothing is launched).
- * Every call on one GPU shares that array: calls of one handle are ordered
- * (see the conventions above), but calls of different handles, and graph
- * replays, that overlap on one GPU race.  ni_kv_profile does not time the
- * launches of this call (timing would take events from the handle's pool,
- * which may create them). */
+ * The first handle to call it on a GPU holds that GPU's array until
+ * ni_kv_destroy (which first waits for the handle's work); calls through
+ * any other handle on that GPU meanwhile return NI_ERR_BAD_ARG.  The
+ * holder's calls are ordered (see the conventions above), but replays of
+ * graphs captured from them that overlap on the GPU race.  ni_kv_profile
+ * does not time the launches of this call (timing would take events from
+ * the handle's pool, which may create them). */
 int ni_kv_step_noalloc(ni_kv* kv, const ni_work* work, uint32_t n_work, const float* q, const float* k,
                        const float* v, int64_t row_stride, int64_t layer_stride, float* out, int64_t out_row_stride,
                        int64_t out_layer_stride, uint32_t split_tokens, ni_stream stream);

@@ -22,6 +22,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -51,6 +52,27 @@ constexpr uint32_t kMinSplit = 64;  // smallest partition the planner uses (toke
 constexpr size_t kProfileEvents = 8192;  // events created when profiling starts
 
 thread_local std::string g_create_error;
+
+// ni_kv_step_noalloc's scratch array is one per GPU: the first handle to call
+// that entry point on a device holds it until ni_kv_destroy, and calls
+// through any other handle on that device are refused (their launches would
+// overwrite each other's partials whenever the two overlap).
+std::mutex g_scratch_mu;
+std::vector<const void*> g_scratch_holder;  // per device index
+
+bool claim_scratch(const void* kv, int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (dev < 0) return false;
+    if ((size_t)dev >= g_scratch_holder.size()) g_scratch_holder.resize((size_t)dev + 1, nullptr);
+    if (!g_scratch_holder[dev]) g_scratch_holder[dev] = kv;
+    return g_scratch_holder[dev] == kv;
+}
+
+void release_scratch(const void* kv, int dev) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (dev >= 0 && (size_t)dev < g_scratch_holder.size() && g_scratch_holder[dev] == kv)
+        g_scratch_holder[dev] = nullptr;
+}
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
@@ -1098,6 +1120,7 @@ void ni_kv_destroy(ni_kv* kv) {
         }
         if (kv->kpool) (void)hipFree(kv->kpool);
         if (kv->copy_stream) (void)hipStreamDestroy(kv->copy_stream);
+        release_scratch(kv, kv->device);
     }
     delete kv;
 }
@@ -1431,6 +1454,11 @@ int ni_kv_step_noalloc(ni_kv* kv, const ni_work* work, uint32_t n_work, const fl
     if (!kv->scratch)
         return kv->fail(NI_ERR_HIP, "ni_kv_step_noalloc: no scratch on this device (hipGetSymbolAddress: %s)",
                         hipGetErrorString(kv->scratch_err));
+    if (!claim_scratch(kv, kv->device))
+        return kv->fail(NI_ERR_BAD_ARG,
+                        "ni_kv_step_noalloc: device %d's scratch array is held by another handle (the first handle "
+                        "to call this entry point on a GPU holds it until ni_kv_destroy)",
+                        kv->device);
     struct Scope {
         ni_kv* kv;
         explicit Scope(ni_kv* k_) : kv(k_) { kv->no_alloc = true; }

@@ -9,7 +9,10 @@ bit-identical -- on two calls in a row, the second smaller (the array keeps
 the first call's contents).  The no-allocation call must not lower the
 device's free memory, and steps beyond its limits (a plan over 32 KB, split
 partials over 32 MiB) are refused with a clear error, launching nothing.
-Captured in a HIP graph, the call replays bit-identically.
+Captured in a HIP graph, the call replays bit-identically.  The array
+belongs to the first handle that calls the entry point on the GPU until that
+handle is destroyed (each test closes its caller); other handles are
+refused meanwhile.
 """
 import ctypes as C
 import sys
@@ -99,6 +102,7 @@ def test_noalloc_equals_step_on_two_calls(gpu):
         assert torch.isfinite(out_a[:, qi]).all()
         assert torch.equal(out_a[:, qi], out_b[:, qi])
         same_state(a, b, seqs)
+    b.close()  # (the GPU's scratch array goes back with its holder)
 
 
 def test_noalloc_q8_prompt_chunks_appended_by_the_prefill_launch(gpu):
@@ -144,6 +148,7 @@ def test_noalloc_q8_prompt_chunks_appended_by_the_prefill_launch(gpu):
         for x, y in zip(ga, gb):
             for xx, yy in zip(x, y):
                 assert torch.equal(xx, yy)
+    b.close()
 
 
 def test_noalloc_limits(gpu):
@@ -191,6 +196,7 @@ def test_noalloc_limits(gpu):
     assert rc == 0, lib.ni_kv_last_error(kv.handle).decode()
     torch.cuda.synchronize()
     assert torch.isfinite(out2).all()
+    kv.close()
 
 
 def test_noalloc_step_replayed_from_a_graph(gpu):
@@ -234,3 +240,40 @@ def test_noalloc_step_replayed_from_a_graph(gpu):
         same_state(a, b, seqs)  # eager gathers between the replays
         x = torch.randn((1024, 1024), device="cuda", generator=g)
         (x @ x).sum().item()  # unrelated eager work
+    del graph
+    b.close()
+
+
+def test_noalloc_scratch_held_by_one_handle(gpu):
+    """The GPU's one scratch array belongs to the first handle that calls
+    ni_kv_step_noalloc: another handle's call is refused (nothing launched,
+    its pages and lengths unchanged) until the holder is destroyed, and
+    then succeeds with the holder's results."""
+    L, H, D = 2, 4, 64
+    C_ = H * D
+    opts = na.BatchOpts(n_layer=L, n_head=H, head_dim=D, kv_blocks=64, max_seqs=4, n_ctx=512, max_rows=64)
+    a, b = na.PagedKv(opts), na.PagedKv(opts)
+    g = torch.Generator(device="cuda").manual_seed(79)
+    fill([a, b], [0, 1], [40, 200], g, C_)
+    lib = _abi.lib()
+    work = [(0, 1, 1), (1, 1, 1)]
+    q, k, v = (torch.randn((L, 2, C_), device="cuda", generator=g) for _ in range(3))
+    out_a = torch.full((L, 2, C_), float("nan"), device="cuda")
+    out_b = torch.full((L, 2, C_), float("nan"), device="cuda")
+    say("no-alloc scratch: two handles")
+    rc = call(a, lib.ni_kv_step_noalloc, work, q, k, v, out_a, 0)
+    assert rc == 0, lib.ni_kv_last_error(a.handle).decode()
+    rc = call(b, lib.ni_kv_step_noalloc, work, q, k, v, out_b, 0)
+    assert rc == _abi.NI_ERR_BAD_ARG
+    msg = lib.ni_kv_last_error(b.handle).decode()
+    assert "scratch array is held by another handle" in msg, msg
+    assert b.seq_len(0) == 40 and b.seq_len(1) == 200
+    torch.cuda.synchronize()
+    assert torch.isnan(out_b).all()
+    a.close()  # releases the array
+    rc = call(b, lib.ni_kv_step_noalloc, work, q, k, v, out_b, 0)
+    assert rc == 0, lib.ni_kv_last_error(b.handle).decode()
+    torch.cuda.synchronize()
+    assert torch.isfinite(out_b).all() and torch.equal(out_a, out_b)
+    assert b.seq_len(0) == 41 and b.seq_len(1) == 201
+    b.close()
