@@ -493,7 +493,9 @@ def run_config3(args):
                      timed_trace_steps=[ramp + args.warmup, ramp + args.warmup + args.steps - 1],
                      mean_live_seqs=round(r["mean_live"], 2), mean_context=round(r["mean_context"], 1),
                      algorithmic_bytes_per_step=int(r["bytes"] / r["steps"])),
-                "synthetic (seeded N(0,1) q/k/v resident in HBM, seeded Poisson request trace)")
+                "synthetic (seeded N(0,1) q/k/v resident in HBM, seeded Poisson request trace; one q/k/v/out "
+                "buffer serves every step, so its rows, ~2% of a step's bytes, may stay in the last-level cache "
+                "between steps, as a model's freshly projected rows would)")
     res["repetitions"] = spread
     res["host_idle_us"] = {"ni_kv_step": round(r["idle_us_plan_call"], 2)}  # per call, device idle
     res["config"]["kv_serving"] = kv_serving_summary(r, ramp + args.warmup + args.steps)
