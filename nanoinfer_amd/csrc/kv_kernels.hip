@@ -3063,6 +3063,22 @@ uint32_t device_cus() {
     return per_device[dev];
 }
 
+// Workgroups of `threads` threads of kernel f that one CU of the current
+// device holds at once, looked up once per (device, kernel); 0 if unknown.
+static uint32_t blocks_per_cu(const void* f, int threads) {
+    static std::mutex mu;
+    static std::vector<std::pair<std::pair<int, const void*>, uint32_t>> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (const auto& c : cache)
+        if (c.first.first == dev && c.first.second == f) return c.second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess || n < 0) n = 0;
+    cache.push_back({{dev, f}, (uint32_t)n});
+    return (uint32_t)n;
+}
+
 uint32_t wide_blocks_per_cu(uint32_t head_dim, bool q8, uint32_t nq_tile, bool fused) {
     if (head_dim != 64) return 0;
     // the kernel attn_dispatch picks for a wide launch with these parameters
@@ -3086,17 +3102,14 @@ uint32_t wide_blocks_per_cu(uint32_t head_dim, bool q8, uint32_t nq_tile, bool f
     } else {
         return 0;
     }
-    static std::mutex mu;
-    static std::vector<std::pair<std::pair<int, const void*>, uint32_t>> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    std::lock_guard<std::mutex> lock(mu);
-    for (const auto& c : cache)
-        if (c.first.first == dev && c.first.second == f) return c.second;
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess || n < 0) n = 0;
-    cache.push_back({{dev, f}, (uint32_t)n});
-    return (uint32_t)n;
+    return blocks_per_cu(f, threads);
+}
+
+uint32_t prefill_blocks_per_cu(uint32_t head_dim) {
+    constexpr int INL = (int)kInlinePlanSmall;
+    if (head_dim == 64) return blocks_per_cu((const void*)attn_prefill_kernel<64, kPrefillPages, INL>, 256);
+    if (head_dim == 128) return blocks_per_cu((const void*)attn_prefill_kernel<128, 1, INL>, 256);
+    return 0;
 }
 
 template <int WF>

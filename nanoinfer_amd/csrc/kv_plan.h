@@ -298,6 +298,8 @@ uint32_t device_cus();
 // own resource use (hipOccupancyMaxActiveBlocksPerMultiprocessor); 0 if
 // unknown.
 uint32_t wide_blocks_per_cu(uint32_t head_dim, bool q8, uint32_t nq_tile, bool fused);
+// The same for the f16 prefill launch (attn_prefill_kernel) at this head_dim.
+uint32_t prefill_blocks_per_cu(uint32_t head_dim);
 bool attention_supported(uint32_t head_dim);
 
 }  // namespace ni
