@@ -569,22 +569,26 @@ def run_config3(args):
 # launch form, every prompt row queried).  "step": one ni_kv_step per step
 # (all layers per launch); "layers": ni_kv_step_begin, one ni_kv_step_layer
 # per layer (the form a model's forward runs, batch.rs:390-416), ni_kv_step_end.
+# Lines without a ramp warm up for ~100 ms of their own steps: from idle the
+# GPU's first ~50 ms of work run slower (16 x 512 prefill launches 290 ->
+# 230 us over the first ~100 launches; config 2 and the prefill kernel measured
+# 2.5% and 3% slower after 20 and 10 warmup steps than after 2000 and 200).
 SECONDARY_LINES = {
-    "config2": ("config2", 200, 20, "attn_split_kernel (fused append)", "step", False),
-    "config4": ("config4", 100, 10, "attn_split_kernel + attn_merge_kernel", "step", False),
-    "config5": ("config5", 200, 20, "kv_append_kernel + attn_mfma_kernel", "step", False),
+    "config2": ("config2", 200, 2000, "attn_split_kernel (fused append)", "step", False),
+    "config4": ("config4", 100, 300, "attn_split_kernel + attn_merge_kernel", "step", False),
+    "config5": ("config5", 200, 800, "kv_append_kernel + attn_mfma_kernel", "step", False),
     "config3q8": ("config3q8", 200, 20, "kv_append_kernel + attn_q8_kernel, Q8 cache", "step", False),
-    "prefill": ("prefill", 100, 10, "attn_prefill_kernel (after its append launch)", "step", False),
-    "qkv64": ("qkv64", 200, 20, "qkv_mid_kernel (append in the epilogue)", "step", False),
+    "prefill": ("prefill", 100, 250, "attn_prefill_kernel (after its append launch)", "step", False),
+    "qkv64": ("qkv64", 200, 1000, "qkv_mid_kernel (append in the epilogue)", "step", False),
     # every prompt row queried (the reference's attention covers every row of a
     # step, batch.rs:577-600): decode rows fused, prompt chunks appended by the
     # same launch's extra blocks, then their prefill launch
     "config3_all_prompt_rows": ("config3", 200, 20, "attn_split_kernel (fused) + attn_prefill_kernel", "step", True),
     "config3_per_layer_q8": ("config3q8", 200, 20, "attn_q8_kernel (wide, fused), per layer", "layers", False),
-    "config5_per_layer": ("config5", 200, 20, "attn_mfma_kernel (wide, fused), per layer", "layers", False),
-    "config5_per_layer_q8": ("config5q8", 200, 20, "attn_mfma_kernel (wide, fused), per layer, Q8 cache", "layers",
+    "config5_per_layer": ("config5", 200, 500, "attn_mfma_kernel (wide, fused), per layer", "layers", False),
+    "config5_per_layer_q8": ("config5q8", 200, 600, "attn_mfma_kernel (wide, fused), per layer, Q8 cache", "layers",
                              False),
-    "prefill_per_layer": ("prefill", 50, 5, "kv_append_kernel + attn_prefill_kernel, per layer", "layers", False),
+    "prefill_per_layer": ("prefill", 50, 200, "kv_append_kernel + attn_prefill_kernel, per layer", "layers", False),
 }
 
 
