@@ -1497,16 +1497,24 @@ __global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma
     constexpr int LPP = kPage / KPL;
     constexpr int CH = D / 8;       // 16-byte chunks per V row
     constexpr int NQ = 16;
-    __shared__ float red[W][NQ][D + 2];
     // Per-wave V tile, row major with tile_chunk's chunk swizzle: rows go in
     // with 16-byte writes, V^T comes out through transposing reads.
-    __shared__ __attribute__((aligned(16))) _Float16 vt[W][PB * kPage * D];
     // f16: K rows load coalesced (as V) and reach the A operand through a
     // per-wave tile of the same layout (config 5 5684 -> 5852 GB/s against
     // each lane loading its operand chunk directly; Q8 keeps its direct
-    // 8-byte loads: an int8 tile measured 12% slower).
+    // 8-byte loads: an int8 tile measured 12% slower).  The waves' merge
+    // buffer `red`, used after the loop, shares the tiles' LDS: 16.9 KB per
+    // 4-wave workgroup instead of 33, and with one PV accumulator (92 VGPRs)
+    // 5 waves per SIMD (config 5 6053-6057 -> 6069-6077 GB/s, on the Q8
+    // cache 5361-5372 -> 5432-5478).
     constexpr bool KT = !Q8;
-    __shared__ __attribute__((aligned(16))) _Float16 kt[KT ? W : 1][KT ? PB * kPage * D : 8];
+    constexpr size_t kTileBytes = (size_t)W * PB * kPage * D * 2;
+    constexpr size_t kRedBytes = (size_t)W * NQ * (D + 2) * 4;
+    constexpr size_t kLds = (KT ? 2 : 1) * kTileBytes > kRedBytes ? (KT ? 2 : 1) * kTileBytes : kRedBytes;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+    auto& vt = *reinterpret_cast<_Float16(*)[W][PB * kPage * D]>(lds);
+    auto& kt = *reinterpret_cast<_Float16(*)[KT ? W : 1][KT ? PB * kPage * D : 8]>(lds + (KT ? kTileBytes : 0));
+    auto& red = *reinterpret_cast<float(*)[W][NQ][D + 2]>(lds);
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1633,9 +1641,9 @@ __global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma
         }
     }
     float m = kMinScore, lsum = 0.f;
-    float4_t o[VC], ol[VC];  // PV products of p's hi and lo parts
+    float4_t o[VC];  // PV products of p's hi and lo parts, into one accumulator
 #pragma unroll
-    for (int c = 0; c < VC; c++) o[c] = ol[c] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < VC; c++) o[c] = float4_t{0.f, 0.f, 0.f, 0.f};
     // Q8: p enters PV as p * vs / vref (at most 2^14 after scaling, so its
     // f16 hi never overflows) and the accumulators hold the sum in units of
     // vref: vref starts at 1 (scales up to 1, values up to 127 in magnitude,
@@ -1770,10 +1778,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma
         // multiplies change nothing.
         if (__any(oalpha != 1.f)) {
 #pragma unroll
-            for (int c = 0; c < VC; c++) {
-                o[c] *= oalpha;
-                ol[c] *= oalpha;
-            }
+            for (int c = 0; c < VC; c++) o[c] *= oalpha;
         }
         // O^T += V^T P^T, 16 dims per product; V^T (dim c*16 + col of keys
         // 4*rg .. 4*rg+3) by a transposing read of the row-major tile, as in
@@ -1794,7 +1799,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma
                 for (int c = 0; c < VC; c++) {
                     const half8_t v8 = __builtin_shufflevector(vread(b, c), vread(b + 1, c), 0, 1, 2, 3, 4, 5, 6, 7);
                     o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8h, o[c], 0, 0, 0);
-                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, ol[c], 0, 0, 0);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(v8, p8l, o[c], 0, 0, 0);
                 }
             }
         } else {
@@ -1804,7 +1809,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma
                 for (int b = 0; b < PB; b++) {
                     const half4_t vt4 = vread(b, c);
                     o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, ph[b], o[c], 0, 0, 0);
-                    ol[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl[b], ol[c], 0, 0, 0);
+                    o[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt4, pl[b], o[c], 0, 0, 0);
                 }
             }
         }
@@ -1815,6 +1820,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma
     }
     // Lanes q, q+16, q+32, q+48 hold partial sums of query q's softmax.
     lsum = rows4_sum(lsum);
+    __syncthreads();  // every wave is done with its tiles, which `red` overwrites
     if (qok) {
         if (rg == 0) {
             red[wave][col][0] = m;
@@ -1824,7 +1830,7 @@ __global__ __launch_bounds__(64 * W, D == 64 ? kMfmaMinWaves : 1) void attn_mfma
         for (int c = 0; c < VC; c++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                red[wave][col][2 + c * 16 + 4 * rg + j] = (o[c][j] + ol[c][j]) * (kPUnscale * vref);
+                red[wave][col][2 + c * 16 + 4 * rg + j] = o[c][j] * (kPUnscale * vref);
     }
     __syncthreads();
     for (uint32_t t = threadIdx.x; t < it.nq * D; t += 64 * W) {
