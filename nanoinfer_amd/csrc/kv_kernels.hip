@@ -2217,8 +2217,10 @@ __global__ __launch_bounds__(256) void attn_prefill_q8_kernel(const AttnLaunch a
     // values are exact in f16.
     half8_t qh[QC], ql[QC];
     {
+        // (a lane without a query reads the item's first row: rows past nq
+        // may lie past the end of the caller's q)
         const float* qb = a.q + (int64_t)lay * a.q_layer_stride +
-                          (int64_t)(it.row0 + r0 + (qok ? col : 0)) * a.q_row_stride + head * D + 8 * rg;
+                          (int64_t)(it.row0 + (qok ? r0 + col : 0)) * a.q_row_stride + head * D + 8 * rg;
 #pragma unroll
         for (int c = 0; c < QC; c++) {
             float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -2533,8 +2535,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 6
     // q rows and 64 page ids (from the item's first page) while those land.
     float4 xq[2 * QC];
     {
+        // (a lane without a query reads the item's first row: rows past nq
+        // may lie past the end of the caller's q)
         const float* qb = a.q + (int64_t)lay * a.q_layer_stride +
-                          (int64_t)(it.row0 + r0 + (qok ? col : 0)) * a.q_row_stride + head * D + 8 * rg;
+                          (int64_t)(it.row0 + (qok ? r0 + col : 0)) * a.q_row_stride + head * D + 8 * rg;
 #pragma unroll
         for (int c = 0; c < QC; c++) {
             xq[2 * c] = reinterpret_cast<const float4*>(qb + c * 32)[0];
