@@ -97,6 +97,7 @@ struct Plan {
     std::vector<uint32_t> table;
     std::vector<PrefillSeq> pseqs;  // prompt-chunk step: the prefill launch appends, a workgroup per sequence
     std::vector<uint16_t> order;    // balanced wide launch: the (item, layer, head) unit of each workgroup
+    std::vector<uint16_t> porder;   // balanced one-round prefill launch: the same, over pitems
     uint32_t n_slots = 0;
     uint32_t n_pslots = 0;
     uint32_t nq_tile = 1;
@@ -114,6 +115,7 @@ struct Plan {
         orphans.clear();
         pseqs.clear();
         order.clear();
+        porder.clear();
         seq_prefill = false;
         items.clear();
         merges.clear();
@@ -132,7 +134,7 @@ struct Plan {
 
 // Byte offsets of each part of a serialised plan.
 struct Offsets {
-    size_t app, orphans, items, merges, pitems, pmerges, pseqs, table, order, total;
+    size_t app, orphans, items, merges, pitems, pmerges, pseqs, table, order, porder, total;
 };
 
 // Where the kernels find a plan: in the launch arguments (small plans) or in
@@ -342,6 +344,31 @@ int layer_range(ni_kv* kv, int32_t layer, uint32_t* layer0, uint32_t* n_lay) {
 // the largest item of every round.  Instead the (item, layer, head) units go
 // to CUs longest first, each to the least loaded CU with a free slot, and
 // P.order records the unit each block runs.
+// Longest first, round by round: round r gives block c + r * C to every CU
+// c that takes one (all but the last round: every CU; the last: CUs below
+// rem), the largest units of the round to the least loaded CUs.  `cost`:
+// (cost, item) sorted by cost, largest first; order[b] = the unit (item *
+// lh + layer * heads + head) block b runs.
+void deal_units(const std::vector<std::pair<uint64_t, uint32_t>>& cost, uint64_t lh, uint64_t C, uint64_t R,
+                uint64_t rem, std::vector<uint16_t>& order) {
+    std::vector<uint64_t> load(C, 0);
+    std::vector<uint32_t> cus(C);
+    order.assign((R - 1) * C + rem, 0);
+    uint64_t u = 0;  // position in the cost order, (item, unit of the item)
+    for (uint64_t r = 0; r < R; r++) {
+        const uint32_t n_r = (uint32_t)(r + 1 < R ? C : rem);
+        for (uint32_t c = 0; c < n_r; c++) cus[c] = c;
+        if (r > 0)
+            std::stable_sort(cus.begin(), cus.begin() + n_r, [&](uint32_t x, uint32_t y) { return load[x] < load[y]; });
+        for (uint32_t k = 0; k < n_r; k++, u++) {
+            const auto& ci = cost[u / lh];
+            const uint32_t c = cus[k];
+            order[c + C * r] = (uint16_t)(ci.second * lh + u % lh);
+            load[c] += ci.first;
+        }
+    }
+}
+
 void balance_units(ni_kv* kv, Plan& P, uint32_t n_lay) {
     P.order.clear();
     if (!P.wide || P.items.empty() || kv->host_only) return;
@@ -366,25 +393,34 @@ void balance_units(ni_kv* kv, Plan& P, uint32_t n_lay) {
                      [](const std::pair<uint64_t, uint32_t>& x, const std::pair<uint64_t, uint32_t>& y) {
                          return x.first > y.first;
                      });
-    // Longest first, round by round: round r gives block c + r * C to every
-    // CU c that takes one (all but the last round: every CU; the last: CUs
-    // below rem), the largest units of the round to the least loaded CUs.
-    std::vector<uint64_t> load(C, 0);
-    std::vector<uint32_t> cus(C);
-    P.order.assign(n_units, 0);
-    uint64_t u = 0;  // position in the cost order, (item, unit of the item)
-    for (uint64_t r = 0; r < R; r++) {
-        const uint32_t n_r = (uint32_t)(r + 1 < R ? C : rem);
-        for (uint32_t c = 0; c < n_r; c++) cus[c] = c;
-        if (r > 0)
-            std::stable_sort(cus.begin(), cus.begin() + n_r, [&](uint32_t x, uint32_t y) { return load[x] < load[y]; });
-        for (uint32_t k = 0; k < n_r; k++, u++) {
-            const auto& ci = cost[u / lh];
-            const uint32_t c = cus[k];
-            P.order[c + C * r] = (uint16_t)(ci.second * lh + u % lh);
-            load[c] += ci.first;
-        }
+    deal_units(cost, lh, C, R, rem, P.order);
+}
+
+// A one-layer-per-launch prefill step on an f16 pool whose (item, layer,
+// head) units all fit on the GPU at once (at most prefill_blocks_per_cu x
+// CUs): block b runs on CU b % C as in the wide launches above, so the units
+// are dealt to CUs the same way (cost: the item's 32-key tiles) and P.porder
+// records the unit each block runs.  16 x 512-row prompts, one layer per
+// launch (1536 units, 6 per CU): in plan order the most loaded CU held 1.26x
+// the mean work, dealt 1.00x; 470.0-471.7 against 485.5-488.4 us per step
+// (`ni_drive prefill --step-layers`).
+void balance_prefill_units(Plan& P, uint32_t n_lay, uint32_t n_head, uint64_t C, uint64_t S) {
+    P.porder.clear();
+    const uint64_t lh = (uint64_t)n_lay * n_head;
+    const uint64_t n_units = (uint64_t)P.pitems.size() * lh;
+    if (S == 0 || n_units <= C || n_units > C * S || n_units > 65536) return;
+    const uint64_t R = (n_units + C - 1) / C;
+    const uint64_t rem = n_units - (R - 1) * C;
+    std::vector<std::pair<uint64_t, uint32_t>> cost(P.pitems.size());
+    for (uint32_t i = 0; i < P.pitems.size(); i++) {
+        const AttnItem& it = P.pitems[i];
+        cost[i] = {(it.kv_end - it.kv_begin + 31) / 32, i};
     }
+    std::stable_sort(cost.begin(), cost.end(),
+                     [](const std::pair<uint64_t, uint32_t>& x, const std::pair<uint64_t, uint32_t>& y) {
+                         return x.first > y.first;
+                     });
+    deal_units(cost, lh, C, R, rem, P.porder);
 }
 
 // Attention part of a plan: group consecutive query rows of one sequence at
@@ -618,16 +654,21 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
             const uint32_t pb = it.kv_begin / kPage, pe = (it.kv_end + kPage - 1) / kPage;
             for (uint32_t i = 0; i < 4; i++) it.first_pages[i] = pe > pb ? P.table[it.tab + std::min(pb + i, pe - 1)] : 0u;
         }
-        // A launch of at most two rounds of the GPU's resident workgroups
-        // ends on the groups that start last: there the groups of at most
-        // a quarter of the longest group's keys go last, longest first (each
-        // sequence's other groups keep the order above; the short ones
-        // re-read only its first keys).  One layer per launch, 16 x 512 rows
+        // A launch whose workgroups are all resident at once has its units
+        // dealt to the CUs (balance_prefill_units).  A launch of at most two
+        // rounds of the GPU's resident workgroups ends on the groups that
+        // start last: there the groups of at most a quarter of the longest
+        // group's keys go last, longest first (each sequence's other groups
+        // keep the order above; the short ones re-read only its first keys).
+        // One layer per launch, 16 x 512 rows, when 5 workgroups fit a CU
         // (1.2 rounds): 30.0 -> 26.9 us; all 12 layers (14 rounds) do not
         // take it (~0.8% slower reordered).
         const uint64_t units = (uint64_t)P.pitems.size() * n_lay * kv->o.n_head;
-        const uint64_t resident = (uint64_t)prefill_blocks_per_cu(kv->o.head_dim) * device_cus();
-        if (units <= 2 * resident) {
+        const uint64_t per_cu = prefill_blocks_per_cu(kv->o.head_dim), C = device_cus();
+        const uint64_t resident = per_cu * C;
+        if (units <= resident) {
+            balance_prefill_units(P, n_lay, kv->o.n_head, C, per_cu);
+        } else if (units <= 2 * resident) {
             uint32_t longest_all = 0;
             for (const AttnItem& it : P.pitems) longest_all = std::max(longest_all, it.kv_end - it.kv_begin);
             const uint32_t short_keys = longest_all / 4;
@@ -777,7 +818,8 @@ Offsets layout(const Plan& P) {
     o.pseqs = align_up(o.pmerges + P.pmerges.size() * sizeof(MergeItem), kAlign);
     o.table = align_up(o.pseqs + P.pseqs.size() * sizeof(PrefillSeq), kAlign);
     o.order = align_up(o.table + P.table.size() * sizeof(uint32_t), kAlign);
-    o.total = align_up(o.order + P.order.size() * sizeof(uint16_t), kAlign);
+    o.porder = align_up(o.order + P.order.size() * sizeof(uint16_t), kAlign);
+    o.total = align_up(o.porder + P.porder.size() * sizeof(uint16_t), kAlign);
     return o;
 }
 
@@ -829,6 +871,8 @@ int place_plan(ni_kv* kv, const Plan& P, std::vector<uint8_t>& blob, hipStream_t
     if (!P.pseqs.empty()) memcpy(blob.data() + off->pseqs, P.pseqs.data(), P.pseqs.size() * sizeof(PrefillSeq));
     if (!P.table.empty()) memcpy(blob.data() + off->table, P.table.data(), P.table.size() * sizeof(uint32_t));
     if (!P.order.empty()) memcpy(blob.data() + off->order, P.order.data(), P.order.size() * sizeof(uint16_t));
+    if (!P.porder.empty())
+        memcpy(blob.data() + off->porder, P.porder.data(), P.porder.size() * sizeof(uint16_t));
     *ref = PlanRef{};
     if (kv->no_alloc) {
         // No staging slot (it would be allocated): the plan travels inline.
@@ -966,6 +1010,8 @@ int run_placed(ni_kv* kv, const Plan& P, const Offsets& off, const PlanRef& ref,
         a.layer0 = layer0;
         a.n_lay = n_lay;
         a.nq_tile = kPrefillRows;
+        a.off_order = (uint32_t)off.porder;
+        a.ordered = P.porder.empty() ? 0u : 1u;
         a.qscale = (float)(1.4426950408889634 / std::sqrt((double)D));
         if (P.seq_prefill) {  // the launch appends the rows too
             a.k = k;

@@ -2457,7 +2457,8 @@ __global__ __launch_bounds__(256) void attn_prefill_q8_kernel(const AttnLaunch a
 //    took 90 at 5 waves: 418-420 against 412-413 us per 16 x 512 step).
 // The prologue issues the first tiles' DMA from the page ids the item
 // carries, the item's q rows and 64 page ids beside it, then splits q while
-// the tiles land.  One workgroup per (head, layer, item): blockIdx.x, .y, .z.
+// the tiles land.  One workgroup per (head, layer, item): blockIdx.x, .y, .z,
+// or (a.ordered) a 1-D grid whose block b runs unit order[b] of the plan.
 template <int ST>
 struct RingStage {
     static constexpr int value = ST;
@@ -2481,9 +2482,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 6
 
     const int lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t head = blockIdx.x, lay = blockIdx.y;
     const uint8_t* plan = plan_base(pa, a.plan);
-    const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[blockIdx.z];
+    uint32_t head = blockIdx.x, lay = blockIdx.y, item = blockIdx.z;
+    if (a.ordered) {  // a 1-D grid: block b runs unit order[b], dealt to the CUs by the host
+        const AttnUnit un = attn_unit(a, plan, blockIdx.x);
+        item = un.item;
+        lay = un.lay;
+        head = un.head;
+    }
+    const AttnItem it = reinterpret_cast<const AttnItem*>(plan + a.off_items)[item];
     const int col = lane & 15;  // query slot of S^T / O^T columns
     const int rg = lane >> 4;   // row group: keys (or dims) 4*rg .. 4*rg+3
 
@@ -2748,7 +2755,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 64 ? 6
     } else {
         // (m, l, o) with l and o in units of exp2(s - m), m = mref + 2^7's
         // exponent; a row with no key of the partition weighs nothing.
-        float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * gridDim.x + head) * kPrefillRows + r0 + col) * (D + 2);
+        float* p = a.partials + ((((uint64_t)it.part_slot * a.n_lay + lay) * a.pool.n_head + head) * kPrefillRows + r0 + col) * (D + 2);
         if (rg == 0) {
             p[0] = lsum > 0.f ? mref + kLog2PScalePre : kMinScore;
             p[1] = lsum * kPUnscalePre;
@@ -2950,6 +2957,12 @@ hipError_t prefill_launch_t(const AttnLaunch& a, const void* ip, uint32_t ib, hi
         }
         if (a.pool.q8) return hipErrorInvalidValue;
         if (seq) return hipErrorInvalidValue;  // the host plans sequences on Q8 pools only
+        if (a.ordered) {  // one block per unit of the host's order (uint16_t indices)
+            if (blocks > 65536) return hipErrorInvalidValue;
+            hipExtLaunchKernelGGL(attn_prefill_kernel<D, PT, INL>, dim3((uint32_t)blocks), dim3(256), 0, s, t.start,
+                                  t.stop, 0, a, pa);
+            return hipGetLastError();
+        }
         if (a.n_items > 65535 || a.n_lay > 65535) return hipErrorInvalidValue;  // grid y and z
         hipExtLaunchKernelGGL(attn_prefill_kernel<D, PT, INL>, dim3(a.pool.n_head, a.n_lay, a.n_items), dim3(256),
                               0, s, t.start, t.stop, 0, a, pa);
