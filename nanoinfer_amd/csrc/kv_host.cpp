@@ -667,7 +667,9 @@ int plan_attention(ni_kv* kv, uint32_t split_tokens, uint32_t n_lay) {
         const uint64_t per_cu = prefill_blocks_per_cu(kv->o.head_dim), C = device_cus();
         const uint64_t resident = per_cu * C;
         if (units <= resident) {
-            balance_prefill_units(P, n_lay, kv->o.n_head, C, per_cu);
+            // (not in ni_kv_step_noalloc, whose plans travel inline: the order
+            // array would lower the size of step it takes)
+            if (!kv->no_alloc) balance_prefill_units(P, n_lay, kv->o.n_head, C, per_cu);
         } else if (units <= 2 * resident) {
             uint32_t longest_all = 0;
             for (const AttnItem& it : P.pitems) longest_all = std::max(longest_all, it.kv_end - it.kv_begin);
